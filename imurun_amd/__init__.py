@@ -1,0 +1,251 @@
+"""MI355X (gfx950) quantized-matmul path of FISH, driven from Python.
+
+The product is libfish_hip.so (C ABI in include/fish_hip.h); this module
+binds it with ctypes the way IMURUN's model/fish_native.py binds libfish.so,
+and adds thin helpers that pass torch device tensors as raw pointers. There
+is no fallback: if the library or a gfx950 device is missing, calls raise.
+
+Operator names follow FISH (model/fish/include/fish/ops.h, quant.h):
+  quantize(x)                     ActBatch::quantize  (ops.cpp:158-175)
+  repack(type, gguf, n_in, n_out) ComputeBackend::upload's device copy (backend.h:41-42)
+  matmul(type, w, act, ...)       matmul_batch's int8 path (ops.cpp:177-216)
+  matmul_batch(type, w, x, n_out) the convenience overload (ops.cpp:254-264)
+  HipBackend                      ComputeBackend over host buffers (backend.h:26-163)
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libfish_hip.so")
+
+Q4_0, Q8_0, Q4_K, Q6_K = 2, 8, 12, 14
+TYPE_NAMES = {Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q6_K: "Q6_K"}
+BLOCK_ELEMS = {Q4_0: 32, Q8_0: 32, Q4_K: 256, Q6_K: 256}
+BLOCK_BYTES = {Q4_0: 18, Q8_0: 34, Q4_K: 144, Q6_K: 210}
+
+_P = ctypes.c_void_p
+_lib = None
+
+
+class FishHipError(RuntimeError):
+    pass
+
+
+def gguf_row_bytes(t: int, n_in: int) -> int:
+    return (n_in // BLOCK_ELEMS[t]) * BLOCK_BYTES[t]
+
+
+def load() -> ctypes.CDLL:
+    """The loaded libfish_hip.so with argument types set (raises if absent)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise FishHipError(f"{LIB_PATH} is missing: run __graft_entry__.build() (hipcc --offload-arch=gfx950)")
+    L = ctypes.CDLL(LIB_PATH)
+    sig = {
+        "fish_hip_abi_version": ([], ctypes.c_int),
+        "fish_hip_kernel_name": ([], ctypes.c_char_p),
+        "fish_hip_last_error": ([], ctypes.c_char_p),
+        "fish_hip_weight_bytes": ([ctypes.c_uint32, ctypes.c_int, ctypes.c_int], ctypes.c_uint64),
+        "fish_hip_act_bytes": ([ctypes.c_int, ctypes.c_int], ctypes.c_uint64),
+        "fish_hip_quantize": ([_P, ctypes.c_int, ctypes.c_int, _P, _P, _P, _P], ctypes.c_int),
+        "fish_hip_repack": ([ctypes.c_uint32, _P, ctypes.c_int, ctypes.c_int, _P, _P], ctypes.c_int),
+        "fish_hip_matmul": ([ctypes.c_uint32, _P, _P, ctypes.c_int, ctypes.c_int, ctypes.c_int, _P, _P], ctypes.c_int),
+        "fish_hip_block_ints": ([ctypes.c_uint32, _P, _P, ctypes.c_int, ctypes.c_int, _P, _P], ctypes.c_int),
+        "fish_hip_quantize_rows": ([ctypes.c_uint32, _P, _P, ctypes.c_int, ctypes.c_int, ctypes.c_int], ctypes.c_int),
+        "fish_hip_backend_available": ([], ctypes.c_int),
+        "fish_hip_device_name": ([], ctypes.c_char_p),
+        "fish_hip_memory_total": ([], ctypes.c_uint64),
+        "fish_hip_memory_free": ([], ctypes.c_uint64),
+        "fish_hip_supports": ([ctypes.c_uint32], ctypes.c_int),
+        "fish_hip_upload": ([_P, ctypes.c_uint32, _P, ctypes.c_int, ctypes.c_int, ctypes.c_int], ctypes.c_int),
+        "fish_hip_resident": ([_P], ctypes.c_int),
+        "fish_hip_release": ([_P], None),
+        "fish_hip_bytes_resident": ([], ctypes.c_uint64),
+        "fish_hip_backend_matmul": ([_P, _P, ctypes.c_int, ctypes.c_int, ctypes.c_int, _P], ctypes.c_int),
+        "fish_hip_backend_matmul_group": ([_P, ctypes.c_int, _P, ctypes.c_int, ctypes.c_int, _P, _P], ctypes.c_int),
+    }
+    for name, (args, res) in sig.items():
+        fn = getattr(L, name)
+        fn.argtypes = args
+        fn.restype = res
+    _lib = L
+    return L
+
+
+def last_error() -> str:
+    return (load().fish_hip_last_error() or b"").decode()
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != 0:
+        raise FishHipError(f"{what} failed ({rc}): {last_error()}")
+
+
+def _stream(stream) -> int | None:
+    if stream is None:
+        import torch
+        return torch.cuda.current_stream().cuda_stream or None
+    return stream
+
+
+def _ptr(t) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+# ------------------------------------------------------------------ block writer (host)
+
+def quantize_rows(t: int, w: np.ndarray, n_threads: int | None = None) -> np.ndarray:
+    """FISH's quantize_row over the rows of w (f32 [n_rows, n_in]) -> GGUF bytes."""
+    w = np.ascontiguousarray(w, np.float32)
+    n_rows, n_in = w.shape
+    out = np.empty(gguf_row_bytes(t, n_in) * n_rows, np.uint8)
+    threads = n_threads or min(16, os.cpu_count() or 1)
+    _check(load().fish_hip_quantize_rows(t, w.ctypes.data, out.ctypes.data, n_rows, n_in, threads), "quantize_rows")
+    return out
+
+
+# ------------------------------------------------------------------ device operators (torch tensors)
+
+def weight_bytes(t: int, n_in: int, n_out: int) -> int:
+    return int(load().fish_hip_weight_bytes(t, n_in, n_out))
+
+
+def act_bytes(n_tok: int, n_in: int) -> int:
+    return int(load().fish_hip_act_bytes(n_tok, n_in))
+
+
+def quantize(x, act=None, fish_layouts: bool = False, stream=None):
+    """ActBatch::quantize on the device. x: f32 cuda [n_tok, n_in].
+    Returns act (uint8 cuda) or (act, q32 bytes, q256 bytes) with FISH's layouts."""
+    import torch
+    assert x.is_cuda and x.dtype == torch.float32 and x.dim() == 2 and x.is_contiguous()
+    n_tok, n_in = x.shape
+    if act is None:
+        act = torch.empty(act_bytes(n_tok, n_in), dtype=torch.uint8, device=x.device)
+    q32 = q256 = None
+    if fish_layouts:
+        q32 = torch.empty(n_tok * (n_in // 32) * 40, dtype=torch.uint8, device=x.device)
+        if n_in % 256 == 0:
+            q256 = torch.empty(n_tok * (n_in // 256) * 276, dtype=torch.uint8, device=x.device)
+    _check(load().fish_hip_quantize(x.data_ptr(), n_tok, n_in, act.data_ptr(), _ptr(q32), _ptr(q256),
+                                    _stream(stream)), "quantize")
+    return (act, q32, q256) if fish_layouts else act
+
+
+def repack(t: int, gguf, n_in: int, n_out: int, stream=None):
+    """GGUF rows (uint8 cuda tensor) -> repacked device tensor."""
+    import torch
+    assert gguf.is_cuda and gguf.dtype == torch.uint8
+    if gguf.numel() < gguf_row_bytes(t, n_in) * n_out:
+        raise FishHipError("repack: source smaller than n_out GGUF rows")
+    nb = weight_bytes(t, n_in, n_out)
+    if nb == 0:
+        raise FishHipError(f"repack: type {t} with n_in={n_in} unsupported")
+    w = torch.empty(nb, dtype=torch.uint8, device=gguf.device)
+    _check(load().fish_hip_repack(t, gguf.data_ptr(), n_in, n_out, w.data_ptr(), _stream(stream)), "repack")
+    return w
+
+
+def matmul(t: int, w, act, n_tok: int, n_in: int, n_out: int, y=None, stream=None):
+    """y[n_tok, n_out] = W . x on a repacked tensor and a quantized activation buffer."""
+    import torch
+    if w.numel() < weight_bytes(t, n_in, n_out) or act.numel() < act_bytes(n_tok, n_in):
+        raise FishHipError("matmul: buffer smaller than its layout")
+    if y is None:
+        y = torch.empty((n_tok, n_out), dtype=torch.float32, device=w.device)
+    assert y.numel() >= n_tok * n_out and y.is_contiguous()
+    _check(load().fish_hip_matmul(t, w.data_ptr(), act.data_ptr(), n_tok, n_in, n_out, y.data_ptr(),
+                                  _stream(stream)), "matmul")
+    return y
+
+
+def matmul_batch(t: int, w, x, n_out: int, stream=None):
+    """Quantize x then multiply (the convenience matmul_batch, ops.cpp:254-264)."""
+    act = quantize(x, stream=stream)
+    return matmul(t, w, act, x.shape[0], x.shape[1], n_out, stream=stream)
+
+
+def block_ints(t: int, w, act, n_in: int, n_out: int, stream=None):
+    """Per-block integer dots of every row with token 0 (int32 cuda tensor)."""
+    import torch
+    per_row = (2 * (n_in // 256)) if t == Q4_K else ((n_in // 256) if t == Q6_K else n_in // 32)
+    out = torch.empty(n_out * per_row, dtype=torch.int32, device=w.device)
+    _check(load().fish_hip_block_ints(t, w.data_ptr(), act.data_ptr(), n_in, n_out, out.data_ptr(),
+                                      _stream(stream)), "block_ints")
+    return out
+
+
+# ------------------------------------------------------------------ backend (host buffers)
+
+class HipBackend:
+    """ComputeBackend over host numpy buffers (backend.h:26-163)."""
+
+    def __init__(self):
+        self.L = load()
+        self._keys: dict[str, ctypes.c_void_p] = {}
+        self._anchors = []
+
+    def available(self) -> bool:
+        return bool(self.L.fish_hip_backend_available())
+
+    def name(self) -> str:
+        return "hip"
+
+    def device_name(self) -> str:
+        return (self.L.fish_hip_device_name() or b"").decode()
+
+    def memory_total(self) -> int:
+        return int(self.L.fish_hip_memory_total())
+
+    def memory_free(self) -> int:
+        return int(self.L.fish_hip_memory_free())
+
+    def supports(self, t: int) -> bool:
+        return bool(self.L.fish_hip_supports(t))
+
+    def _key(self, name: str) -> ctypes.c_void_p:
+        if name not in self._keys:
+            buf = ctypes.create_string_buffer(1)
+            self._anchors.append(buf)
+            self._keys[name] = ctypes.cast(buf, ctypes.c_void_p)
+        return self._keys[name]
+
+    def upload(self, name: str, t: int, data: np.ndarray, n_in: int, n_out: int, n_expert: int = 1) -> bool:
+        data = np.ascontiguousarray(data, dtype=np.uint8)
+        if data.size < gguf_row_bytes(t, n_in) * n_out * n_expert:
+            return False
+        return bool(self.L.fish_hip_upload(self._key(name), t, data.ctypes.data, n_in, n_out, n_expert))
+
+    def resident(self, name: str) -> bool:
+        return name in self._keys and bool(self.L.fish_hip_resident(self._keys[name]))
+
+    def release(self, name: str) -> None:
+        if name in self._keys:
+            self.L.fish_hip_release(self._keys[name])
+
+    def bytes_resident(self) -> int:
+        return int(self.L.fish_hip_bytes_resident())
+
+    def matmul(self, name: str, x: np.ndarray, n_out: int):
+        """y[n_tok, n_out] or None when the device call failed (caller uses the CPU)."""
+        x = np.ascontiguousarray(x, np.float32)
+        n_tok, n_in = x.shape
+        y = np.empty((n_tok, n_out), np.float32)
+        ok = self.L.fish_hip_backend_matmul(self._key(name), x.ctypes.data, n_tok, n_in, n_out, y.ctypes.data)
+        return y if ok else None
+
+    def matmul_group(self, names, x: np.ndarray, n_outs):
+        x = np.ascontiguousarray(x, np.float32)
+        n_tok, n_in = x.shape
+        ys = [np.empty((n_tok, n), np.float32) for n in n_outs]
+        keys = (ctypes.c_void_p * len(names))(*[self._key(n).value for n in names])
+        outs = (ctypes.c_int * len(names))(*n_outs)
+        yp = (ctypes.c_void_p * len(names))(*[y.ctypes.data for y in ys])
+        ok = self.L.fish_hip_backend_matmul_group(keys, len(names), x.ctypes.data, n_tok, n_in, outs, yp)
+        return ys if ok else None

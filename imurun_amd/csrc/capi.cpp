@@ -1,0 +1,290 @@
+// C ABI of libfish_hip.so and the host-side backend object.
+//
+// HipBackend mirrors FISH's ComputeBackend (include/fish/backend.h:26-163):
+// weights are uploaded once (copied, then repacked on the device), keyed by
+// the caller's TensorInfo pointer; matmul is synchronous; one call at a time
+// (a mutex, like vulkan_backend.cpp:316); any HIP error disables the backend
+// for the rest of the process (the sticky broken_ flag of
+// vulkan_backend.cpp:1139-1156), after which every call returns "failed" so
+// that the caller computes on the CPU (ops.cpp:283-291). The device is
+// opened lazily on first use, never from a static initializer.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/fish_hip.h"
+#include "common.h"
+#include "kernels.h"
+
+using namespace fishhip;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const std::string& msg) {
+    g_err = msg;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    return fail(FISH_HIP_ERR_DEVICE, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
+
+bool type_ok(uint32_t type) { return type == kQ8_0 || type == kQ4_0 || type == kQ4_K || type == kQ6_K; }
+
+// Matmul dispatch on an already quantized activation buffer: few tokens ->
+// the bandwidth-bound GEMV; many tokens of a K-quant -> the MFMA GEMM.
+constexpr int kGemvMaxTok = 8;
+
+hipError_t dispatch_matmul(const void* w, const WeightLayout& L, const void* act, int n_tok, float* y, int ldy,
+                           hipStream_t s) {
+    if (n_tok > kGemvMaxTok && is_kquant(L.type)) return launch_gemm(w, L, act, n_tok, y, ldy, s);
+    return launch_gemv(w, L, act, n_tok, y, ldy, s);
+}
+
+struct Resident {
+    void* dev = nullptr;
+    WeightLayout layout;
+    int n_expert = 1;
+    size_t bytes = 0;
+};
+
+class HipBackend {
+public:
+    static HipBackend& instance() {
+        static HipBackend* b = new HipBackend();  // deliberately leaked: no driver calls at exit
+        return *b;
+    }
+
+    bool available() {
+        std::lock_guard<std::mutex> lk(mu_);
+        return ensure_init();
+    }
+
+    const char* device_name() {
+        std::lock_guard<std::mutex> lk(mu_);
+        ensure_init();
+        return name_.c_str();
+    }
+
+    uint64_t memory(bool total) {
+        std::lock_guard<std::mutex> lk(mu_);
+        if (!ensure_init()) return 0;
+        size_t f = 0, t = 0;
+        if (hipMemGetInfo(&f, &t) != hipSuccess) return 0;
+        return total ? t : f;
+    }
+
+    bool upload(const void* key, uint32_t type, const void* data, int n_in, int n_out, int n_expert) {
+        std::lock_guard<std::mutex> lk(mu_);
+        if (!ensure_init() || !key || !data || !type_ok(type) || n_expert < 1) return false;
+        if (map_.count(key)) return true;
+        const WeightLayout L = weight_layout(type, n_in, n_out * n_expert);
+        if (!L.total) return false;
+        const size_t src_bytes = gguf_row_bytes(type, n_in) * size_t(n_out) * size_t(n_expert);
+        Resident r;
+        r.layout = L;
+        r.n_expert = n_expert;
+        r.bytes = L.total;
+        void* staging = nullptr;
+        if (hipMalloc(&r.dev, L.total) != hipSuccess) { r.dev = nullptr; return false; }
+        if (hipMalloc(&staging, src_bytes) != hipSuccess) { (void)hipFree(r.dev); return false; }
+        hipError_t e = hipMemcpyAsync(staging, data, src_bytes, hipMemcpyHostToDevice, stream_);
+        if (e == hipSuccess) e = launch_repack(type, staging, n_in, n_out * n_expert, r.dev, stream_);
+        if (e == hipSuccess) e = hipStreamSynchronize(stream_);
+        (void)hipFree(staging);
+        if (e != hipSuccess) {
+            (void)hipFree(r.dev);
+            mark_broken(e, "upload");
+            return false;
+        }
+        bytes_ += r.bytes;
+        map_[key] = r;
+        return true;
+    }
+
+    bool resident(const void* key) {
+        std::lock_guard<std::mutex> lk(mu_);
+        return !broken_ && map_.count(key) != 0;
+    }
+
+    void release(const void* key) {
+        std::lock_guard<std::mutex> lk(mu_);
+        auto it = map_.find(key);
+        if (it == map_.end()) return;
+        (void)hipFree(it->second.dev);
+        bytes_ -= it->second.bytes;
+        map_.erase(it);
+    }
+
+    uint64_t bytes_resident() {
+        std::lock_guard<std::mutex> lk(mu_);
+        return bytes_;
+    }
+
+    // Synchronous matmul group on host buffers; y untouched on failure.
+    bool matmul_group(const void* const* keys, int n, const float* x, int n_tok, int n_in, const int* n_outs,
+                      float* const* ys) {
+        std::lock_guard<std::mutex> lk(mu_);
+        if (!ensure_init() || broken_ || n <= 0 || n_tok <= 0 || !x) return false;
+        std::vector<const Resident*> rs(static_cast<size_t>(n));
+        size_t y_total = 0;
+        for (int i = 0; i < n; ++i) {
+            auto it = map_.find(keys[i]);
+            if (it == map_.end()) return false;
+            const Resident& r = it->second;
+            if (r.layout.n_in != n_in || r.layout.n_out != n_outs[i] * r.n_expert || r.n_expert != 1) return false;
+            rs[size_t(i)] = &r;
+            y_total += size_t(n_tok) * size_t(n_outs[i]);
+        }
+        const ActLayout AL = act_layout(n_tok, n_in);
+        if (!AL.total) return false;
+        for (int i = 0; i < n; ++i)
+            if (is_kquant(rs[size_t(i)]->layout.type) && !AL.has256) return false;
+        const size_t x_bytes = size_t(n_tok) * size_t(n_in) * 4;
+        if (!reserve(x_bytes, AL.total, y_total * 4)) return false;
+        hipError_t e = hipMemcpyAsync(d_x_, x, x_bytes, hipMemcpyHostToDevice, stream_);
+        if (e == hipSuccess) e = launch_quantize(static_cast<const float*>(d_x_), n_tok, n_in, n_in, d_act_, nullptr,
+                                                 nullptr, stream_);
+        size_t off = 0;
+        for (int i = 0; i < n && e == hipSuccess; ++i) {
+            e = dispatch_matmul(rs[size_t(i)]->dev, rs[size_t(i)]->layout, d_act_, n_tok,
+                                static_cast<float*>(d_y_) + off, n_outs[i], stream_);
+            off += size_t(n_tok) * size_t(n_outs[i]);
+        }
+        if (e == hipSuccess) e = hipStreamSynchronize(stream_);
+        if (e != hipSuccess) {
+            mark_broken(e, "matmul");
+            return false;
+        }
+        off = 0;
+        for (int i = 0; i < n; ++i) {
+            const size_t cnt = size_t(n_tok) * size_t(n_outs[i]);
+            e = hipMemcpy(ys[i], static_cast<float*>(d_y_) + off, cnt * 4, hipMemcpyDeviceToHost);
+            if (e != hipSuccess) {
+                mark_broken(e, "readback");
+                return false;
+            }
+            off += cnt;
+        }
+        return true;
+    }
+
+private:
+    HipBackend() = default;
+
+    bool ensure_init() {
+        if (init_done_) return ok_;
+        init_done_ = true;
+        int n = 0;
+        if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return ok_ = false;
+        hipDeviceProp_t p;
+        if (hipGetDeviceProperties(&p, 0) != hipSuccess) return ok_ = false;
+        name_ = p.name;
+        if (std::string(p.gcnArchName).rfind("gfx950", 0) != 0) return ok_ = false;
+        if (hipStreamCreate(&stream_) != hipSuccess) return ok_ = false;
+        return ok_ = true;
+    }
+
+    bool reserve(size_t xb, size_t ab, size_t yb) {
+        auto grow = [&](void*& p, size_t& cap, size_t need) {
+            if (need <= cap) return true;
+            if (p) (void)hipFree(p);
+            p = nullptr;
+            cap = 0;
+            if (hipMalloc(&p, need) != hipSuccess) return false;
+            cap = need;
+            return true;
+        };
+        return grow(d_x_, cap_x_, xb) && grow(d_act_, cap_act_, ab) && grow(d_y_, cap_y_, yb);
+    }
+
+    void mark_broken(hipError_t e, const char* what) {
+        broken_ = true;
+        g_err = std::string("hip backend disabled after ") + what + ": " + hipGetErrorString(e);
+        std::fprintf(stderr, "[fish_hip] %s\n", g_err.c_str());
+    }
+
+    std::mutex mu_;
+    bool init_done_ = false, ok_ = false, broken_ = false;
+    std::string name_ = "";
+    hipStream_t stream_ = nullptr;
+    std::unordered_map<const void*, Resident> map_;
+    uint64_t bytes_ = 0;
+    void *d_x_ = nullptr, *d_act_ = nullptr, *d_y_ = nullptr;
+    size_t cap_x_ = 0, cap_act_ = 0, cap_y_ = 0;
+};
+
+}  // namespace
+
+extern "C" {
+
+int fish_hip_abi_version(void) { return FISH_HIP_ABI_VERSION; }
+const char* fish_hip_kernel_name(void) { return "hip-gfx950"; }
+const char* fish_hip_last_error(void) { return g_err.c_str(); }
+
+uint64_t fish_hip_weight_bytes(uint32_t type, int n_in, int n_out) { return weight_layout(type, n_in, n_out).total; }
+uint64_t fish_hip_act_bytes(int n_tok, int n_in) { return act_layout(n_tok, n_in).total; }
+
+int fish_hip_quantize(const float* x, int n_tok, int n_in, void* act, void* q32_fish, void* q256_fish, void* stream) {
+    if (!x || !act || n_tok <= 0 || n_in <= 0 || n_in % 32) return fail(FISH_HIP_ERR_ARG, "quantize: bad arguments");
+    const hipError_t e = launch_quantize(x, n_tok, n_in, n_in, act, q32_fish, q256_fish, as_stream(stream));
+    return e == hipSuccess ? 0 : hip_fail(e, "quantize");
+}
+
+int fish_hip_repack(uint32_t type, const void* gguf, int n_in, int n_out, void* w, void* stream) {
+    if (!gguf || !w || !weight_layout(type, n_in, n_out).total) return fail(FISH_HIP_ERR_ARG, "repack: bad arguments");
+    const hipError_t e = launch_repack(type, gguf, n_in, n_out, w, as_stream(stream));
+    return e == hipSuccess ? 0 : hip_fail(e, "repack");
+}
+
+int fish_hip_matmul(uint32_t type, const void* w, const void* act, int n_tok, int n_in, int n_out, float* y,
+                    void* stream) {
+    const WeightLayout L = weight_layout(type, n_in, n_out);
+    if (!w || !act || !y || !L.total || n_tok <= 0) return fail(FISH_HIP_ERR_ARG, "matmul: bad arguments");
+    if (is_kquant(type) && n_in % 256) return fail(FISH_HIP_ERR_ARG, "matmul: K-quant needs n_in % 256 == 0");
+    const hipError_t e = dispatch_matmul(w, L, act, n_tok, y, n_out, as_stream(stream));
+    return e == hipSuccess ? 0 : hip_fail(e, "matmul");
+}
+
+int fish_hip_block_ints(uint32_t type, const void* w, const void* act, int n_in, int n_out, int32_t* out,
+                        void* stream) {
+    const WeightLayout L = weight_layout(type, n_in, n_out);
+    if (!w || !act || !out || !L.total) return fail(FISH_HIP_ERR_ARG, "block_ints: bad arguments");
+    const hipError_t e = launch_block_ints(w, L, act, out, as_stream(stream));
+    return e == hipSuccess ? 0 : hip_fail(e, "block_ints");
+}
+
+int fish_hip_backend_available(void) { return HipBackend::instance().available() ? 1 : 0; }
+const char* fish_hip_device_name(void) { return HipBackend::instance().device_name(); }
+uint64_t fish_hip_memory_total(void) { return HipBackend::instance().memory(true); }
+uint64_t fish_hip_memory_free(void) { return HipBackend::instance().memory(false); }
+int fish_hip_supports(uint32_t type) { return type_ok(type) ? 1 : 0; }
+
+int fish_hip_upload(const void* key, uint32_t type, const void* data, int n_in, int n_out, int n_expert) {
+    return HipBackend::instance().upload(key, type, data, n_in, n_out, n_expert) ? 1 : 0;
+}
+int fish_hip_resident(const void* key) { return HipBackend::instance().resident(key) ? 1 : 0; }
+void fish_hip_release(const void* key) { HipBackend::instance().release(key); }
+uint64_t fish_hip_bytes_resident(void) { return HipBackend::instance().bytes_resident(); }
+
+int fish_hip_backend_matmul(const void* key, const float* x, int n_tok, int n_in, int n_out, float* y) {
+    const void* keys[1] = {key};
+    float* ys[1] = {y};
+    return HipBackend::instance().matmul_group(keys, 1, x, n_tok, n_in, &n_out, ys) ? 1 : 0;
+}
+
+int fish_hip_backend_matmul_group(const void* const* keys, int n, const float* x, int n_tok, int n_in,
+                                  const int* n_outs, float* const* ys) {
+    return HipBackend::instance().matmul_group(keys, n, x, n_tok, n_in, n_outs, ys) ? 1 : 0;
+}
+
+}  // extern "C"

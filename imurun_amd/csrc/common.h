@@ -1,0 +1,185 @@
+// Shared definitions of the gfx950 quantized-matmul path: GGUF type ids,
+// the device layouts of weights and activations, and small device helpers.
+//
+// Device weight layout (one allocation per tensor, planes 256-byte aligned).
+// GGUF blocks are 18/34/144/210 bytes, which defeats 128-bit loads, so a
+// tensor is repacked once at upload into planes with the same total size:
+//   Q8_0  codes [N][K] int8                 d    [N][K/32]  f16
+//   Q4_0  codes [N][K/32][16] nibbles       d    [N][K/32]  f16
+//   Q4_K  codes [N][K/32][16] nibbles       meta [N][K/256][16] (d, dmin, scales[12])
+//   Q6_K  codes [N][K/32][16] low nibbles   qh   [N][K/32][8]  high bits
+//         sc   [N][K/16] int8               d    [N][K/256] f16
+// Every 16-byte code chunk holds one 32-element group in Q4_0's nibble order:
+// byte j = element j (low nibble) | element j+16 (high nibble). For Q6_K the
+// 8 qh bytes are two dwords (elements 0..15, 16..31); byte b of a dword holds
+// in bits 2k..2k+1 the two high bits of element 4k+b of that half.
+//
+// Device activation layout (written by the quantizer, read by the matmuls):
+//   q32  [M][K] int8   d32 [M][K/32] f32    s32 [M][K/32] int32   (Q8Act)
+//   q256 [M][K] int8   d256 [M][K/256] f32  s16 [M][K/16] int16   (Q8ActK)
+//   bsm  [M][K/256][16] int8: bytes 0..7 = bsum_g >> 6, 8..15 = bsum_g & 63
+// (bsum_g = the Q8ActK per-32 sum; s16 holds per-16 sums, two of which make
+// a bsum). The 256 planes exist only when K % 256 == 0.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace fishhip {
+
+enum : uint32_t { kQ4_0 = 2, kQ8_0 = 8, kQ4_K = 12, kQ6_K = 14 };
+
+inline size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
+
+struct WeightLayout {
+    uint32_t type = 0;
+    int n_in = 0, n_out = 0;
+    size_t codes = 0, aux = 0, sc = 0, d = 0, total = 0;  // plane byte offsets
+};
+
+// Plane offsets of a repacked tensor; total == 0 when the type/shape is refused.
+inline WeightLayout weight_layout(uint32_t type, int n_in, int n_out) {
+    WeightLayout L;
+    L.type = type;
+    L.n_in = n_in;
+    L.n_out = n_out;
+    const size_t N = size_t(n_out), K = size_t(n_in);
+    if (n_in <= 0 || n_out <= 0) return L;
+    size_t off = 0;
+    switch (type) {
+        case kQ8_0:
+            if (K % 32) return L;
+            L.codes = off; off = align256(off + N * K);
+            L.d = off;     off = align256(off + N * (K / 32) * 2);
+            break;
+        case kQ4_0:
+            if (K % 32) return L;
+            L.codes = off; off = align256(off + N * (K / 32) * 16);
+            L.d = off;     off = align256(off + N * (K / 32) * 2);
+            break;
+        case kQ4_K:
+            if (K % 256) return L;
+            L.codes = off; off = align256(off + N * (K / 32) * 16);
+            L.aux = off;   off = align256(off + N * (K / 256) * 16);
+            break;
+        case kQ6_K:
+            if (K % 256) return L;
+            L.codes = off; off = align256(off + N * (K / 32) * 16);
+            L.aux = off;   off = align256(off + N * (K / 32) * 8);
+            L.sc = off;    off = align256(off + N * (K / 16));
+            L.d = off;     off = align256(off + N * (K / 256) * 2);
+            break;
+        default:
+            return L;
+    }
+    L.total = off;
+    return L;
+}
+
+// GGUF bytes of one row (gguf.cpp:216-263 type table).
+inline size_t gguf_row_bytes(uint32_t type, int n_in) {
+    switch (type) {
+        case kQ8_0: return size_t(n_in / 32) * 34;
+        case kQ4_0: return size_t(n_in / 32) * 18;
+        case kQ4_K: return size_t(n_in / 256) * 144;
+        case kQ6_K: return size_t(n_in / 256) * 210;
+        default: return 0;
+    }
+}
+
+inline bool is_kquant(uint32_t type) { return type == kQ4_K || type == kQ6_K; }
+
+struct ActLayout {
+    int n_tok = 0, n_in = 0;
+    size_t q32 = 0, d32 = 0, s32 = 0, q256 = 0, d256 = 0, s16 = 0, bsm = 0, total = 0;
+    bool has256 = false;
+};
+
+inline ActLayout act_layout(int n_tok, int n_in) {
+    ActLayout L;
+    L.n_tok = n_tok;
+    L.n_in = n_in;
+    if (n_tok <= 0 || n_in <= 0 || n_in % 32) return L;
+    const size_t M = size_t(n_tok), K = size_t(n_in);
+    size_t off = 0;
+    L.q32 = off;  off = align256(off + M * K);
+    L.d32 = off;  off = align256(off + M * (K / 32) * 4);
+    L.s32 = off;  off = align256(off + M * (K / 32) * 4);
+    L.has256 = (K % 256) == 0;
+    if (L.has256) {
+        L.q256 = off; off = align256(off + M * K);
+        L.d256 = off; off = align256(off + M * (K / 256) * 4);
+        L.s16 = off;  off = align256(off + M * (K / 16) * 2);
+        L.bsm = off;  off = align256(off + M * (K / 256) * 16);
+    }
+    L.total = off;
+    return L;
+}
+
+// Device pointers of one activation buffer.
+struct ActPtrs {
+    const int8_t* q32;
+    const float* d32;
+    const int32_t* s32;
+    const int8_t* q256;
+    const float* d256;
+    const int16_t* s16;
+    const int8_t* bsm;
+};
+
+inline ActPtrs act_ptrs(const void* base, const ActLayout& L) {
+    const uint8_t* b = static_cast<const uint8_t*>(base);
+    ActPtrs p;
+    p.q32 = reinterpret_cast<const int8_t*>(b + L.q32);
+    p.d32 = reinterpret_cast<const float*>(b + L.d32);
+    p.s32 = reinterpret_cast<const int32_t*>(b + L.s32);
+    p.q256 = L.has256 ? reinterpret_cast<const int8_t*>(b + L.q256) : nullptr;
+    p.d256 = L.has256 ? reinterpret_cast<const float*>(b + L.d256) : nullptr;
+    p.s16 = L.has256 ? reinterpret_cast<const int16_t*>(b + L.s16) : nullptr;
+    p.bsm = L.has256 ? reinterpret_cast<const int8_t*>(b + L.bsm) : nullptr;
+    return p;
+}
+
+struct WeightPtrs {
+    const uint8_t* codes;
+    const uint8_t* aux;
+    const int8_t* sc;
+    const uint16_t* d;
+};
+
+inline WeightPtrs weight_ptrs(const void* base, const WeightLayout& L) {
+    const uint8_t* b = static_cast<const uint8_t*>(base);
+    WeightPtrs p;
+    p.codes = b + L.codes;
+    p.aux = b + L.aux;
+    p.sc = reinterpret_cast<const int8_t*>(b + L.sc);
+    p.d = reinterpret_cast<const uint16_t*>(b + L.d);
+    return p;
+}
+
+// ------------------------------------------------------------ device helpers
+
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, h));
+}
+
+__device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot4(static_cast<int>(a), static_cast<int>(b), c, false);
+}
+
+// 6-bit scale and min of sub-block g (0..7) from the 12 packed bytes s0..s11
+// held in three dwords (quant.cpp:136-144 layout).
+__device__ __forceinline__ void k4_scale_min(uint32_t s03, uint32_t s47, uint32_t s811, int g, int& sc, int& mn) {
+    const int h = (g & 3) * 8;
+    const uint32_t a = (s03 >> h) & 0xFF, b = (s47 >> h) & 0xFF, c = (s811 >> h) & 0xFF;
+    if (g < 4) {
+        sc = int(a & 63);
+        mn = int(b & 63);
+    } else {
+        sc = int((c & 15) | ((a >> 6) << 4));
+        mn = int((c >> 4) | ((b >> 6) << 4));
+    }
+}
+
+}  // namespace fishhip

@@ -1,0 +1,148 @@
+// Activation quantizer for gfx950: f32 rows -> FISH's two int8 layouts.
+//
+// Semantics (quantize_acts_scalar / quantize_acts_k_scalar, quant.cpp:400-434,
+// built per row by ActBatch::quantize, ops.cpp:158-175):
+//   per block of B values (B = 32 or 256): amax = max |x|; d = amax / 127
+//   (IEEE f32 division); id = d > 0 ? 1 / d : 0; q = clamp(rint(x * id),
+//   -127, 127) with round-half-to-even; 32-layout keeps sum(q), 256-layout
+//   keeps the eight per-32 sums.
+// The absmax is order independent, so a wavefront reduction is exact; the
+// division and reciprocal are the correctly rounded IEEE operations (the
+// build keeps -fhip-fp32-correctly-rounded-divide-sqrt and denormals), and
+// x * id is a single rounding fed to v_rndne_f32. Inputs are assumed free of
+// NaN (FISH's std::max would skip them; the hardware max would not).
+//
+// One wavefront per (token, 256-value chunk); each lane owns 4 consecutive
+// values. Lanes 8j..8j+7 form the 32-block j of the chunk.
+#include "common.h"
+#include "kernels.h"
+
+namespace fishhip {
+
+namespace {
+
+__device__ __forceinline__ float wave_max8(float v) {
+    v = fmaxf(v, __shfl_xor(v, 1));
+    v = fmaxf(v, __shfl_xor(v, 2));
+    v = fmaxf(v, __shfl_xor(v, 4));
+    return v;
+}
+
+__device__ __forceinline__ int wave_sum8(int v) {
+    v += __shfl_xor(v, 1);
+    v += __shfl_xor(v, 2);
+    v += __shfl_xor(v, 4);
+    return v;
+}
+
+__device__ __forceinline__ int code(float x, float id) {
+    const float p = __fmul_rn(x, id);
+    const int q = static_cast<int>(__builtin_rintf(p));
+    return q < -127 ? -127 : (q > 127 ? 127 : q);
+}
+
+__device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
+    return (uint32_t(a) & 0xFF) | ((uint32_t(b) & 0xFF) << 8) | ((uint32_t(c) & 0xFF) << 16) | (uint32_t(d) << 24);
+}
+
+struct QuantOut {
+    int8_t* q32; float* d32; int32_t* s32;
+    int8_t* q256; float* d256; int16_t* s16; int8_t* bsm;
+    uint8_t* aos32;   // optional FISH Q8Act rows (40 B blocks)
+    uint8_t* aos256;  // optional FISH Q8ActK rows (276 B blocks)
+};
+
+__global__ __launch_bounds__(256) void quantize_kernel(const float* __restrict__ x, int n_tok, int n_in, int ldx,
+                                                       QuantOut o) {
+    const int lane = threadIdx.x & 63;
+    const int chunks = (n_in + 255) / 256;
+    const long wave = long(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (wave >= long(n_tok) * chunks) return;
+    const int t = int(wave / chunks), c = int(wave % chunks);
+    const int k0 = c * 256 + lane * 4;
+    const bool active = k0 < n_in;  // n_in % 32 == 0: whole 8-lane groups switch together
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (active) v = *reinterpret_cast<const float4*>(x + size_t(t) * ldx + k0);
+    const float a = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+
+    // ---- 32-value blocks
+    {
+        const float amax = wave_max8(a);
+        const float d = amax / 127.0f;
+        const float id = d > 0.0f ? 1.0f / d : 0.0f;
+        const int q0 = code(v.x, id), q1 = code(v.y, id), q2 = code(v.z, id), q3 = code(v.w, id);
+        const int sum = wave_sum8(q0 + q1 + q2 + q3);
+        if (active) {
+            const uint32_t packed = pack4(q0, q1, q2, q3);
+            *reinterpret_cast<uint32_t*>(o.q32 + size_t(t) * n_in + k0) = packed;
+            const size_t blk = size_t(t) * (n_in / 32) + k0 / 32;
+            if ((lane & 7) == 0) {
+                o.d32[blk] = d;
+                o.s32[blk] = sum;
+            }
+            if (o.aos32) {
+                uint8_t* b = o.aos32 + blk * 40;
+                *reinterpret_cast<uint32_t*>(b + 8 + 4 * (lane & 7)) = packed;
+                if ((lane & 7) == 0) {
+                    *reinterpret_cast<float*>(b) = d;
+                    *reinterpret_cast<int32_t*>(b + 4) = sum;
+                }
+            }
+        }
+    }
+
+    // ---- 256-value blocks (only when every row is a whole number of them)
+    if (o.q256 && (n_in % 256) == 0) {
+        float amax = a;
+        for (int off = 1; off < 64; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+        const float d = amax / 127.0f;
+        const float id = d > 0.0f ? 1.0f / d : 0.0f;
+        const int q0 = code(v.x, id), q1 = code(v.y, id), q2 = code(v.z, id), q3 = code(v.w, id);
+        const int s4 = q0 + q1 + q2 + q3;
+        // per-16 sums: lanes 4j..4j+3 hold one 16-value group; 8 lanes one 32-value group
+        int g16 = s4 + __shfl_xor(s4, 1);
+        g16 += __shfl_xor(g16, 2);
+        const int g32 = g16 + __shfl_xor(g16, 4);
+        const uint32_t packed = pack4(q0, q1, q2, q3);
+        *reinterpret_cast<uint32_t*>(o.q256 + size_t(t) * n_in + k0) = packed;
+        const size_t sb = size_t(t) * (n_in / 256) + c;
+        if (lane == 0) o.d256[sb] = d;
+        if ((lane & 3) == 0) o.s16[size_t(t) * (n_in / 16) + k0 / 16] = int16_t(g16);
+        if ((lane & 7) == 0) {
+            const int g = lane >> 3;
+            o.bsm[sb * 16 + g] = int8_t(g32 >> 6);      // arithmetic shift: floor(bsum / 64)
+            o.bsm[sb * 16 + 8 + g] = int8_t(g32 & 63);
+        }
+        if (o.aos256) {
+            uint8_t* b = o.aos256 + sb * 276;
+            *reinterpret_cast<uint32_t*>(b + 20 + 4 * lane) = packed;
+            if (lane == 0) *reinterpret_cast<float*>(b) = d;
+            if ((lane & 7) == 0) *reinterpret_cast<int16_t*>(b + 4 + 2 * (lane >> 3)) = int16_t(g32);
+        }
+    }
+}
+
+}  // namespace
+
+hipError_t launch_quantize(const float* x, int n_tok, int n_in, int ldx, void* act, void* aos32, void* aos256,
+                           hipStream_t stream) {
+    const ActLayout L = act_layout(n_tok, n_in);
+    if (!L.total) return hipErrorInvalidValue;
+    uint8_t* b = static_cast<uint8_t*>(act);
+    QuantOut o;
+    o.q32 = reinterpret_cast<int8_t*>(b + L.q32);
+    o.d32 = reinterpret_cast<float*>(b + L.d32);
+    o.s32 = reinterpret_cast<int32_t*>(b + L.s32);
+    o.q256 = L.has256 ? reinterpret_cast<int8_t*>(b + L.q256) : nullptr;
+    o.d256 = L.has256 ? reinterpret_cast<float*>(b + L.d256) : nullptr;
+    o.s16 = L.has256 ? reinterpret_cast<int16_t*>(b + L.s16) : nullptr;
+    o.bsm = L.has256 ? reinterpret_cast<int8_t*>(b + L.bsm) : nullptr;
+    o.aos32 = static_cast<uint8_t*>(aos32);
+    o.aos256 = L.has256 ? static_cast<uint8_t*>(aos256) : nullptr;
+    const long waves = long(n_tok) * ((n_in + 255) / 256);
+    const unsigned blocks = unsigned((waves + 3) / 4);
+    hipLaunchKernelGGL(quantize_kernel, dim3(blocks), dim3(256), 0, stream, x, n_tok, n_in, ldx, o);
+    return hipGetLastError();
+}
+
+}  // namespace fishhip

@@ -1,0 +1,125 @@
+/*
+ * fish_hip.h -- C ABI of the MI355X (gfx950) quantized-matmul path of FISH.
+ *
+ * libfish_hip.so exports these entry points. They replace FISH's CPU
+ * matmul hot path and plug in where FISH's device backends plug in:
+ *   - the operator surface (device pointers, asynchronous on a HIP stream)
+ *     replaces ActBatch::quantize / matmul_batch / moe_ffn;
+ *   - the backend surface (host pointers, synchronous) is the
+ *     ComputeBackend contract of include/fish/backend.h, reachable from C.
+ * Citations are files of the reference repository under model/fish/.
+ *
+ * Conventions
+ *   type       GGUF type id (gguf.h:25-33): 2 Q4_0, 8 Q8_0, 12 Q4_K, 14 Q6_K
+ *   n_in (K)   reduction length; n_out (N) weight rows; n_tok (M) tokens
+ *   y          f32 [n_tok][n_out], row-major (ops.h:78-84)
+ *   stream     a hipStream_t passed as void*, NULL = the null stream
+ *   return     0 on success, a negative code on error (fish_hip_last_error()
+ *              says why), like the int-returning fish_* functions (c_api.h:98-102)
+ * No entry point allocates device memory except the backend surface, which
+ * owns its weight copies and staging buffers (backend.h:41-71).
+ */
+#ifndef FISH_HIP_H
+#define FISH_HIP_H
+
+#include <stdint.h>
+
+#if defined(_WIN32)
+#define FISH_HIP_API __declspec(dllexport)
+#else
+#define FISH_HIP_API __attribute__((visibility("default")))
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FISH_HIP_ABI_VERSION 1
+
+#define FISH_HIP_ERR_ARG (-1)     /* bad argument or unsupported type/shape */
+#define FISH_HIP_ERR_DEVICE (-2)  /* HIP runtime error; the backend is disabled */
+#define FISH_HIP_ERR_NODEV (-3)   /* no usable gfx950 device */
+
+/* ---------------------------------------------------------------- identity */
+
+/* replaces fish_abi_version (c_api.h:93) for this library */
+FISH_HIP_API int fish_hip_abi_version(void);
+/* replaces fish_kernel_name (c_api.h:155-156, c_api.cpp:477): "hip-gfx950" */
+FISH_HIP_API const char* fish_hip_kernel_name(void);
+/* replaces fish_last_error (c_api.h:98-102); one message per calling thread */
+FISH_HIP_API const char* fish_hip_last_error(void);
+
+/* ---------------------------------------------------------------- layouts */
+
+/* Bytes of the repacked device copy of an [n_out][n_in] tensor, 0 when the
+ * type/shape is unsupported (the device counterpart of ggml_row_size * n_out,
+ * gguf.cpp:258-263). */
+FISH_HIP_API uint64_t fish_hip_weight_bytes(uint32_t type, int n_in, int n_out);
+/* Bytes of a device activation buffer for n_tok rows of n_in values (both
+ * int8 layouts of ActBatch, ops.h:63-76). */
+FISH_HIP_API uint64_t fish_hip_act_bytes(int n_tok, int n_in);
+
+/* ---------------------------------------------------------------- block writer (host) */
+
+/* FISH's quantize_row (quant.h:119, quantize.cpp:400-416) for n_rows rows of
+ * n_in f32 values on the host, byte-identical to FISH's packer, on n_threads
+ * threads. Prepares weights for upload. */
+FISH_HIP_API int fish_hip_quantize_rows(uint32_t type, const float* x, void* dst, int n_rows, int n_in,
+                                        int n_threads);
+
+/* ---------------------------------------------------------------- operators (device pointers) */
+
+/* ActBatch::quantize (ops.cpp:158-175) on the device: x f32 [n_tok][n_in] ->
+ * act (fish_hip_act_bytes). q32_fish / q256_fish (nullable) also receive
+ * FISH's byte layouts Q8Act[n_tok][n_in/32] / Q8ActK[n_tok][n_in/256]
+ * (quant.h:58-70), bit-identical to quantize_acts / quantize_acts_k. */
+FISH_HIP_API int fish_hip_quantize(const float* x, int n_tok, int n_in, void* act, void* q32_fish, void* q256_fish,
+                                   void* stream);
+
+/* Upload-time repack of GGUF rows already in device memory (n_out rows of
+ * ggml_row_size(type, n_in) bytes) into the device layout at w (the device
+ * side of ComputeBackend::upload, backend.h:41-42). */
+FISH_HIP_API int fish_hip_repack(uint32_t type, const void* gguf, int n_in, int n_out, void* w, void* stream);
+
+/* matmul_batch's int8 path (ops.cpp:177-216): y[t][i] = W_i . x_t on a
+ * repacked tensor and a quantized activation buffer. */
+FISH_HIP_API int fish_hip_matmul(uint32_t type, const void* w, const void* act, int n_tok, int n_in, int n_out,
+                                 float* y, void* stream);
+
+/* The per-block integers of FISH's AVX2 kernels (quant_x86.cpp:280-495) for
+ * every row of w against token 0 of act: Q8_0/Q4_0 one int32 per 32-block,
+ * Q4_K two per super-block (sum sc*dot, sum m*bsum), Q6_K one per super-block. */
+FISH_HIP_API int fish_hip_block_ints(uint32_t type, const void* w, const void* act, int n_in, int n_out,
+                                     int32_t* out, void* stream);
+
+/* ---------------------------------------------------------------- backend (host pointers, synchronous) */
+
+/* gpu_backend() != NULL (backend.h:191): a gfx950 device is usable. */
+FISH_HIP_API int fish_hip_backend_available(void);
+/* ComputeBackend::device_name / memory_total / memory_free (backend.h:31-36) */
+FISH_HIP_API const char* fish_hip_device_name(void);
+FISH_HIP_API uint64_t fish_hip_memory_total(void);
+FISH_HIP_API uint64_t fish_hip_memory_free(void);
+/* ComputeBackend::supports (backend.h:39): 1 when matmul on this type runs here */
+FISH_HIP_API int fish_hip_supports(uint32_t type);
+/* ComputeBackend::upload (backend.h:41-42): copy + repack one tensor, keyed by
+ * the caller's TensorInfo* (any stable pointer). data = GGUF bytes (host).
+ * n_expert > 1 uploads a 3-D [n_expert][n_out][n_in] expert tensor.
+ * Returns 1 on success, 0 when refused (earlier uploads stay intact). */
+FISH_HIP_API int fish_hip_upload(const void* key, uint32_t type, const void* data, int n_in, int n_out, int n_expert);
+/* ComputeBackend::resident / release / bytes_resident (backend.h:43, :70-71) */
+FISH_HIP_API int fish_hip_resident(const void* key);
+FISH_HIP_API void fish_hip_release(const void* key);
+FISH_HIP_API uint64_t fish_hip_bytes_resident(void);
+/* ComputeBackend::matmul (backend.h:73-76): y valid on return; 1 ok, 0 failed
+ * (y untouched; the caller recomputes on the CPU, ops.cpp:283-291). */
+FISH_HIP_API int fish_hip_backend_matmul(const void* key, const float* x, int n_tok, int n_in, int n_out, float* y);
+/* ComputeBackend::matmul_group (backend.h:78-87): several tensors, one input. */
+FISH_HIP_API int fish_hip_backend_matmul_group(const void* const* keys, int n, const float* x, int n_tok, int n_in,
+                                               const int* n_outs, float* const* ys);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FISH_HIP_H */

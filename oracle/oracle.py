@@ -1,0 +1,246 @@
+"""ctypes bindings of the checker libraries -- TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import
+this module; the product path (imurun_amd) never does.
+
+  Oracle  -> oracle/liboracle.so, the C restatement of FISH's CPU path
+  Ref     -> oracle/_ref/libfishref.so, the reference's own CPU path compiled
+             from its sources (None when it was not built)
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ORACLE_SO = os.path.join(HERE, "liboracle.so")
+REF_SO = os.path.join(HERE, "_ref", "libfishref.so")
+
+Q4_0, Q8_0, Q4_K, Q5_K, Q6_K = 2, 8, 12, 13, 14
+BLOCK_ELEMS = {Q4_0: 32, Q8_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256}
+BLOCK_BYTES = {Q4_0: 18, Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210}
+ACT32, ACT256 = 40, 276
+
+_P = ctypes.c_void_p
+_F = ctypes.POINTER(ctypes.c_float)
+
+
+def _ptr(a: np.ndarray):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def row_bytes(t: int, n: int) -> int:
+    return (n // BLOCK_ELEMS[t]) * BLOCK_BYTES[t]
+
+
+def uses_k_layout(t: int) -> bool:
+    return BLOCK_ELEMS[t] == 256
+
+
+def build(quiet: bool = True) -> None:
+    """Compile liboracle.so (and _ref when the reference sources exist)."""
+    out = subprocess.run(["make", "-C", HERE, "all"], capture_output=True, text=True)
+    if out.returncode != 0:
+        raise RuntimeError("oracle build failed:\n" + out.stdout + out.stderr)
+    if not quiet:
+        print(out.stdout)
+
+
+class Oracle:
+    def __init__(self, path: str = ORACLE_SO):
+        if not os.path.exists(path):
+            build()
+        L = ctypes.CDLL(path)
+        self.L = L
+        L.or_fp16_to_fp32.argtypes = [ctypes.c_uint16]
+        L.or_fp16_to_fp32.restype = ctypes.c_float
+        L.or_fp32_to_fp16.argtypes = [ctypes.c_float]
+        L.or_fp32_to_fp16.restype = ctypes.c_uint16
+        L.or_quantize_acts.argtypes = [_P, ctypes.c_uint64, _P]
+        L.or_quantize_acts_k.argtypes = [_P, ctypes.c_uint64, _P]
+        L.or_dequant_row.argtypes = [ctypes.c_uint32, _P, _P, ctypes.c_uint64]
+        L.or_block_dots.argtypes = [ctypes.c_uint32, _P, _P, ctypes.c_uint64, _P]
+        L.or_block_dots.restype = ctypes.c_int64
+        L.or_vec_dot_q8.argtypes = [ctypes.c_uint32, _P, _P, ctypes.c_uint64]
+        L.or_vec_dot_q8.restype = ctypes.c_float
+        L.or_matmul_batch.argtypes = [ctypes.c_uint32, _P, _P, _P, ctypes.c_int, ctypes.c_int, ctypes.c_int, _P, ctypes.c_int]
+        L.or_act_batch.argtypes = [_P, ctypes.c_int, ctypes.c_int, _P, _P]
+        L.or_quantize_row.argtypes = [ctypes.c_uint32, _P, _P, ctypes.c_uint64]
+        L.or_quantize_rows.argtypes = [ctypes.c_uint32, _P, _P, ctypes.c_int64, ctypes.c_uint64, ctypes.c_int]
+        L.or_route.argtypes = [_P, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, _P, _P]
+        L.or_silu.argtypes = [ctypes.c_float]
+        L.or_silu.restype = ctypes.c_float
+        L.or_moe_ffn.argtypes = [_P, _P, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                 ctypes.c_int, ctypes.c_uint32, _P, ctypes.c_uint32, _P, ctypes.c_uint32, _P, _P,
+                                 ctypes.c_int]
+        self.threads = min(16, os.cpu_count() or 1)
+
+    # activations -----------------------------------------------------------
+    def quantize_acts(self, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32)
+        n = x.size
+        out = np.zeros(n // 32 * ACT32, np.uint8)
+        self.L.or_quantize_acts(_ptr(x), n, _ptr(out))
+        return out
+
+    def quantize_acts_k(self, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32)
+        n = x.size
+        out = np.zeros(n // 256 * ACT256, np.uint8)
+        self.L.or_quantize_acts_k(_ptr(x), n, _ptr(out))
+        return out
+
+    def act_batch(self, x: np.ndarray):
+        """ActBatch::quantize: (q32 bytes, q256 bytes or None) for x[n_tok][n_in]."""
+        x = np.ascontiguousarray(x, np.float32)
+        n_tok, n_in = x.shape
+        q32 = np.zeros(n_tok * (n_in // 32) * ACT32, np.uint8)
+        q256 = np.zeros(n_tok * (n_in // 256) * ACT256, np.uint8) if n_in % 256 == 0 else None
+        self.L.or_act_batch(_ptr(x), n_tok, n_in, _ptr(q32), _ptr(q256) if q256 is not None else None)
+        return q32, q256
+
+    # weights ---------------------------------------------------------------
+    def quantize_rows(self, t: int, w: np.ndarray) -> np.ndarray:
+        w = np.ascontiguousarray(w, np.float32)
+        n_rows, n_in = w.shape
+        out = np.zeros(n_rows * row_bytes(t, n_in), np.uint8)
+        if not self.L.or_quantize_rows(t, _ptr(w), _ptr(out), n_rows, n_in, self.threads):
+            raise ValueError("bad type/shape")
+        return out
+
+    def dequant_row(self, t: int, row: np.ndarray, n: int) -> np.ndarray:
+        out = np.zeros(n, np.float32)
+        if not self.L.or_dequant_row(t, _ptr(np.ascontiguousarray(row)), _ptr(out), n):
+            raise ValueError("bad type/shape")
+        return out
+
+    def block_dots(self, t: int, row: np.ndarray, acts: np.ndarray, n: int) -> np.ndarray:
+        per = 2 if t in (Q4_K, Q5_K) else 1
+        out = np.zeros((n // BLOCK_ELEMS[t]) * per, np.int32)
+        k = self.L.or_block_dots(t, _ptr(np.ascontiguousarray(row)), _ptr(np.ascontiguousarray(acts)), n, _ptr(out))
+        assert k == out.size
+        return out
+
+    def vec_dot(self, t: int, row: np.ndarray, acts: np.ndarray, n: int) -> float:
+        return self.L.or_vec_dot_q8(t, _ptr(np.ascontiguousarray(row)), _ptr(np.ascontiguousarray(acts)), n)
+
+    def matmul(self, t: int, w: np.ndarray, q32, q256, n_tok: int, n_in: int, n_out: int) -> np.ndarray:
+        y = np.zeros((n_tok, n_out), np.float32)
+        ok = self.L.or_matmul_batch(t, _ptr(w), _ptr(q32) if q32 is not None else None,
+                                    _ptr(q256) if q256 is not None else None, n_tok, n_in, n_out, _ptr(y),
+                                    self.threads)
+        if not ok:
+            raise ValueError("bad matmul arguments")
+        return y
+
+    def matmul_f32(self, t: int, w: np.ndarray, x: np.ndarray, n_out: int) -> np.ndarray:
+        q32, q256 = self.act_batch(x)
+        return self.matmul(t, w, q32, q256, x.shape[0], x.shape[1], n_out)
+
+    # MoE ---------------------------------------------------------------------
+    def route(self, logits: np.ndarray, k: int, norm: bool = True):
+        logits = np.ascontiguousarray(logits, np.float32)
+        n_tok, ne = logits.shape
+        sel = np.zeros((n_tok, k), np.int32)
+        wsel = np.zeros((n_tok, k), np.float32)
+        self.L.or_route(_ptr(logits), n_tok, ne, k, int(norm), _ptr(sel), _ptr(wsel))
+        return sel, wsel
+
+    def silu(self, v: float) -> float:
+        return self.L.or_silu(v)
+
+    def moe_ffn(self, x, logits, E, F, NE, K, norm, tg, wg, tu, wu, td, wd) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32)
+        logits = np.ascontiguousarray(logits, np.float32)
+        n_tok = x.shape[0]
+        out = np.zeros((n_tok, E), np.float32)
+        self.L.or_moe_ffn(_ptr(x), _ptr(logits), n_tok, E, F, NE, K, int(norm), tg, _ptr(wg), tu, _ptr(wu), td,
+                          _ptr(wd), _ptr(out), self.threads)
+        return out
+
+
+class Ref:
+    """The reference's compiled CPU path (FISH's installed kernel table)."""
+
+    def __init__(self, path: str = REF_SO):
+        L = ctypes.CDLL(path)
+        self.L = L
+        L.ref_kernel_name.restype = ctypes.c_char_p
+        L.ref_fp16_to_fp32.argtypes = [ctypes.c_uint16]
+        L.ref_fp16_to_fp32.restype = ctypes.c_float
+        L.ref_fp32_to_fp16.argtypes = [ctypes.c_float]
+        L.ref_fp32_to_fp16.restype = ctypes.c_uint16
+        L.ref_quantize_acts.argtypes = [_P, ctypes.c_uint64, _P, ctypes.c_int]
+        L.ref_quantize_acts_k.argtypes = [_P, ctypes.c_uint64, _P, ctypes.c_int]
+        L.ref_dequant_row.argtypes = [ctypes.c_uint32, _P, _P, ctypes.c_uint64]
+        L.ref_quantize_row.argtypes = [ctypes.c_uint32, _P, _P, ctypes.c_uint64]
+        L.ref_vec_dot_q8.argtypes = [ctypes.c_uint32, _P, _P, ctypes.c_uint64, ctypes.c_int]
+        L.ref_vec_dot_q8.restype = ctypes.c_float
+        L.ref_matmul_f32.argtypes = [ctypes.c_uint32, _P, _P, ctypes.c_int, ctypes.c_int, ctypes.c_int, _P]
+        L.ref_matmul_acts.argtypes = [ctypes.c_uint32, _P, _P, _P, ctypes.c_int, ctypes.c_int, ctypes.c_int, _P]
+        L.ref_moe_ffn.argtypes = [_P, _P, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                  ctypes.c_int, ctypes.c_uint32, _P, ctypes.c_uint32, _P, ctypes.c_uint32, _P, _P, _P,
+                                  _P]
+
+    @staticmethod
+    def available() -> bool:
+        return os.path.exists(REF_SO)
+
+    def kernel_name(self) -> str:
+        return self.L.ref_kernel_name().decode()
+
+    def threads(self) -> int:
+        return self.L.ref_threads()
+
+    def quantize_acts(self, x, scalar=False):
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.zeros(x.size // 32 * ACT32, np.uint8)
+        self.L.ref_quantize_acts(_ptr(x), x.size, _ptr(out), int(scalar))
+        return out
+
+    def quantize_acts_k(self, x, scalar=False):
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.zeros(x.size // 256 * ACT256, np.uint8)
+        self.L.ref_quantize_acts_k(_ptr(x), x.size, _ptr(out), int(scalar))
+        return out
+
+    def quantize_row(self, t, x):
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.zeros(row_bytes(t, x.size), np.uint8)
+        assert self.L.ref_quantize_row(t, _ptr(x), _ptr(out), x.size)
+        return out
+
+    def dequant_row(self, t, row, n):
+        out = np.zeros(n, np.float32)
+        assert self.L.ref_dequant_row(t, _ptr(np.ascontiguousarray(row)), _ptr(out), n)
+        return out
+
+    def vec_dot(self, t, row, acts, n, scalar=False):
+        return self.L.ref_vec_dot_q8(t, _ptr(np.ascontiguousarray(row)), _ptr(np.ascontiguousarray(acts)), n,
+                                     int(scalar))
+
+    def matmul_f32(self, t, w, x, n_out):
+        x = np.ascontiguousarray(x, np.float32)
+        y = np.zeros((x.shape[0], n_out), np.float32)
+        self.L.ref_matmul_f32(t, _ptr(w), _ptr(x), x.shape[0], x.shape[1], n_out, _ptr(y))
+        return y
+
+    def matmul_acts(self, t, w, q32, q256, n_tok, n_in, n_out):
+        y = np.zeros((n_tok, n_out), np.float32)
+        self.L.ref_matmul_acts(t, _ptr(w), _ptr(q32), _ptr(q256) if q256 is not None else None, n_tok, n_in, n_out,
+                               _ptr(y))
+        return y
+
+    def moe_ffn(self, x, logits, E, F, NE, K, norm, tg, wg, tu, wu, td, wd):
+        x = np.ascontiguousarray(x, np.float32)
+        logits = np.ascontiguousarray(logits, np.float32)
+        n_tok = x.shape[0]
+        out = np.zeros((n_tok, E), np.float32)
+        sel = np.zeros((n_tok, K), np.int32)
+        wsel = np.zeros((n_tok, K), np.float32)
+        self.L.ref_moe_ffn(_ptr(x), _ptr(logits), n_tok, E, F, NE, K, int(norm), tg, _ptr(wg), tu, _ptr(wu), td,
+                           _ptr(wd), _ptr(out), _ptr(sel), _ptr(wsel))
+        return out, sel, wsel

@@ -1,0 +1,150 @@
+"""Writes the golden fixtures in this directory from the reference's own CPU path.
+
+Run in a container that holds the reference sources:
+    make -C oracle ref && python tests/golden/make_golden.py
+It loads oracle/_ref/libfishref.so (FISH's gguf/quant/quantize/quant_x86/ops
+sources compiled by oracle/Makefile) and stores inputs and outputs only.
+
+Fixtures (numpy .npz, no pickles):
+  acts.npz    Q8Act / Q8ActK bytes for the activation kinds of
+              test/test_kernels.cpp:135-152 (plain, outliers, zero blocks,
+              exact ties) at n = 256 and 4096.
+  pack.npz    quantize_row blocks and dequant_row floats for Q8_0, Q4_0,
+              Q4_K, Q5_K, Q6_K.
+  dots.npz    per-row int8 dots (scalar table and installed AVX2 table) on
+              fresh packed rows and on random-byte rows with sane scales
+              (test/test_kernels.cpp:89-107).
+  matmul.npz  ActBatch::quantize + matmul_batch outputs, N=32,
+              K in {512, 768}, M in {1, 3, 17}.
+  moe.npz     a tiny expert layer (NE=4, top-2, E=256, F=256, M=6,
+              gate/up Q4_K, down Q6_K) composed in model.cpp's order.
+"""
+from __future__ import annotations
+
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.dirname(os.path.dirname(HERE)))
+
+from imurun_amd.synth import normal, uniform  # noqa: E402
+from oracle.oracle import Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, Ref  # noqa: E402
+
+TYPES = [Q8_0, Q4_0, Q4_K, Q5_K, Q6_K]
+D_OFF = {Q4_0: 0, Q8_0: 0, Q4_K: 0, Q5_K: 0, Q6_K: 208}
+DMIN_OFF = {Q4_K: 2, Q5_K: 2}
+BSIZE = {Q4_0: 18, Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210}
+BLK = {Q4_0: 32, Q8_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256}
+
+
+def make_acts(n: int, kind: int, seed: int) -> np.ndarray:
+    u = uniform(seed, 2 * n).reshape(n, 2)
+    sym = (u[:, 0] * 2.0 - 1.0)
+    if kind == 0:
+        x = sym * 2.0
+    elif kind == 1:
+        x = sym * np.where(u[:, 1] < 0.01, 50.0, 1.0)
+    elif kind == 2:
+        x = np.where((np.arange(n) // 64) % 3 == 0, 0.0, sym * 0.01)
+    else:
+        r = np.floor(u[:, 0] * 253).astype(np.int64) - 126
+        x = r + 0.5 * (u[:, 1] < 0.5)
+        x = np.where(np.arange(n) % 32 == 0, 127.0, x)
+    return x.astype(np.float32)
+
+
+def random_row(ref: Ref, t: int, n: int, seed: int, mode: int) -> np.ndarray:
+    if mode == 0:
+        w = normal(seed, n, 1.0) * np.where(uniform(seed + 1, n) < 0.02, 8.0, 1.0).astype(np.float32)
+        return ref.quantize_row(t, w.astype(np.float32))
+    nb = n // BLK[t]
+    row = (np.asarray(uniform(seed, nb * BSIZE[t])) * 256).astype(np.uint8)
+    blocks = row.reshape(nb, BSIZE[t])
+    scales = (0.001 + uniform(seed + 7, 2 * nb).reshape(nb, 2) * 0.05).astype(np.float32)
+    h = scales.astype(np.float16).view(np.uint16)
+    blocks[:, D_OFF[t]:D_OFF[t] + 2] = h[:, 0:1].view(np.uint8).reshape(nb, 2)
+    if t in DMIN_OFF:
+        blocks[:, DMIN_OFF[t]:DMIN_OFF[t] + 2] = h[:, 1:2].view(np.uint8).reshape(nb, 2)
+    return blocks.reshape(-1).copy()
+
+
+def main() -> None:
+    ref = Ref()
+    print("reference kernel table:", ref.kernel_name())
+
+    d = {}
+    for n in (256, 4096):
+        for kind in range(4):
+            x = make_acts(n, kind, 7 + 10 * kind + n)
+            d[f"x_{n}_{kind}"] = x
+            d[f"q32_{n}_{kind}"] = ref.quantize_acts(x, scalar=True)
+            d[f"q256_{n}_{kind}"] = ref.quantize_acts_k(x, scalar=True)
+            assert np.array_equal(d[f"q32_{n}_{kind}"], ref.quantize_acts(x))
+            assert np.array_equal(d[f"q256_{n}_{kind}"], ref.quantize_acts_k(x))
+    np.savez_compressed(os.path.join(HERE, "acts.npz"), **d)
+
+    d = {}
+    for t in TYPES:
+        w = np.concatenate([normal(100 + t, 1024, 0.02), normal(200 + t, 1024, 1.0) *
+                            np.where(uniform(300 + t, 1024) < 0.02, 8.0, 1.0).astype(np.float32),
+                            np.zeros(256, np.float32)]).astype(np.float32)
+        packed = ref.quantize_row(t, w)
+        d[f"w_{t}"] = w
+        d[f"packed_{t}"] = packed
+        d[f"deq_{t}"] = ref.dequant_row(t, packed, w.size)
+    np.savez_compressed(os.path.join(HERE, "pack.npz"), **d)
+
+    d = {}
+    for t in TYPES:
+        rows, acts, want_s, want_a, ns = [], [], [], [], []
+        for n in (256, 1024):
+            for r in range(8):
+                row = random_row(ref, t, n, 1000 * t + 17 * r + n, r & 1)
+                x = make_acts(n, r % 3, 5000 * t + r + n)
+                a = ref.quantize_acts(x) if BLK[t] == 32 else ref.quantize_acts_k(x)
+                rows.append(row)
+                acts.append(a)
+                ns.append(n)
+                want_s.append(ref.vec_dot(t, row, a, n, scalar=True))
+                want_a.append(ref.vec_dot(t, row, a, n, scalar=False))
+        d[f"n_{t}"] = np.array(ns, np.int32)
+        d[f"rows_{t}"] = np.concatenate(rows)
+        d[f"acts_{t}"] = np.concatenate(acts)
+        d[f"scalar_{t}"] = np.array(want_s, np.float32)
+        d[f"avx2_{t}"] = np.array(want_a, np.float32)
+    np.savez_compressed(os.path.join(HERE, "dots.npz"), **d)
+
+    d = {}
+    n_out = 32
+    for t in (Q8_0, Q4_0, Q4_K, Q6_K):
+        for k in (512, 768):
+            w = normal(7000 + t + k, (n_out, k), 0.02)
+            packed = np.concatenate([ref.quantize_row(t, w[i]) for i in range(n_out)])
+            d[f"w_{t}_{k}"] = packed
+            for m in (1, 3, 17):
+                x = normal(8000 + t + k + m, (m, k), 1.0)
+                d[f"x_{t}_{k}_{m}"] = x
+                d[f"y_{t}_{k}_{m}"] = ref.matmul_f32(t, packed, x, n_out)
+    np.savez_compressed(os.path.join(HERE, "matmul.npz"), **d)
+
+    E, F, NE, K, M = 256, 256, 4, 2, 6
+    wg = normal(9001, (NE * F, E), 0.02)
+    wu = normal(9002, (NE * F, E), 0.02)
+    wd = normal(9003, (NE * E, F), 0.02)
+    pg = np.concatenate([ref.quantize_row(Q4_K, r) for r in wg])
+    pu = np.concatenate([ref.quantize_row(Q4_K, r) for r in wu])
+    pd = np.concatenate([ref.quantize_row(Q6_K, r) for r in wd])
+    x = normal(9004, (M, E), 1.0)
+    logits = normal(9005, (M, NE), 1.0)
+    out, sel, wsel = ref.moe_ffn(x, logits, E, F, NE, K, True, Q4_K, pg, Q4_K, pu, Q6_K, pd)
+    np.savez_compressed(os.path.join(HERE, "moe.npz"), E=E, F=F, NE=NE, K=K, x=x, logits=logits, gate=pg, up=pu,
+                        down=pd, out=out, sel=sel, wsel=wsel)
+    for f in sorted(os.listdir(HERE)):
+        if f.endswith(".npz"):
+            print(f, os.path.getsize(os.path.join(HERE, f)))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,75 @@
+"""The C-ABI library loads and exports what include/fish_hip.h declares (no GPU needed)."""
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+import imurun_amd as fh
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "fish_hip.h")
+
+
+def declared_symbols():
+    src = open(HEADER).read()
+    return sorted(set(re.findall(r"FISH_HIP_API\s+[\w\s\*]+?\b(fish_hip_\w+)\s*\(", src)))
+
+
+def test_header_declares_entry_points():
+    names = declared_symbols()
+    assert "fish_hip_matmul" in names and "fish_hip_quantize" in names and len(names) >= 20
+
+
+def test_library_exports_every_declared_symbol():
+    L = fh.load()
+    out = subprocess.run(["nm", "-D", "--defined-only", fh.LIB_PATH], capture_output=True, text=True).stdout
+    exported = set(re.findall(r"\sT\s+(\w+)", out))
+    for name in declared_symbols():
+        assert name in exported, name
+        assert getattr(L, name) is not None
+
+
+def test_identity():
+    L = fh.load()
+    assert L.fish_hip_abi_version() == 1
+    assert L.fish_hip_kernel_name() == b"hip-gfx950"
+
+
+@pytest.mark.parametrize("t", [fh.Q8_0, fh.Q4_0, fh.Q4_K, fh.Q6_K])
+@pytest.mark.parametrize("n_in,n_out", [(4096, 4096), (4096, 14336), (14336, 4096), (768, 2048), (2048, 768)])
+def test_weight_layout_size_matches_gguf(t, n_in, n_out):
+    # the repacked copy holds exactly the GGUF bytes plus at most 4 alignment pads
+    got = fh.weight_bytes(t, n_in, n_out)
+    gguf = fh.gguf_row_bytes(t, n_in) * n_out
+    assert gguf <= got <= gguf + 4 * 256
+
+
+def test_layout_refusals():
+    assert fh.weight_bytes(fh.Q4_K, 4000, 16) == 0     # K-quant rows need n_in % 256 == 0
+    assert fh.weight_bytes(fh.Q8_0, 48, 16) == 0       # 32-blocks need n_in % 32 == 0
+    assert fh.weight_bytes(99, 4096, 16) == 0
+    assert fh.act_bytes(4, 48) == 0
+    assert fh.act_bytes(1, 4096) >= 4096 * 2 + 4096 // 32 * 8
+
+
+def test_bad_arguments_return_errors_without_device_work():
+    L = fh.load()
+    assert L.fish_hip_quantize(None, 1, 4096, None, None, None, None) == -1
+    assert "bad arguments" in fh.last_error()
+    assert L.fish_hip_matmul(fh.Q4_K, None, None, 1, 4000, 16, None, None) == -1
+    assert L.fish_hip_supports(fh.Q4_K) == 1 and L.fish_hip_supports(3) == 0
+
+
+@pytest.mark.parametrize("t", [fh.Q8_0, fh.Q4_0, fh.Q4_K, fh.Q6_K])
+def test_block_writer_matches_golden_and_oracle(golden, oracle, t):
+    """The library's host packer (input preparation) writes FISH's bytes."""
+    g = golden("pack")
+    w = g[f"w_{t}"]
+    assert np.array_equal(fh.quantize_rows(t, w.reshape(1, -1)), g[f"packed_{t}"])
+    from imurun_amd.synth import normal
+    x = normal(31 + t, (64, 1024), 0.02)
+    x[3, :256] = 0.0
+    x[5, 7] = 9.0
+    assert np.array_equal(fh.quantize_rows(t, x, n_threads=3), oracle.quantize_rows(t, x))

@@ -1,0 +1,199 @@
+"""Parity of the HIP path (through the C ABI) with the oracle and the golden vectors.
+
+Bars: int8 activations, f32 activation scales and per-block int32 dot sums
+bit-exact; f32 outputs within 1e-4 * max|y_ref| (max abs error over the
+output), y_ref being FISH's CPU result on identical inputs.
+"""
+import numpy as np
+import pytest
+
+import imurun_amd as fh
+from imurun_amd.synth import normal, uniform
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+TYPES = [fh.Q8_0, fh.Q4_0, fh.Q4_K, fh.Q6_K]
+
+
+@pytest.fixture(scope="module")
+def torch_dev():
+    import torch
+    assert torch.cuda.is_available(), "GPU tests need a ROCm device"
+    fh.load()
+    return torch, torch.device("cuda:0")
+
+
+def dev_u8(torch_dev, a):
+    torch, d = torch_dev
+    return torch.from_numpy(np.ascontiguousarray(a, np.uint8)).to(d)
+
+
+def dev_f32(torch_dev, a):
+    torch, d = torch_dev
+    return torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(d)
+
+
+def packed_weights(oracle, t, n_out, n_in, seed, std=0.02):
+    return oracle.quantize_rows(t, normal(seed, (n_out, n_in), std))
+
+
+def random_rows(t, n_out, n_in, seed):
+    """Random bytes with sane f16 scales: every code / scale bit pattern (test_kernels.cpp:89-107)."""
+    be, bb = fh.BLOCK_ELEMS[t], fh.BLOCK_BYTES[t]
+    nb = n_out * n_in // be
+    blocks = (uniform(seed, nb * bb) * 256).astype(np.uint8).reshape(nb, bb)
+    sc = (0.001 + uniform(seed + 1, 2 * nb) * 0.05).astype(np.float32).astype(np.float16).view(np.uint16)
+    sc = sc.reshape(nb, 2)
+    d_off = 208 if t == fh.Q6_K else 0
+    blocks[:, d_off:d_off + 2] = sc[:, :1].view(np.uint8).reshape(nb, 2)
+    if t == fh.Q4_K:
+        blocks[:, 2:4] = sc[:, 1:].view(np.uint8).reshape(nb, 2)
+    return blocks.reshape(-1)
+
+
+def gpu_matmul(torch_dev, t, packed, x, n_out):
+    n_tok, n_in = x.shape
+    w = fh.repack(t, dev_u8(torch_dev, packed), n_in, n_out)
+    y = fh.matmul_batch(t, w, dev_f32(torch_dev, x), n_out)
+    return y.cpu().numpy()
+
+
+def check_close(got, want, what):
+    err = float(np.max(np.abs(got - want)))
+    scale = float(np.max(np.abs(want)))
+    assert err <= TOL * scale, f"{what}: max err {err:.3e} vs {TOL} * {scale:.3e}"
+
+
+# ------------------------------------------------------------------ quantizer
+
+@pytest.mark.parametrize("n", [256, 4096])
+@pytest.mark.parametrize("kind", [0, 1, 2, 3])
+def test_quantizer_matches_golden_bytes(torch_dev, golden, n, kind):
+    g = golden("acts")
+    x = dev_f32(torch_dev, g[f"x_{n}_{kind}"].reshape(1, n))
+    _, q32, q256 = fh.quantize(x, fish_layouts=True)
+    assert np.array_equal(q32.cpu().numpy(), g[f"q32_{n}_{kind}"])
+    assert np.array_equal(q256.cpu().numpy(), g[f"q256_{n}_{kind}"])
+
+
+@pytest.mark.parametrize("n_tok,n_in", [(1, 4096), (7, 14336), (64, 2048), (33, 768), (5, 96), (3, 32)])
+def test_quantizer_batches_match_oracle(torch_dev, oracle, n_tok, n_in):
+    x = normal(1000 + n_tok + n_in, (n_tok, n_in)) * np.float32(2.0)
+    x[0, :32] = 0.0                                      # a zero block
+    if n_in >= 64:
+        x[-1, 32:64] *= np.float32(50.0)                 # an outlier block
+    _, q32, q256 = fh.quantize(dev_f32(torch_dev, x), fish_layouts=True)
+    w32, w256 = oracle.act_batch(x)
+    assert np.array_equal(q32.cpu().numpy(), w32)
+    if n_in % 256 == 0:
+        assert np.array_equal(q256.cpu().numpy(), w256)
+    else:
+        assert q256 is None
+
+
+# ------------------------------------------------------------------ per-block integers
+
+@pytest.mark.parametrize("t", TYPES)
+@pytest.mark.parametrize("n_in", [256, 768, 4096])
+@pytest.mark.parametrize("mode", ["packed", "random"])
+def test_block_ints_bit_exact(torch_dev, oracle, t, n_in, mode):
+    n_out = 48
+    rows = packed_weights(oracle, t, n_out, n_in, 77 + n_in) if mode == "packed" else random_rows(t, n_out, n_in, 78)
+    x = normal(90 + n_in, (1, n_in)) * np.float32(1.5)
+    a32, a256 = oracle.act_batch(x)
+    w = fh.repack(t, dev_u8(torch_dev, rows), n_in, n_out)
+    act = fh.quantize(dev_f32(torch_dev, x))
+    got = fh.block_ints(t, w, act, n_in, n_out).cpu().numpy()
+    rb = fh.gguf_row_bytes(t, n_in)
+    acts = a32 if fh.BLOCK_ELEMS[t] == 32 else a256
+    want = np.concatenate([oracle.block_dots(t, rows[i * rb:(i + 1) * rb], acts, n_in) for i in range(n_out)])
+    assert np.array_equal(got, want)
+
+
+# ------------------------------------------------------------------ matmul
+
+@pytest.mark.parametrize("t", TYPES)
+@pytest.mark.parametrize("n_tok", [1, 2, 3, 4, 5, 8, 9, 16, 33, 130])
+def test_matmul_matches_oracle(torch_dev, oracle, t, n_tok):
+    n_in, n_out = (768 if t in (fh.Q4_K, fh.Q6_K) else 736), 96
+    rows = packed_weights(oracle, t, n_out, n_in, 300 + n_tok)
+    x = normal(400 + n_tok, (n_tok, n_in))
+    got = gpu_matmul(torch_dev, t, rows, x, n_out)
+    want = oracle.matmul_f32(t, rows, x, n_out)
+    check_close(got, want, f"{fh.TYPE_NAMES[t]} M={n_tok}")
+
+
+@pytest.mark.parametrize("t", TYPES)
+def test_matmul_random_codes(torch_dev, oracle, t):
+    n_in, n_out, n_tok = 1024, 80, 20
+    rows = random_rows(t, n_out, n_in, 501)
+    x = normal(502, (n_tok, n_in))
+    got = gpu_matmul(torch_dev, t, rows, x, n_out)
+    want = oracle.matmul_f32(t, rows, x, n_out)
+    check_close(got, want, f"{fh.TYPE_NAMES[t]} random codes")
+
+
+@pytest.mark.parametrize("t", TYPES)
+@pytest.mark.parametrize("k", [512, 768])
+def test_matmul_matches_reference_golden(torch_dev, golden, t, k):
+    g = golden("matmul")
+    for m in (1, 3, 17):
+        want = g[f"y_{t}_{k}_{m}"]
+        got = gpu_matmul(torch_dev, t, g[f"w_{t}_{k}"], g[f"x_{t}_{k}_{m}"], want.shape[1])
+        check_close(got, want, f"{fh.TYPE_NAMES[t]} K={k} M={m}")
+
+
+@pytest.mark.parametrize("t,n_out,n_in,n_tok", [
+    (fh.Q8_0, 4096, 4096, 1),
+    (fh.Q4_0, 14336, 4096, 1),
+    (fh.Q4_0, 4096, 14336, 1),
+    (fh.Q4_K, 14336, 4096, 512),
+    (fh.Q6_K, 4096, 14336, 512),
+])
+def test_full_size_shapes(torch_dev, oracle, t, n_out, n_in, n_tok):
+    """Full-size shapes: all rows on the GPU; a row/token sample checked against
+    the oracle, and row slicing must reproduce the full result bit for bit."""
+    torch, d = torch_dev
+    rows_np = packed_weights(oracle, t, n_out, n_in, 7, 0.02)
+    x = normal(8, (n_tok, n_in))
+    w = fh.repack(t, dev_u8(torch_dev, rows_np), n_in, n_out)
+    y = fh.matmul_batch(t, w, dev_f32(torch_dev, x), n_out).cpu().numpy()
+    rb = fh.gguf_row_bytes(t, n_in)
+    sel_rows = np.unique(np.concatenate([np.arange(64), (uniform(9, 64) * n_out).astype(int), [n_out - 1]]))
+    sel_tok = np.unique(np.concatenate([np.arange(min(n_tok, 8)), (uniform(10, 8) * n_tok).astype(int)]))
+    sub = np.concatenate([rows_np[i * rb:(i + 1) * rb] for i in sel_rows])
+    want = oracle.matmul_f32(t, sub, x[sel_tok], sel_rows.size)
+    check_close(y[np.ix_(sel_tok, sel_rows)], want, f"{fh.TYPE_NAMES[t]} {n_out}x{n_in} M={n_tok}")
+    # row slicing: the first 1024 rows on their own give identical bits
+    w_part = fh.repack(t, dev_u8(torch_dev, rows_np[:1024 * rb]), n_in, 1024)
+    y_part = fh.matmul_batch(t, w_part, dev_f32(torch_dev, x), 1024).cpu().numpy()
+    assert np.array_equal(y_part, y[:, :1024])
+
+
+# ------------------------------------------------------------------ backend surface
+
+def test_backend_upload_matmul_group(torch_dev, oracle):
+    be = fh.HipBackend()
+    assert be.available() and be.device_name()
+    n_in = 1024
+    ts = {"q": (fh.Q4_K, 256), "k": (fh.Q6_K, 128), "v": (fh.Q8_0, 64), "o": (fh.Q4_0, 96)}
+    packed = {}
+    for i, (name, (t, n_out)) in enumerate(ts.items()):
+        packed[name] = packed_weights(oracle, t, n_out, n_in, 600 + i)
+        before = be.bytes_resident()
+        assert be.upload(name, t, packed[name], n_in, n_out)
+        assert be.resident(name) and be.bytes_resident() > before
+    for n_tok in (1, 6, 40):
+        x = normal(700 + n_tok, (n_tok, n_in))
+        ys = be.matmul_group(list(ts), x, [n for _, n in ts.values()])
+        assert ys is not None
+        for (name, (t, n_out)), y in zip(ts.items(), ys):
+            check_close(y, oracle.matmul_f32(t, packed[name], x, n_out), f"backend {name} M={n_tok}")
+        y1 = be.matmul("q", x, 256)
+        assert np.array_equal(y1, ys[0])
+    # refusals leave the caller to compute on the CPU
+    assert be.matmul("missing", normal(1, (1, n_in)), 16) is None
+    assert be.matmul("q", normal(1, (1, n_in)), 255) is None
+    be.release("q")
+    assert not be.resident("q")
