@@ -37,7 +37,7 @@ def gemv_step_bytes():
     w = fh.gguf_row_bytes(fh.Q4_0, E) * F
     gate = w + E * 4 + F * 4
     down = fh.gguf_row_bytes(fh.Q4_0, F) * E + F * 4 + E * 4
-    return w + E * 4 + F * 4, 2 * gate + down, gate
+    return 2 * gate + down, gate
 
 
 def run_gemv(args, torch, fh, dev):
@@ -202,7 +202,7 @@ def main() -> int:
     dev = torch.device("cuda:0")
     fh.load()
 
-    step_bytes, _, gate_bytes = gemv_step_bytes()
+    step_bytes, gate_bytes = gemv_step_bytes()
     elapsed, copies, gate_us = run_gemv(args, torch, fh, dev)
     ms = elapsed / args.steps * 1e3
     value = step_bytes / (elapsed / args.steps) / 1e9

@@ -6,8 +6,10 @@
 // row's 32-element groups sub, sub+LPR, ... so one load instruction of the
 // wavefront covers LPR consecutive 16-byte chunks of a row. The lane computes
 // each group's exact integer dot (dots.h) and scales it in f32; the LPR
-// partial sums are reduced with cross-lane shuffles at the end. Activations
-// (a few KB) are read through the caches; the weights stream past once.
+// partial sums are reduced with cross-lane shuffles at the end. Each
+// wavefront walks several rows with their loads issued together; for a single
+// token its activation groups are loaded once into registers, otherwise they
+// are read through the caches. The weights stream past once.
 //
 // Also here: the per-block integer dump used by the parity tests, built from
 // the same dots.h functions.
@@ -57,77 +59,121 @@ __device__ __forceinline__ Frag load_group(const WeightPtrs& W, int row, int c, 
     return f;
 }
 
-// f32 contribution of group c of a row for token t.
+// Activation side of one 32-element group for one token.
+struct ActFrag {
+    uint4 a0, a1;  // 32 int8 codes
+    float d;       // Q8Act d (32-layouts) or Q8ActK d of the super-block
+    int s, s2;     // Q4_0: block sum; K-quants: the two per-16 sums
+};
+
 template <uint32_t T>
-__device__ __forceinline__ float group_dot(const Frag& f, const ActPtrs& A, int t, int c, int n_in) {
+__device__ __forceinline__ ActFrag load_act(const ActPtrs& A, int t, int c, int n_in) {
+    ActFrag a;
     if constexpr (T == kQ8_0 || T == kQ4_0) {
-        const uint4* a = reinterpret_cast<const uint4*>(A.q32 + size_t(t) * n_in + size_t(c) * 32);
-        const uint4 a0 = a[0], a1 = a[1];
+        const uint4* p = reinterpret_cast<const uint4*>(A.q32 + size_t(t) * n_in + size_t(c) * 32);
+        a.a0 = p[0];
+        a.a1 = p[1];
         const size_t bi = size_t(t) * (n_in / 32) + c;
-        const float s = f.d * A.d32[bi];
-        int isum;
-        if constexpr (T == kQ8_0) isum = isum_q8_0(f.w0, f.w1, a0, a1);
-        else isum = isum_q4_0(f.w0, a0, a1, A.s32[bi]);
-        return float(isum) * s;
+        a.d = A.d32[bi];
+        a.s = (T == kQ4_0) ? A.s32[bi] : 0;
+        a.s2 = 0;
     } else {
-        const uint4* a = reinterpret_cast<const uint4*>(A.q256 + size_t(t) * n_in + size_t(c) * 32);
-        const uint4 a0 = a[0], a1 = a[1];
-        const float xd = A.d256[size_t(t) * (n_in / 256) + (c >> 3)];
+        const uint4* p = reinterpret_cast<const uint4*>(A.q256 + size_t(t) * n_in + size_t(c) * 32);
+        a.a0 = p[0];
+        a.a1 = p[1];
+        a.d = A.d256[size_t(t) * (n_in / 256) + (c >> 3)];
         const uint32_t s2 = *reinterpret_cast<const uint32_t*>(A.s16 + size_t(t) * (n_in / 16) + 2 * c);
-        const int s16a = int(int16_t(s2 & 0xFFFF)), s16b = int(int16_t(s2 >> 16));
-        if constexpr (T == kQ4_K) {
-            const int sumi = f.sca * dot_q4_k(f.w0, a0, a1);
-            const int mins = f.scb * (s16a + s16b);
-            return xd * (f.d * float(sumi) - f.dmin * float(mins));
-        } else {
-            const int sumi = isum_q6_k(f.w0, f.qh, a0, a1, s16a, s16b, f.sca, f.scb);
-            return (f.d * xd) * float(sumi);
-        }
+        a.s = int(int16_t(s2 & 0xFFFF));
+        a.s2 = int(int16_t(s2 >> 16));
+    }
+    return a;
+}
+
+// f32 contribution of one group (weights f, activations a).
+template <uint32_t T>
+__device__ __forceinline__ float group_dot(const Frag& f, const ActFrag& a) {
+    if constexpr (T == kQ8_0) {
+        return float(isum_q8_0(f.w0, f.w1, a.a0, a.a1)) * (f.d * a.d);
+    } else if constexpr (T == kQ4_0) {
+        return float(isum_q4_0(f.w0, a.a0, a.a1, a.s)) * (f.d * a.d);
+    } else if constexpr (T == kQ4_K) {
+        const int sumi = f.sca * dot_q4_k(f.w0, a.a0, a.a1);
+        const int mins = f.scb * (a.s + a.s2);
+        return a.d * (f.d * float(sumi) - f.dmin * float(mins));
+    } else {
+        const int sumi = isum_q6_k(f.w0, f.qh, a.a0, a.a1, a.s, a.s2, f.sca, f.scb);
+        return (f.d * a.d) * float(sumi);
     }
 }
 
-template <uint32_t T, int NT, int LPR, int U>
-__global__ __launch_bounds__(256) void gemv_kernel(WeightPtrs W, ActPtrs A, int n_in, int n_out, int n_tok,
+// Wavefront-row scheme: LPR lanes per row; a wavefront owns RPW = 64/LPR
+// interleaved rows per pass and `rpw` passes, RB passes at a time with all of
+// their weight loads in flight together. Lane `sub` covers groups
+// sub, sub + LPR, ... (at most MAXC of them). For one token the lane's
+// activation groups stay in registers for every row of the wavefront.
+template <uint32_t T, int NT, int LPR, int MAXC, int RB>
+__global__ __launch_bounds__(256) void gemv_kernel(WeightPtrs W, ActPtrs A, int n_in, int n_out, int n_tok, int rpw,
                                                    float* __restrict__ y, int ldy) {
-    constexpr int RPW = 64 / LPR;  // rows per wavefront
+    constexpr int RPW = 64 / LPR;
     const int lane = threadIdx.x & 63;
     const int sub = lane % LPR;
-    const int row = (int(blockIdx.x) * 4 + int(threadIdx.x >> 6)) * RPW + lane / LPR;
+    const int wave_id = int(blockIdx.x) * 4 + int(threadIdx.x >> 6);
+    const int row_base = wave_id * rpw * RPW + lane / LPR;
     const int t0 = int(blockIdx.y) * NT;
-    if (row >= n_out) return;  // whole LPR groups leave together
     const int groups = n_in / 32;
-    float acc[NT];
-#pragma unroll
-    for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
 
-    for (int c0 = sub; c0 < groups; c0 += LPR * U) {
-        Frag f[U];
+    ActFrag ac[NT == 1 ? MAXC : 1];
+    if constexpr (NT == 1) {
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int c = c0 + u * LPR;
-            if (c < groups) f[u] = load_group<T>(W, row, c, n_in);
+        for (int k = 0; k < MAXC; ++k) {
+            const int c = sub + k * LPR;
+            if (c < groups) ac[k] = load_act<T>(A, t0, c, n_in);
         }
+    }
+
+    for (int p0 = 0; p0 < rpw; p0 += RB) {
+        Frag f[RB][MAXC];
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int c = c0 + u * LPR;
-            if (c < groups) {
+        for (int rb = 0; rb < RB; ++rb) {
+            const int row = row_base + (p0 + rb) * RPW;
 #pragma unroll
-                for (int t = 0; t < NT; ++t)
-                    if (t0 + t < n_tok) acc[t] += group_dot<T>(f[u], A, t0 + t, c, n_in);
+            for (int k = 0; k < MAXC; ++k) {
+                const int c = sub + k * LPR;
+                if (row < n_out && c < groups) f[rb][k] = load_group<T>(W, row, c, n_in);
             }
         }
-    }
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
-        float v = acc[t];
+        for (int rb = 0; rb < RB; ++rb) {
+            const int row = row_base + (p0 + rb) * RPW;
+            float acc[NT];
 #pragma unroll
-        for (int off = LPR / 2; off > 0; off >>= 1) v += __shfl_xor(v, off);
-        acc[t] = v;
-    }
-    if (sub == 0) {
+            for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
 #pragma unroll
-        for (int t = 0; t < NT; ++t)
-            if (t0 + t < n_tok) y[size_t(t0 + t) * ldy + row] = acc[t];
+            for (int k = 0; k < MAXC; ++k) {
+                const int c = sub + k * LPR;
+                if (row < n_out && c < groups) {
+                    if constexpr (NT == 1) {
+                        acc[0] += group_dot<T>(f[rb][k], ac[k]);
+                    } else {
+#pragma unroll
+                        for (int t = 0; t < NT; ++t)
+                            if (t0 + t < n_tok) acc[t] += group_dot<T>(f[rb][k], load_act<T>(A, t0 + t, c, n_in));
+                    }
+                }
+            }
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                float v = acc[t];
+#pragma unroll
+                for (int off = LPR / 2; off > 0; off >>= 1) v += __shfl_xor(v, off);
+                acc[t] = v;
+            }
+            if (sub == 0 && row < n_out) {
+#pragma unroll
+                for (int t = 0; t < NT; ++t)
+                    if (t0 + t < n_tok) y[size_t(t0 + t) * ldy + row] = acc[t];
+            }
+        }
     }
 }
 
@@ -142,21 +188,20 @@ __global__ void block_ints_kernel(WeightPtrs W, ActPtrs A, int n_in, int n_out, 
     const int row = int(gid / per_row), b = int(gid % per_row);
     if constexpr (!kq) {
         const Frag f = load_group<T>(W, row, b, n_in);
-        const uint4* a = reinterpret_cast<const uint4*>(A.q32 + size_t(b) * 32);
-        if constexpr (T == kQ8_0) out[gid] = isum_q8_0(f.w0, f.w1, a[0], a[1]);
-        else out[gid] = isum_q4_0(f.w0, a[0], a[1], A.s32[b]);
+        const ActFrag a = load_act<T>(A, 0, b, n_in);
+        if constexpr (T == kQ8_0) out[gid] = isum_q8_0(f.w0, f.w1, a.a0, a.a1);
+        else out[gid] = isum_q4_0(f.w0, a.a0, a.a1, a.s);
     } else {
         int sumi = 0, mins = 0;
         for (int g = 0; g < 8; ++g) {
             const int c = 8 * b + g;
             const Frag f = load_group<T>(W, row, c, n_in);
-            const uint4* a = reinterpret_cast<const uint4*>(A.q256 + size_t(c) * 32);
-            const int s16a = A.s16[2 * c], s16b = A.s16[2 * c + 1];
+            const ActFrag a = load_act<T>(A, 0, c, n_in);
             if constexpr (T == kQ4_K) {
-                sumi += f.sca * dot_q4_k(f.w0, a[0], a[1]);
-                mins += f.scb * (s16a + s16b);
+                sumi += f.sca * dot_q4_k(f.w0, a.a0, a.a1);
+                mins += f.scb * (a.s + a.s2);
             } else {
-                sumi += isum_q6_k(f.w0, f.qh, a[0], a[1], s16a, s16b, f.sca, f.scb);
+                sumi += isum_q6_k(f.w0, f.qh, a.a0, a.a1, a.s, a.s2, f.sca, f.scb);
             }
         }
         if constexpr (T == kQ4_K) {
@@ -168,24 +213,40 @@ __global__ void block_ints_kernel(WeightPtrs W, ActPtrs A, int n_in, int n_out, 
     }
 }
 
-template <uint32_t T, int NT, int LPR>
+template <uint32_t T, int NT, int LPR, int MAXC>
 hipError_t gemv_launch(const WeightPtrs& W, const ActPtrs& A, int n_in, int n_out, int n_tok, float* y, int ldy,
                        hipStream_t s) {
-    constexpr int U = (T == kQ8_0) ? 2 : 4;
-    const int rows_per_block = 4 * (64 / LPR);
-    const dim3 grid(unsigned((n_out + rows_per_block - 1) / rows_per_block), unsigned((n_tok + NT - 1) / NT));
-    hipLaunchKernelGGL((gemv_kernel<T, NT, LPR, U>), grid, dim3(256), 0, s, W, A, n_in, n_out, n_tok, y, ldy);
+    constexpr int RPW = 64 / LPR;
+    constexpr int RB = (NT == 1) ? (MAXC <= 2 ? 4 : (MAXC <= 4 ? 2 : 2)) : 1;
+    // passes per wavefront: enough rows that ~4096 wavefronts cover the matrix
+    const int row_groups = (n_out + RPW - 1) / RPW;
+    const int rpw = RB * ((row_groups + RB * 4096 - 1) / (RB * 4096));
+    const int waves = (row_groups + rpw - 1) / rpw;
+    const dim3 grid(unsigned((waves + 3) / 4), unsigned((n_tok + NT - 1) / NT));
+    hipLaunchKernelGGL((gemv_kernel<T, NT, LPR, MAXC, RB>), grid, dim3(256), 0, s, W, A, n_in, n_out, n_tok, rpw, y,
+                       ldy);
     return hipGetLastError();
+}
+
+template <uint32_t T, int NT, int LPR>
+hipError_t gemv_pick_maxc(const WeightPtrs& W, const ActPtrs& A, int n_in, int n_out, int n_tok, float* y, int ldy,
+                          hipStream_t s) {
+    const int per_lane = (n_in / 32 + LPR - 1) / LPR;
+    if (per_lane <= 1) return gemv_launch<T, NT, LPR, 1>(W, A, n_in, n_out, n_tok, y, ldy, s);
+    if (per_lane <= 2) return gemv_launch<T, NT, LPR, 2>(W, A, n_in, n_out, n_tok, y, ldy, s);
+    if (per_lane <= 4) return gemv_launch<T, NT, LPR, 4>(W, A, n_in, n_out, n_tok, y, ldy, s);
+    if (per_lane <= 8) return gemv_launch<T, NT, LPR, 8>(W, A, n_in, n_out, n_tok, y, ldy, s);
+    return gemv_launch<T, NT, LPR, 16>(W, A, n_in, n_out, n_tok, y, ldy, s);
 }
 
 template <uint32_t T, int NT>
 hipError_t gemv_pick_lpr(const WeightPtrs& W, const ActPtrs& A, int n_in, int n_out, int n_tok, float* y, int ldy,
                          hipStream_t s) {
     const int groups = n_in / 32;
-    if (groups >= 64) return gemv_launch<T, NT, 64>(W, A, n_in, n_out, n_tok, y, ldy, s);
-    if (groups >= 32) return gemv_launch<T, NT, 32>(W, A, n_in, n_out, n_tok, y, ldy, s);
-    if (groups >= 16) return gemv_launch<T, NT, 16>(W, A, n_in, n_out, n_tok, y, ldy, s);
-    return gemv_launch<T, NT, 8>(W, A, n_in, n_out, n_tok, y, ldy, s);
+    if (groups >= 64) return gemv_pick_maxc<T, NT, 64>(W, A, n_in, n_out, n_tok, y, ldy, s);
+    if (groups >= 32) return gemv_pick_maxc<T, NT, 32>(W, A, n_in, n_out, n_tok, y, ldy, s);
+    if (groups >= 16) return gemv_pick_maxc<T, NT, 16>(W, A, n_in, n_out, n_tok, y, ldy, s);
+    return gemv_pick_maxc<T, NT, 8>(W, A, n_in, n_out, n_tok, y, ldy, s);
 }
 
 template <uint32_t T>
