@@ -58,6 +58,13 @@ def load() -> ctypes.CDLL:
         "fish_hip_matmul": ([ctypes.c_uint32, _P, _P, ctypes.c_int, ctypes.c_int, ctypes.c_int, _P, _P], ctypes.c_int),
         "fish_hip_block_ints": ([ctypes.c_uint32, _P, _P, ctypes.c_int, ctypes.c_int, _P, _P], ctypes.c_int),
         "fish_hip_quantize_rows": ([ctypes.c_uint32, _P, _P, ctypes.c_int, ctypes.c_int, ctypes.c_int], ctypes.c_int),
+        "fish_hip_moe_workspace_bytes": ([ctypes.c_int] * 5, ctypes.c_uint64),
+        "fish_hip_moe_ffn": ([_P, _P, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                              ctypes.c_int, ctypes.c_uint32, _P, ctypes.c_uint32, _P, ctypes.c_uint32, _P, _P,
+                              ctypes.c_uint64, _P, _P], ctypes.c_int),
+        "fish_hip_moe_route": ([_P, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, _P, ctypes.c_uint64, _P,
+                                _P, _P], ctypes.c_int),
+        "fish_hip_silu_mul_quantize": ([_P, _P, ctypes.c_int, ctypes.c_int, _P, _P, _P, _P], ctypes.c_int),
         "fish_hip_backend_available": ([], ctypes.c_int),
         "fish_hip_device_name": ([], ctypes.c_char_p),
         "fish_hip_memory_total": ([], ctypes.c_uint64),
@@ -179,6 +186,53 @@ def block_ints(t: int, w, act, n_in: int, n_out: int, stream=None):
     _check(load().fish_hip_block_ints(t, w.data_ptr(), act.data_ptr(), n_in, n_out, out.data_ptr(),
                                       _stream(stream)), "block_ints")
     return out
+
+
+# ------------------------------------------------------------------ expert FFN (torch tensors)
+
+def moe_workspace_bytes(n_tok: int, n_embd: int, n_ff: int, n_expert: int, k: int) -> int:
+    return int(load().fish_hip_moe_workspace_bytes(n_tok, n_embd, n_ff, n_expert, k))
+
+
+def moe_ffn(x, logits, n_ff: int, n_expert: int, k: int, norm: bool, tg: int, wg, tu: int, wu, td: int, wd,
+            out=None, workspace=None, stream=None):
+    """LlamaModel::moe_ffn with given router logits; weights repacked (n_expert * rows)."""
+    import torch
+    n_tok, n_embd = x.shape
+    nb = moe_workspace_bytes(n_tok, n_embd, n_ff, n_expert, k)
+    if nb == 0:
+        raise FishHipError("moe_ffn: unsupported sizes")
+    if workspace is None:
+        workspace = torch.empty(nb, dtype=torch.uint8, device=x.device)
+    if out is None:
+        out = torch.empty((n_tok, n_embd), dtype=torch.float32, device=x.device)
+    _check(load().fish_hip_moe_ffn(x.data_ptr(), logits.data_ptr(), n_tok, n_embd, n_ff, n_expert, k, int(norm), tg,
+                                   wg.data_ptr(), tu, wu.data_ptr(), td, wd.data_ptr(), workspace.data_ptr(),
+                                   workspace.numel(), out.data_ptr(), _stream(stream)), "moe_ffn")
+    return out
+
+
+def moe_route(logits, k: int, norm: bool = True, stream=None):
+    import torch
+    n_tok, n_expert = logits.shape
+    ws = torch.empty(moe_workspace_bytes(n_tok, 32, 32, n_expert, k), dtype=torch.uint8, device=logits.device)
+    sel = torch.empty((n_tok, k), dtype=torch.int32, device=logits.device)
+    wsel = torch.empty((n_tok, k), dtype=torch.float32, device=logits.device)
+    _check(load().fish_hip_moe_route(logits.data_ptr(), n_tok, n_expert, k, int(norm), ws.data_ptr(), ws.numel(),
+                                     sel.data_ptr(), wsel.data_ptr(), _stream(stream)), "moe_route")
+    return sel, wsel
+
+
+def silu_mul_quantize(g, u, stream=None):
+    """(act, FISH Q8ActK bytes or None, h) for h = silu(g) * u."""
+    import torch
+    n_rows, n_ff = g.shape
+    act = torch.empty(act_bytes(n_rows, n_ff), dtype=torch.uint8, device=g.device)
+    q256 = torch.empty(n_rows * (n_ff // 256) * 276, dtype=torch.uint8, device=g.device) if n_ff % 256 == 0 else None
+    h = torch.empty((n_rows, n_ff), dtype=torch.float32, device=g.device)
+    _check(load().fish_hip_silu_mul_quantize(g.data_ptr(), u.data_ptr(), n_rows, n_ff, act.data_ptr(), _ptr(q256),
+                                             h.data_ptr(), _stream(stream)), "silu_mul_quantize")
+    return act, q256, h
 
 
 # ------------------------------------------------------------------ backend (host buffers)

@@ -10,6 +10,7 @@
 // opened lazily on first use, never from a static initializer.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdio>
 #include <cstring>
 #include <mutex>
@@ -47,7 +48,92 @@ constexpr int kGemvMaxTok = 8;
 hipError_t dispatch_matmul(const void* w, const WeightLayout& L, const void* act, int n_tok, float* y, int ldy,
                            hipStream_t s) {
     if (n_tok > kGemvMaxTok && is_kquant(L.type)) return launch_gemm(w, L, act, n_tok, y, ldy, s);
-    return launch_gemv(w, L, act, n_tok, y, ldy, s);
+    return launch_gemv(w, L, act, n_tok, n_tok, y, ldy, s);
+}
+
+// Workspace of one expert-FFN call: routing arrays, the quantized input, the
+// per-slot gate/up/down rows and the quantized hidden rows (slot = one chosen
+// (token, expert) pair, grouped by expert).
+struct MoeWork {
+    int slots = 0, item_tokens = 1, max_items = 0;
+    size_t sel = 0, wsel = 0, counts = 0, offsets = 0, slot_tok = 0, tok_slot = 0, items = 0, n_items = 0;
+    size_t act_x = 0, g = 0, u = 0, act_h = 0, dn = 0, total = 0;
+};
+
+MoeWork moe_work(int n_tok, int n_embd, int n_ff, int n_expert, int k) {
+    MoeWork w;
+    if (n_tok <= 0 || n_embd <= 0 || n_ff <= 0 || n_expert <= 0 || k <= 0 || k > n_expert || k > 16 ||
+        n_expert > 256 || n_embd % 32 || n_ff % 32)
+        return w;
+    w.slots = n_tok * k;
+    const int avg = (w.slots + n_expert - 1) / n_expert;
+    w.item_tokens = avg <= 1 ? 1 : (avg <= 2 ? 2 : (avg <= 4 ? 4 : (avg <= 8 ? 8 : 16)));
+    w.max_items = std::min(n_expert, w.slots) + w.slots / w.item_tokens + 1;
+    const ActLayout ax = act_layout(n_tok, n_embd), ah = act_layout(w.slots, n_ff);
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        const size_t at = off;
+        off = align256(off + bytes);
+        return at;
+    };
+    w.sel = take(size_t(w.slots) * 4);
+    w.wsel = take(size_t(w.slots) * 4);
+    w.counts = take(size_t(n_expert) * 4);
+    w.offsets = take(size_t(n_expert + 1) * 4);
+    w.slot_tok = take(size_t(w.slots) * 4);
+    w.tok_slot = take(size_t(w.slots) * 4);
+    w.items = take(size_t(w.max_items) * 12);
+    w.n_items = take(4);
+    w.act_x = take(ax.total);
+    w.g = take(size_t(w.slots) * n_ff * 4);
+    w.u = take(size_t(w.slots) * n_ff * 4);
+    w.act_h = take(ah.total);
+    w.dn = take(size_t(w.slots) * n_embd * 4);
+    w.total = off;
+    return w;
+}
+
+MoeRouting moe_routing(void* ws, const MoeWork& w) {
+    uint8_t* b = static_cast<uint8_t*>(ws);
+    MoeRouting r;
+    r.sel = reinterpret_cast<int*>(b + w.sel);
+    r.wsel = reinterpret_cast<float*>(b + w.wsel);
+    r.counts = reinterpret_cast<int*>(b + w.counts);
+    r.offsets = reinterpret_cast<int*>(b + w.offsets);
+    r.slot_tok = reinterpret_cast<int*>(b + w.slot_tok);
+    r.tok_slot = reinterpret_cast<int*>(b + w.tok_slot);
+    r.items = reinterpret_cast<int*>(b + w.items);
+    r.n_items = reinterpret_cast<int*>(b + w.n_items);
+    return r;
+}
+
+// The whole expert FFN on device buffers (weights already repacked:
+// gate/up n_expert * n_ff rows of n_embd, down n_expert * n_embd rows of n_ff).
+hipError_t moe_ffn(const float* x, const float* logits, int n_tok, int n_embd, int n_ff, int n_expert, int k,
+                   int norm, uint32_t tg, const void* wg, uint32_t tu, const void* wu, uint32_t td, const void* wd,
+                   void* ws, const MoeWork& w, float* out, hipStream_t s) {
+    uint8_t* b = static_cast<uint8_t*>(ws);
+    const MoeRouting r = moe_routing(ws, w);
+    const WeightLayout Lg = weight_layout(tg, n_embd, n_expert * n_ff);
+    const WeightLayout Lu = weight_layout(tu, n_embd, n_expert * n_ff);
+    const WeightLayout Ld = weight_layout(td, n_ff, n_expert * n_embd);
+    if (!Lg.total || !Lu.total || !Ld.total) return hipErrorInvalidValue;
+    float* g = reinterpret_cast<float*>(b + w.g);
+    float* u = reinterpret_cast<float*>(b + w.u);
+    float* dn = reinterpret_cast<float*>(b + w.dn);
+    hipError_t e = launch_moe_route(logits, n_tok, n_expert, k, norm, w.item_tokens, r, s);
+    if (e == hipSuccess) e = launch_quantize(x, n_tok, n_embd, n_embd, b + w.act_x, nullptr, nullptr, s);
+    TokenMap up_map{r.items, r.n_items, r.slot_tok, n_ff};
+    if (e == hipSuccess)
+        e = launch_gemv(wg, Lg, b + w.act_x, n_tok, w.slots, g, n_ff, s, &up_map, w.item_tokens, w.max_items);
+    if (e == hipSuccess)
+        e = launch_gemv(wu, Lu, b + w.act_x, n_tok, w.slots, u, n_ff, s, &up_map, w.item_tokens, w.max_items);
+    if (e == hipSuccess) e = launch_quantize(g, w.slots, n_ff, n_ff, b + w.act_h, nullptr, nullptr, s, u, nullptr);
+    TokenMap down_map{r.items, r.n_items, nullptr, n_embd};
+    if (e == hipSuccess)
+        e = launch_gemv(wd, Ld, b + w.act_h, w.slots, w.slots, dn, n_embd, s, &down_map, w.item_tokens, w.max_items);
+    if (e == hipSuccess) e = launch_moe_combine(dn, r, n_tok, k, n_embd, out, s);
+    return e;
 }
 
 struct Resident {
@@ -261,6 +347,45 @@ int fish_hip_block_ints(uint32_t type, const void* w, const void* act, int n_in,
     if (!w || !act || !out || !L.total) return fail(FISH_HIP_ERR_ARG, "block_ints: bad arguments");
     const hipError_t e = launch_block_ints(w, L, act, out, as_stream(stream));
     return e == hipSuccess ? 0 : hip_fail(e, "block_ints");
+}
+
+uint64_t fish_hip_moe_workspace_bytes(int n_tok, int n_embd, int n_ff, int n_expert, int k) {
+    return moe_work(n_tok, n_embd, n_ff, n_expert, k).total;
+}
+
+int fish_hip_moe_ffn(const float* x, const float* logits, int n_tok, int n_embd, int n_ff, int n_expert, int k,
+                     int norm, uint32_t t_gate, const void* w_gate, uint32_t t_up, const void* w_up, uint32_t t_down,
+                     const void* w_down, void* workspace, uint64_t workspace_bytes, float* out, void* stream) {
+    const MoeWork w = moe_work(n_tok, n_embd, n_ff, n_expert, k);
+    if (!w.total || !x || !logits || !w_gate || !w_up || !w_down || !workspace || !out)
+        return fail(FISH_HIP_ERR_ARG, "moe_ffn: bad arguments");
+    if (workspace_bytes < w.total) return fail(FISH_HIP_ERR_ARG, "moe_ffn: workspace too small");
+    if (!type_ok(t_gate) || !type_ok(t_up) || !type_ok(t_down) ||
+        ((is_kquant(t_gate) || is_kquant(t_up)) && n_embd % 256) || (is_kquant(t_down) && n_ff % 256))
+        return fail(FISH_HIP_ERR_ARG, "moe_ffn: unsupported weight type/shape");
+    const hipError_t e = moe_ffn(x, logits, n_tok, n_embd, n_ff, n_expert, k, norm, t_gate, w_gate, t_up, w_up,
+                                 t_down, w_down, workspace, w, out, as_stream(stream));
+    return e == hipSuccess ? 0 : hip_fail(e, "moe_ffn");
+}
+
+int fish_hip_moe_route(const float* logits, int n_tok, int n_expert, int k, int norm, void* workspace,
+                       uint64_t workspace_bytes, int* sel, float* wsel, void* stream) {
+    const MoeWork w = moe_work(n_tok, 32, 32, n_expert, k);
+    if (!w.total || !logits || !workspace || !sel || !wsel) return fail(FISH_HIP_ERR_ARG, "moe_route: bad arguments");
+    if (workspace_bytes < w.total) return fail(FISH_HIP_ERR_ARG, "moe_route: workspace too small");
+    MoeRouting r = moe_routing(workspace, w);
+    r.sel = sel;
+    r.wsel = wsel;
+    const hipError_t e = launch_moe_route(logits, n_tok, n_expert, k, norm, w.item_tokens, r, as_stream(stream));
+    return e == hipSuccess ? 0 : hip_fail(e, "moe_route");
+}
+
+int fish_hip_silu_mul_quantize(const float* g, const float* u, int n_rows, int n_ff, void* act, void* q256_fish,
+                               float* h, void* stream) {
+    if (!g || !u || !act || n_rows <= 0 || n_ff <= 0 || n_ff % 32)
+        return fail(FISH_HIP_ERR_ARG, "silu_mul_quantize: bad arguments");
+    const hipError_t e = launch_quantize(g, n_rows, n_ff, n_ff, act, nullptr, q256_fish, as_stream(stream), u, h);
+    return e == hipSuccess ? 0 : hip_fail(e, "silu_mul_quantize");
 }
 
 int fish_hip_backend_available(void) { return HipBackend::instance().available() ? 1 : 0; }

@@ -111,23 +111,40 @@ __device__ __forceinline__ float group_dot(const Frag& f, const ActFrag& a) {
 // their weight loads in flight together. Lane `sub` covers groups
 // sub, sub + LPR, ... (at most MAXC of them). For one token the lane's
 // activation groups stay in registers for every row of the wavefront.
+// blockIdx.y selects up to NT tokens: consecutive rows of the batch, or one
+// item of an expert work list (TokenMap).
 template <uint32_t T, int NT, int LPR, int MAXC, int RB>
 __global__ __launch_bounds__(256) void gemv_kernel(WeightPtrs W, ActPtrs A, int n_in, int n_out, int n_tok, int rpw,
-                                                   float* __restrict__ y, int ldy) {
+                                                   TokenMap map, float* __restrict__ y, int ldy) {
     constexpr int RPW = 64 / LPR;
     const int lane = threadIdx.x & 63;
     const int sub = lane % LPR;
     const int wave_id = int(blockIdx.x) * 4 + int(threadIdx.x >> 6);
     const int row_base = wave_id * rpw * RPW + lane / LPR;
-    const int t0 = int(blockIdx.y) * NT;
     const int groups = n_in / 32;
+
+    int s0, cnt;
+    size_t wrow0 = 0;  // first weight row of the expert
+    if (map.items) {
+        const int it = int(blockIdx.y);
+        if (it >= *map.n_items) return;
+        wrow0 = size_t(map.items[3 * it]) * size_t(n_out);
+        s0 = map.items[3 * it + 1];
+        cnt = map.items[3 * it + 2];
+    } else {
+        s0 = int(blockIdx.y) * NT;
+        cnt = min(NT, n_tok - s0);
+    }
+    int arow[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) arow[t] = (t < cnt) ? (map.act_row ? map.act_row[s0 + t] : s0 + t) : 0;
 
     ActFrag ac[NT == 1 ? MAXC : 1];
     if constexpr (NT == 1) {
 #pragma unroll
         for (int k = 0; k < MAXC; ++k) {
             const int c = sub + k * LPR;
-            if (c < groups) ac[k] = load_act<T>(A, t0, c, n_in);
+            if (c < groups) ac[k] = load_act<T>(A, arow[0], c, n_in);
         }
     }
 
@@ -139,7 +156,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(WeightPtrs W, ActPtrs A, int 
 #pragma unroll
             for (int k = 0; k < MAXC; ++k) {
                 const int c = sub + k * LPR;
-                if (row < n_out && c < groups) f[rb][k] = load_group<T>(W, row, c, n_in);
+                if (row < n_out && c < groups) f[rb][k] = load_group<T>(W, int(wrow0) + row, c, n_in);
             }
         }
 #pragma unroll
@@ -157,7 +174,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(WeightPtrs W, ActPtrs A, int 
                     } else {
 #pragma unroll
                         for (int t = 0; t < NT; ++t)
-                            if (t0 + t < n_tok) acc[t] += group_dot<T>(f[rb][k], load_act<T>(A, t0 + t, c, n_in));
+                            if (t < cnt) acc[t] += group_dot<T>(f[rb][k], load_act<T>(A, arow[t], c, n_in));
                     }
                 }
             }
@@ -171,7 +188,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(WeightPtrs W, ActPtrs A, int 
             if (sub == 0 && row < n_out) {
 #pragma unroll
                 for (int t = 0; t < NT; ++t)
-                    if (t0 + t < n_tok) y[size_t(t0 + t) * ldy + row] = acc[t];
+                    if (t < cnt) y[size_t(s0 + t) * ldy + row] = acc[t];
             }
         }
     }
@@ -214,64 +231,79 @@ __global__ void block_ints_kernel(WeightPtrs W, ActPtrs A, int n_in, int n_out, 
 }
 
 template <uint32_t T, int NT, int LPR, int MAXC>
-hipError_t gemv_launch(const WeightPtrs& W, const ActPtrs& A, int n_in, int n_out, int n_tok, float* y, int ldy,
-                       hipStream_t s) {
+hipError_t gemv_launch(const WeightPtrs& W, const ActPtrs& A, int n_in, int n_out, int n_tok, const TokenMap& map,
+                       int y_blocks, float* y, int ldy, hipStream_t s) {
     constexpr int RPW = 64 / LPR;
     constexpr int RB = (NT == 1) ? (MAXC <= 2 ? 4 : (MAXC <= 4 ? 2 : 2)) : 1;
     // passes per wavefront: enough rows that ~4096 wavefronts cover the matrix
     const int row_groups = (n_out + RPW - 1) / RPW;
     const int rpw = RB * ((row_groups + RB * 4096 - 1) / (RB * 4096));
     const int waves = (row_groups + rpw - 1) / rpw;
-    const dim3 grid(unsigned((waves + 3) / 4), unsigned((n_tok + NT - 1) / NT));
-    hipLaunchKernelGGL((gemv_kernel<T, NT, LPR, MAXC, RB>), grid, dim3(256), 0, s, W, A, n_in, n_out, n_tok, rpw, y,
-                       ldy);
+    const unsigned gy = map.items ? unsigned(y_blocks) : unsigned((n_tok + NT - 1) / NT);
+    const dim3 grid(unsigned((waves + 3) / 4), gy);
+    hipLaunchKernelGGL((gemv_kernel<T, NT, LPR, MAXC, RB>), grid, dim3(256), 0, s, W, A, n_in, n_out, n_tok, rpw, map,
+                       y, ldy);
     return hipGetLastError();
 }
 
+#define GEMV_ARGS W, A, n_in, n_out, n_tok, map, y_blocks, y, ldy, s
+#define GEMV_PARAMS                                                                                                \
+    const WeightPtrs &W, const ActPtrs &A, int n_in, int n_out, int n_tok, const TokenMap &map, int y_blocks, \
+        float *y, int ldy, hipStream_t s
+
 template <uint32_t T, int NT, int LPR>
-hipError_t gemv_pick_maxc(const WeightPtrs& W, const ActPtrs& A, int n_in, int n_out, int n_tok, float* y, int ldy,
-                          hipStream_t s) {
+hipError_t gemv_pick_maxc(GEMV_PARAMS) {
     const int per_lane = (n_in / 32 + LPR - 1) / LPR;
-    if (per_lane <= 1) return gemv_launch<T, NT, LPR, 1>(W, A, n_in, n_out, n_tok, y, ldy, s);
-    if (per_lane <= 2) return gemv_launch<T, NT, LPR, 2>(W, A, n_in, n_out, n_tok, y, ldy, s);
-    if (per_lane <= 4) return gemv_launch<T, NT, LPR, 4>(W, A, n_in, n_out, n_tok, y, ldy, s);
-    if (per_lane <= 8) return gemv_launch<T, NT, LPR, 8>(W, A, n_in, n_out, n_tok, y, ldy, s);
-    return gemv_launch<T, NT, LPR, 16>(W, A, n_in, n_out, n_tok, y, ldy, s);
+    if (per_lane <= 1) return gemv_launch<T, NT, LPR, 1>(GEMV_ARGS);
+    if (per_lane <= 2) return gemv_launch<T, NT, LPR, 2>(GEMV_ARGS);
+    if (per_lane <= 4) return gemv_launch<T, NT, LPR, 4>(GEMV_ARGS);
+    if (per_lane <= 8) return gemv_launch<T, NT, LPR, 8>(GEMV_ARGS);
+    return gemv_launch<T, NT, LPR, 16>(GEMV_ARGS);
 }
 
 template <uint32_t T, int NT>
-hipError_t gemv_pick_lpr(const WeightPtrs& W, const ActPtrs& A, int n_in, int n_out, int n_tok, float* y, int ldy,
-                         hipStream_t s) {
+hipError_t gemv_pick_lpr(GEMV_PARAMS) {
     const int groups = n_in / 32;
-    if (groups >= 64) return gemv_pick_maxc<T, NT, 64>(W, A, n_in, n_out, n_tok, y, ldy, s);
-    if (groups >= 32) return gemv_pick_maxc<T, NT, 32>(W, A, n_in, n_out, n_tok, y, ldy, s);
-    if (groups >= 16) return gemv_pick_maxc<T, NT, 16>(W, A, n_in, n_out, n_tok, y, ldy, s);
-    return gemv_pick_maxc<T, NT, 8>(W, A, n_in, n_out, n_tok, y, ldy, s);
+    if (groups >= 64) return gemv_pick_maxc<T, NT, 64>(GEMV_ARGS);
+    if (groups >= 32) return gemv_pick_maxc<T, NT, 32>(GEMV_ARGS);
+    if (groups >= 16) return gemv_pick_maxc<T, NT, 16>(GEMV_ARGS);
+    return gemv_pick_maxc<T, NT, 8>(GEMV_ARGS);
 }
 
+// nt: tokens per block (the batch size for plain launches, the item size for
+// expert work lists)
 template <uint32_t T>
-hipError_t gemv_pick_nt(const WeightPtrs& W, const ActPtrs& A, int n_in, int n_out, int n_tok, float* y, int ldy,
-                        hipStream_t s) {
-    if (n_tok <= 1) return gemv_pick_lpr<T, 1>(W, A, n_in, n_out, n_tok, y, ldy, s);
-    if (n_tok <= 2) return gemv_pick_lpr<T, 2>(W, A, n_in, n_out, n_tok, y, ldy, s);
-    if (n_tok <= 4) return gemv_pick_lpr<T, 4>(W, A, n_in, n_out, n_tok, y, ldy, s);
-    return gemv_pick_lpr<T, 8>(W, A, n_in, n_out, n_tok, y, ldy, s);
+hipError_t gemv_pick_nt(int nt, GEMV_PARAMS) {
+    if (nt <= 1) return gemv_pick_lpr<T, 1>(GEMV_ARGS);
+    if (nt <= 2) return gemv_pick_lpr<T, 2>(GEMV_ARGS);
+    if (nt <= 4) return gemv_pick_lpr<T, 4>(GEMV_ARGS);
+    if (nt <= 8) return gemv_pick_lpr<T, 8>(GEMV_ARGS);
+    return gemv_pick_lpr<T, 16>(GEMV_ARGS);
 }
 
 }  // namespace
 
-hipError_t launch_gemv(const void* w, const WeightLayout& WL, const void* act, int n_tok, float* y, int ldy,
-                       hipStream_t s) {
-    const ActLayout AL = act_layout(n_tok, WL.n_in);
+hipError_t launch_gemv(const void* w, const WeightLayout& WL, const void* act, int act_rows, int n_tok, float* y,
+                       int ldy, hipStream_t s, const TokenMap* group, int item_tokens, int max_items) {
+    const ActLayout AL = act_layout(act_rows, WL.n_in);
     if (!WL.total || !AL.total || n_tok <= 0) return hipErrorInvalidValue;
     if (is_kquant(WL.type) && !AL.has256) return hipErrorInvalidValue;
     const WeightPtrs W = weight_ptrs(w, WL);
     const ActPtrs A = act_ptrs(act, AL);
+    TokenMap map{};
+    int nt = n_tok, yb = 0;
+    int n_out = WL.n_out;
+    if (group) {
+        map = *group;
+        nt = item_tokens;
+        yb = max_items;
+        n_out = map.rows_per_expert;
+    }
     switch (WL.type) {
-        case kQ8_0: return gemv_pick_nt<kQ8_0>(W, A, WL.n_in, WL.n_out, n_tok, y, ldy, s);
-        case kQ4_0: return gemv_pick_nt<kQ4_0>(W, A, WL.n_in, WL.n_out, n_tok, y, ldy, s);
-        case kQ4_K: return gemv_pick_nt<kQ4_K>(W, A, WL.n_in, WL.n_out, n_tok, y, ldy, s);
-        case kQ6_K: return gemv_pick_nt<kQ6_K>(W, A, WL.n_in, WL.n_out, n_tok, y, ldy, s);
+        case kQ8_0: return gemv_pick_nt<kQ8_0>(nt, W, A, WL.n_in, n_out, n_tok, map, yb, y, ldy, s);
+        case kQ4_0: return gemv_pick_nt<kQ4_0>(nt, W, A, WL.n_in, n_out, n_tok, map, yb, y, ldy, s);
+        case kQ4_K: return gemv_pick_nt<kQ4_K>(nt, W, A, WL.n_in, n_out, n_tok, map, yb, y, ldy, s);
+        case kQ6_K: return gemv_pick_nt<kQ6_K>(nt, W, A, WL.n_in, n_out, n_tok, map, yb, y, ldy, s);
         default: return hipErrorInvalidValue;
     }
 }

@@ -10,15 +10,54 @@ namespace fishhip {
 
 // f32 x[n_tok][ldx] -> device activation buffer `act` (act_layout(n_tok, n_in)).
 // aos32 / aos256 (nullable) receive FISH's Q8Act / Q8ActK bytes as well.
+// With u != nullptr the quantized values are silu(x) * u (FFN gate and up,
+// ops.cpp:25-30 and model.cpp:1504-1508), optionally also written to h_out.
 hipError_t launch_quantize(const float* x, int n_tok, int n_in, int ldx, void* act, void* aos32, void* aos256,
-                           hipStream_t stream);
+                           hipStream_t stream, const float* u = nullptr, float* h_out = nullptr);
+
+// Expert routing from router logits (model.cpp:1528-1547) and grouping of
+// the chosen (token, expert) pairs by expert, tokens ascending
+// (model.cpp:1551-1561). Single workgroup.
+struct MoeRouting {
+    int* sel;       // [n_tok][k] chosen experts, by probability
+    float* wsel;    // [n_tok][k] their weights (renormalised when norm)
+    int* counts;    // [n_expert]
+    int* offsets;   // [n_expert + 1] first slot of each expert
+    int* slot_tok;  // [n_tok * k] token of each slot
+    int* tok_slot;  // [n_tok][k] slot of each (token, choice)
+    int* items;     // [max_items][3] work list: expert, first slot, count
+    int* n_items;   // [1]
+};
+hipError_t launch_moe_route(const float* logits, int n_tok, int n_expert, int k, int norm, int item_tokens,
+                            const MoeRouting& r, hipStream_t stream);
+
+// out[t][i] = sum over the token's experts in ascending expert order of
+// w * down[slot][i] (model.cpp:1574-1579).
+hipError_t launch_moe_combine(const float* down, const MoeRouting& r, int n_tok, int k, int n_embd, float* out,
+                              hipStream_t stream);
 
 // GGUF rows (device bytes) -> repacked device layout (weight_layout()).
 hipError_t launch_repack(uint32_t type, const void* gguf, int n_in, int n_out, void* dst, hipStream_t stream);
 
-// Few-token matmul: y[t * ldy + i] for t < n_tok, i < n_out.
-hipError_t launch_gemv(const void* w, const WeightLayout& L, const void* act, int n_tok, float* y, int ldy,
-                       hipStream_t stream);
+// Token mapping of a few-token matmul launch. Plain launches (items ==
+// nullptr) take tokens 0..n_tok-1 of the activation buffer and write the same
+// rows of y. Grouped launches walk a device work list of items
+// {expert, first slot, count}: weight rows expert * rows_per_expert + i,
+// activation rows act_row[slot] (or the slot itself when act_row is
+// nullptr), output rows `slot`.
+struct TokenMap {
+    const int* items;
+    const int* n_items;
+    const int* act_row;
+    int rows_per_expert;
+};
+
+// Few-token matmul: y[t * ldy + i] for t < n_tok, i < n_out. `act` holds
+// act_rows rows. With `group`, blocks walk at most max_items work-list items
+// of up to item_tokens tokens each.
+hipError_t launch_gemv(const void* w, const WeightLayout& L, const void* act, int act_rows, int n_tok, float* y,
+                       int ldy, hipStream_t stream, const TokenMap* group = nullptr, int item_tokens = 0,
+                       int max_items = 0);
 
 // Many-token matmul on int8 MFMA (K-quants).
 hipError_t launch_gemm(const void* w, const WeightLayout& L, const void* act, int n_tok, float* y, int ldy,

@@ -52,8 +52,16 @@ struct QuantOut {
     uint8_t* aos256;  // optional FISH Q8ActK rows (276 B blocks)
 };
 
+// silu(g) * u in FISH's float order: g / (1 + exp(-g)), then times u
+// (silu_inplace, ops.cpp:25-30; model.cpp:1504-1508).
+__device__ __forceinline__ float silu_mul(float g, float u) {
+    const float s = g / __fadd_rn(1.0f, expf(-g));
+    return __fmul_rn(s, u);
+}
+
 __global__ __launch_bounds__(256) void quantize_kernel(const float* __restrict__ x, int n_tok, int n_in, int ldx,
-                                                       QuantOut o) {
+                                                       QuantOut o, const float* __restrict__ u,
+                                                       float* __restrict__ h_out) {
     const int lane = threadIdx.x & 63;
     const int chunks = (n_in + 255) / 256;
     const long wave = long(blockIdx.x) * 4 + (threadIdx.x >> 6);
@@ -62,7 +70,14 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float* __restrict__
     const int k0 = c * 256 + lane * 4;
     const bool active = k0 < n_in;  // n_in % 32 == 0: whole 8-lane groups switch together
     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (active) v = *reinterpret_cast<const float4*>(x + size_t(t) * ldx + k0);
+    if (active) {
+        v = *reinterpret_cast<const float4*>(x + size_t(t) * ldx + k0);
+        if (u) {
+            const float4 w = *reinterpret_cast<const float4*>(u + size_t(t) * ldx + k0);
+            v = make_float4(silu_mul(v.x, w.x), silu_mul(v.y, w.y), silu_mul(v.z, w.z), silu_mul(v.w, w.w));
+            if (h_out) *reinterpret_cast<float4*>(h_out + size_t(t) * n_in + k0) = v;
+        }
+    }
     const float a = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
 
     // ---- 32-value blocks
@@ -125,7 +140,7 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float* __restrict__
 }  // namespace
 
 hipError_t launch_quantize(const float* x, int n_tok, int n_in, int ldx, void* act, void* aos32, void* aos256,
-                           hipStream_t stream) {
+                           hipStream_t stream, const float* u, float* h_out) {
     const ActLayout L = act_layout(n_tok, n_in);
     if (!L.total) return hipErrorInvalidValue;
     uint8_t* b = static_cast<uint8_t*>(act);
@@ -141,7 +156,7 @@ hipError_t launch_quantize(const float* x, int n_tok, int n_in, int ldx, void* a
     o.aos256 = L.has256 ? static_cast<uint8_t*>(aos256) : nullptr;
     const long waves = long(n_tok) * ((n_in + 255) / 256);
     const unsigned blocks = unsigned((waves + 3) / 4);
-    hipLaunchKernelGGL(quantize_kernel, dim3(blocks), dim3(256), 0, stream, x, n_tok, n_in, ldx, o);
+    hipLaunchKernelGGL(quantize_kernel, dim3(blocks), dim3(256), 0, stream, x, n_tok, n_in, ldx, o, u, h_out);
     return hipGetLastError();
 }
 

@@ -92,6 +92,39 @@ FISH_HIP_API int fish_hip_matmul(uint32_t type, const void* w, const void* act, 
 FISH_HIP_API int fish_hip_block_ints(uint32_t type, const void* w, const void* act, int n_in, int n_out,
                                      int32_t* out, void* stream);
 
+/* ---------------------------------------------------------------- expert FFN (device pointers) */
+
+/* Device bytes of the workspace fish_hip_moe_ffn needs for these sizes
+ * (0 when unsupported: n_expert <= 256, k <= 16, widths multiples of 32). */
+FISH_HIP_API uint64_t fish_hip_moe_workspace_bytes(int n_tok, int n_embd, int n_ff, int n_expert, int k);
+
+/* LlamaModel::moe_ffn (model.cpp:1523-1580) from given router logits:
+ * softmax over n_expert, top-k, renormalised when norm (expert_weights_norm,
+ * model.cpp:461-462); each expert's tokens as one batch through gate, up,
+ * silu(gate) * up, down; out[t] = sum of w * down in ascending expert order.
+ * x f32 [n_tok][n_embd], logits f32 [n_tok][n_expert], out f32 [n_tok][n_embd];
+ * w_gate / w_up: repacked n_expert * n_ff rows of n_embd (fish_hip_repack of
+ * the 3-D tensor, experts contiguous as expert_ptr, model.cpp:66-69);
+ * w_down: n_expert * n_embd rows of n_ff. This is a new device hook: FISH's
+ * own backends never receive expert matmuls (model.cpp:1466-1470). */
+FISH_HIP_API int fish_hip_moe_ffn(const float* x, const float* logits, int n_tok, int n_embd, int n_ff, int n_expert,
+                                  int k, int norm, uint32_t t_gate, const void* w_gate, uint32_t t_up,
+                                  const void* w_up, uint32_t t_down, const void* w_down, void* workspace,
+                                  uint64_t workspace_bytes, float* out, void* stream);
+
+/* The routing step alone (model.cpp:1528-1547): sel int32 [n_tok][k] and
+ * wsel f32 [n_tok][k] in descending probability; workspace as for
+ * fish_hip_moe_workspace_bytes(n_tok, 32, 32, n_expert, k). */
+FISH_HIP_API int fish_hip_moe_route(const float* logits, int n_tok, int n_expert, int k, int norm, void* workspace,
+                                    uint64_t workspace_bytes, int* sel, float* wsel, void* stream);
+
+/* silu(g) * u (silu_inplace, ops.cpp:25-30; model.cpp:1504-1508) quantized
+ * like ActBatch::quantize into act (fish_hip_act_bytes(n_rows, n_ff));
+ * q256_fish and h (f32 [n_rows][n_ff]) are optional copies of FISH's Q8ActK
+ * bytes and of the f32 values that were quantized. */
+FISH_HIP_API int fish_hip_silu_mul_quantize(const float* g, const float* u, int n_rows, int n_ff, void* act,
+                                            void* q256_fish, float* h, void* stream);
+
 /* ---------------------------------------------------------------- backend (host pointers, synchronous) */
 
 /* gpu_backend() != NULL (backend.h:191): a gfx950 device is usable. */

@@ -1,0 +1,117 @@
+"""Expert-routed FFN on the GPU (fish_hip_moe_*) against the oracle and the golden layer.
+
+Routing (selected experts) must match exactly and weights within 1e-6; the
+silu*up requantization is checked per kernel (the GPU's own f32 h fed to the
+CPU quantizer must give the same bytes); layer outputs within 1e-4 * max|out|.
+"""
+import numpy as np
+import pytest
+
+import imurun_amd as fh
+from imurun_amd.synth import normal
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+
+
+@pytest.fixture(scope="module")
+def torch_dev():
+    import torch
+    assert torch.cuda.is_available(), "GPU tests need a ROCm device"
+    fh.load()
+    return torch, torch.device("cuda:0")
+
+
+def dev(torch_dev, a, dtype=None):
+    torch, d = torch_dev
+    return torch.from_numpy(np.ascontiguousarray(a)).to(d)
+
+
+def check_close(got, want, what):
+    err = float(np.max(np.abs(got - want)))
+    scale = float(np.max(np.abs(want)))
+    assert err <= TOL * scale, f"{what}: max err {err:.3e} vs {TOL} * {scale:.3e}"
+
+
+@pytest.mark.parametrize("n_tok,n_expert,k", [(1, 8, 2), (64, 8, 2), (256, 128, 8), (7, 16, 4)])
+def test_routing_matches_oracle(torch_dev, oracle, n_tok, n_expert, k):
+    logits = normal(40 + n_tok + n_expert, (n_tok, n_expert))
+    sel, wsel = fh.moe_route(dev(torch_dev, logits), k, True)
+    want_sel, want_w = oracle.route(logits, k, True)
+    assert np.array_equal(sel.cpu().numpy(), want_sel)
+    assert np.allclose(wsel.cpu().numpy(), want_w, rtol=0, atol=1e-6)
+    sel2, wsel2 = fh.moe_route(dev(torch_dev, logits), k, False)
+    _, want_w2 = oracle.route(logits, k, False)
+    assert np.array_equal(sel2.cpu().numpy(), want_sel)
+    assert np.allclose(wsel2.cpu().numpy(), want_w2, rtol=0, atol=1e-6)
+
+
+@pytest.mark.parametrize("n_rows,n_ff", [(20, 768), (3, 14336), (64, 256)])
+def test_silu_mul_quantize_bit_exact_on_own_values(torch_dev, oracle, n_rows, n_ff):
+    g = normal(51 + n_ff, (n_rows, n_ff)) * np.float32(2.0)
+    u = normal(52 + n_ff, (n_rows, n_ff))
+    _, q256, h = fh.silu_mul_quantize(dev(torch_dev, g), dev(torch_dev, u))
+    h = h.cpu().numpy()
+    # the values quantized are silu(g) * u to within float rounding of exp
+    want = (g / (np.float32(1.0) + np.exp(-g.astype(np.float64)).astype(np.float32))) * u
+    assert np.max(np.abs(h - want) / (np.abs(want) + 1e-30)) < 1e-5
+    # and their int8 codes / scales / sums are exactly FISH's for those values
+    assert np.array_equal(q256.cpu().numpy(), oracle.quantize_acts_k(h))
+
+
+def repacked_experts(torch_dev, oracle, t, n_expert, rows, n_in, seed, distinct=None):
+    """Expert tensor [n_expert][rows][n_in] packed like FISH (expert slices contiguous), repacked on device.
+    With `distinct`, only that many experts are generated and the rest repeat them."""
+    d = distinct or n_expert
+    packed = np.concatenate([oracle.quantize_rows(t, normal(seed + e, (rows, n_in), 0.02)) for e in range(d)])
+    if d < n_expert:
+        packed = np.tile(packed, n_expert // d)
+    return packed, fh.repack(t, dev(torch_dev, packed), n_in, n_expert * rows)
+
+
+def run_case(torch_dev, oracle, n_tok, n_embd, n_ff, n_expert, k, types, seed, distinct=None):
+    tg, tu, td = types
+    pg, wg = repacked_experts(torch_dev, oracle, tg, n_expert, n_ff, n_embd, seed, distinct)
+    pu, wu = repacked_experts(torch_dev, oracle, tu, n_expert, n_ff, n_embd, seed + 100, distinct)
+    pd, wd = repacked_experts(torch_dev, oracle, td, n_expert, n_embd, n_ff, seed + 200, distinct)
+    x = normal(seed + 300, (n_tok, n_embd))
+    logits = normal(seed + 301, (n_tok, n_expert))
+    out = fh.moe_ffn(dev(torch_dev, x), dev(torch_dev, logits), n_ff, n_expert, k, True, tg, wg, tu, wu, td, wd)
+    want = oracle.moe_ffn(x, logits, n_embd, n_ff, n_expert, k, True, tg, pg, tu, pu, td, pd)
+    check_close(out.cpu().numpy(), want, f"moe M={n_tok} E={n_embd} F={n_ff} NE={n_expert} k={k}")
+
+
+def test_moe_matches_reference_golden(torch_dev, golden):
+    g = golden("moe")
+    E, F, NE, K = int(g["E"]), int(g["F"]), int(g["NE"]), int(g["K"])
+    wg = fh.repack(fh.Q4_K, dev(torch_dev, g["gate"]), E, NE * F)
+    wu = fh.repack(fh.Q4_K, dev(torch_dev, g["up"]), E, NE * F)
+    wd = fh.repack(fh.Q6_K, dev(torch_dev, g["down"]), F, NE * E)
+    out = fh.moe_ffn(dev(torch_dev, g["x"]), dev(torch_dev, g["logits"]), F, NE, K, True, fh.Q4_K, wg, fh.Q4_K, wu,
+                     fh.Q6_K, wd)
+    check_close(out.cpu().numpy(), g["out"], "golden MoE layer")
+
+
+@pytest.mark.parametrize("n_tok", [1, 5, 20, 64])
+def test_moe_mixtral_like(torch_dev, oracle, n_tok):
+    run_case(torch_dev, oracle, n_tok, 512, 1024, 8, 2, (fh.Q4_K, fh.Q4_K, fh.Q4_K), 1000 + n_tok)
+
+
+@pytest.mark.parametrize("n_tok", [1, 33, 96])
+def test_moe_qwen3_like(torch_dev, oracle, n_tok):
+    run_case(torch_dev, oracle, n_tok, 512, 256, 32, 8, (fh.Q4_K, fh.Q4_K, fh.Q6_K), 2000 + n_tok)
+
+
+def test_moe_mixed_types(torch_dev, oracle):
+    run_case(torch_dev, oracle, 9, 256, 512, 4, 2, (fh.Q8_0, fh.Q4_0, fh.Q6_K), 3000)
+
+
+def test_moe_mixtral_full_size_decode(torch_dev, oracle):
+    """Mixtral-8x7B expert shapes at M=1 (one distinct expert, replicated)."""
+    run_case(torch_dev, oracle, 1, 4096, 14336, 8, 2, (fh.Q4_K, fh.Q4_K, fh.Q4_K), 4000, distinct=1)
+
+
+def test_moe_qwen3_full_size(torch_dev, oracle):
+    """Qwen3-30B-A3B expert shapes, 128 experts (8 distinct, repeated), M=24."""
+    run_case(torch_dev, oracle, 24, 2048, 768, 128, 8, (fh.Q4_K, fh.Q4_K, fh.Q6_K), 5000, distinct=8)
