@@ -62,8 +62,8 @@ struct MoeWork {
 
 MoeWork moe_work(int n_tok, int n_embd, int n_ff, int n_expert, int k) {
     MoeWork w;
-    if (n_tok <= 0 || n_embd <= 0 || n_ff <= 0 || n_expert <= 0 || k <= 0 || k > n_expert || k > 16 ||
-        n_expert > 256 || n_embd % 32 || n_ff % 32)
+    if (n_tok <= 0 || n_tok > 2048 || n_embd <= 0 || n_ff <= 0 || n_expert <= 0 || k <= 0 || k > n_expert ||
+        k > 16 || n_expert > 256 || n_embd % 32 || n_ff % 32)
         return w;
     w.slots = n_tok * k;
     const int avg = (w.slots + n_expert - 1) / n_expert;

@@ -95,7 +95,8 @@ FISH_HIP_API int fish_hip_block_ints(uint32_t type, const void* w, const void* a
 /* ---------------------------------------------------------------- expert FFN (device pointers) */
 
 /* Device bytes of the workspace fish_hip_moe_ffn needs for these sizes
- * (0 when unsupported: n_expert <= 256, k <= 16, widths multiples of 32). */
+ * (0 when unsupported: n_tok <= 2048, n_expert <= 256, k <= 16, widths
+ * multiples of 32). */
 FISH_HIP_API uint64_t fish_hip_moe_workspace_bytes(int n_tok, int n_embd, int n_ff, int n_expert, int k);
 
 /* LlamaModel::moe_ffn (model.cpp:1523-1580) from given router logits:
