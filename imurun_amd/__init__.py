@@ -59,6 +59,7 @@ def load() -> ctypes.CDLL:
         "fish_hip_block_ints": ([ctypes.c_uint32, _P, _P, ctypes.c_int, ctypes.c_int, _P, _P], ctypes.c_int),
         "fish_hip_quantize_rows": ([ctypes.c_uint32, _P, _P, ctypes.c_int, ctypes.c_int, ctypes.c_int], ctypes.c_int),
         "fish_hip_moe_workspace_bytes": ([ctypes.c_int] * 5, ctypes.c_uint64),
+        "fish_hip_moe_workspace_layout": ([ctypes.c_int] * 5 + [ctypes.POINTER(ctypes.c_uint64)], ctypes.c_int),
         "fish_hip_moe_ffn": ([_P, _P, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                               ctypes.c_int, ctypes.c_uint32, _P, ctypes.c_uint32, _P, ctypes.c_uint32, _P, _P,
                               ctypes.c_uint64, _P, _P], ctypes.c_int),
@@ -209,6 +210,27 @@ def moe_ffn(x, logits, n_ff: int, n_expert: int, k: int, norm: bool, tg: int, wg
     _check(load().fish_hip_moe_ffn(x.data_ptr(), logits.data_ptr(), n_tok, n_embd, n_ff, n_expert, k, int(norm), tg,
                                    wg.data_ptr(), tu, wu.data_ptr(), td, wd.data_ptr(), workspace.data_ptr(),
                                    workspace.numel(), out.data_ptr(), _stream(stream)), "moe_ffn")
+    return out
+
+
+MOE_PARTS = ("sel", "wsel", "tok_slot", "slot_tok", "gate", "up", "down")
+
+
+def moe_parts(workspace, n_tok: int, n_embd: int, n_ff: int, n_expert: int, k: int) -> dict:
+    """Views of the intermediate buffers a moe_ffn call left in `workspace`."""
+    import torch
+    offs = (ctypes.c_uint64 * len(MOE_PARTS))()
+    _check(load().fish_hip_moe_workspace_layout(n_tok, n_embd, n_ff, n_expert, k, offs), "moe_workspace_layout")
+    slots = n_tok * k
+    shapes = {"sel": ((n_tok, k), torch.int32), "wsel": ((n_tok, k), torch.float32),
+              "tok_slot": ((n_tok, k), torch.int32), "slot_tok": ((slots,), torch.int32),
+              "gate": ((slots, n_ff), torch.float32), "up": ((slots, n_ff), torch.float32),
+              "down": ((slots, n_embd), torch.float32)}
+    out = {}
+    for name, off in zip(MOE_PARTS, offs):
+        shape, dt = shapes[name]
+        n = int(np.prod(shape)) * 4
+        out[name] = workspace[int(off):int(off) + n].view(dt).view(shape)
     return out
 
 

@@ -41,12 +41,17 @@ hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
 
 bool type_ok(uint32_t type) { return type == kQ8_0 || type == kQ4_0 || type == kQ4_K || type == kQ6_K; }
 
-// Matmul dispatch on an already quantized activation buffer: few tokens ->
-// the bandwidth-bound GEMV; many tokens of a K-quant -> the MFMA GEMM.
-constexpr int kGemvMaxTok = 8;
+// Matmul dispatch on an already quantized activation buffer: up to
+// kGemvMaxTok tokens -> the bandwidth-bound GEMV; up to kBatchMaxTok tokens
+// (any count for Q8_0 / Q4_0) -> the 16x16 MFMA batch kernel; more tokens of a
+// K-quant -> the large-tile MFMA GEMM.
+constexpr int kGemvMaxTok = 4;
+constexpr int kBatchMaxTok = 64;
 
 hipError_t dispatch_matmul(const void* w, const WeightLayout& L, const void* act, int n_tok, float* y, int ldy,
                            hipStream_t s) {
+    if (n_tok > kGemvMaxTok && batch_mfma_supported(L) && (n_tok <= kBatchMaxTok || !is_kquant(L.type)))
+        return launch_batch_mfma(w, L, act, n_tok, n_tok, y, ldy, s);
     if (n_tok > kGemvMaxTok && is_kquant(L.type)) return launch_gemm(w, L, act, n_tok, y, ldy, s);
     return launch_gemv(w, L, act, n_tok, n_tok, y, ldy, s);
 }
@@ -56,6 +61,7 @@ hipError_t dispatch_matmul(const void* w, const WeightLayout& L, const void* act
 // (token, expert) pair, grouped by expert).
 struct MoeWork {
     int slots = 0, item_tokens = 1, max_items = 0;
+    bool mfma = false;  // expert products on the MFMA batch kernel (else the GEMV)
     size_t sel = 0, wsel = 0, counts = 0, offsets = 0, slot_tok = 0, tok_slot = 0, items = 0, n_items = 0;
     size_t act_x = 0, g = 0, u = 0, act_h = 0, dn = 0, total = 0;
 };
@@ -66,8 +72,13 @@ MoeWork moe_work(int n_tok, int n_embd, int n_ff, int n_expert, int k) {
         k > 16 || n_expert > 256 || n_embd % 32 || n_ff % 32)
         return w;
     w.slots = n_tok * k;
+    // Work-list items: one token per item at decode sizes (every expert
+    // streams its rows once anyway), else 16- or 32-token MFMA items sized to
+    // the mean tokens per expert.
     const int avg = (w.slots + n_expert - 1) / n_expert;
-    w.item_tokens = avg <= 1 ? 1 : (avg <= 2 ? 2 : (avg <= 4 ? 4 : (avg <= 8 ? 8 : 16)));
+    w.mfma = avg > 1 && n_embd % 256 == 0 && n_ff % 256 == 0;
+    if (w.mfma) w.item_tokens = avg <= 12 ? 16 : kBatchItemTokens;
+    else w.item_tokens = avg <= 1 ? 1 : (avg <= 2 ? 2 : (avg <= 4 ? 4 : (avg <= 8 ? 8 : 16)));
     w.max_items = std::min(n_expert, w.slots) + w.slots / w.item_tokens + 1;
     const ActLayout ax = act_layout(n_tok, n_embd), ah = act_layout(w.slots, n_ff);
     size_t off = 0;
@@ -123,15 +134,17 @@ hipError_t moe_ffn(const float* x, const float* logits, int n_tok, int n_embd, i
     float* dn = reinterpret_cast<float*>(b + w.dn);
     hipError_t e = launch_moe_route(logits, n_tok, n_expert, k, norm, w.item_tokens, r, s);
     if (e == hipSuccess) e = launch_quantize(x, n_tok, n_embd, n_embd, b + w.act_x, nullptr, nullptr, s);
-    TokenMap up_map{r.items, r.n_items, r.slot_tok, n_ff};
-    if (e == hipSuccess)
-        e = launch_gemv(wg, Lg, b + w.act_x, n_tok, w.slots, g, n_ff, s, &up_map, w.item_tokens, w.max_items);
-    if (e == hipSuccess)
-        e = launch_gemv(wu, Lu, b + w.act_x, n_tok, w.slots, u, n_ff, s, &up_map, w.item_tokens, w.max_items);
+    auto grouped = [&](const void* wt, const WeightLayout& L, const void* act, int act_rows, float* y, int ldy,
+                       const TokenMap& map) {
+        if (w.mfma) return launch_batch_mfma(wt, L, act, act_rows, w.slots, y, ldy, s, &map, w.item_tokens, w.max_items);
+        return launch_gemv(wt, L, act, act_rows, w.slots, y, ldy, s, &map, w.item_tokens, w.max_items);
+    };
+    const TokenMap up_map{r.items, r.n_items, r.slot_tok, n_ff};
+    if (e == hipSuccess) e = grouped(wg, Lg, b + w.act_x, n_tok, g, n_ff, up_map);
+    if (e == hipSuccess) e = grouped(wu, Lu, b + w.act_x, n_tok, u, n_ff, up_map);
     if (e == hipSuccess) e = launch_quantize(g, w.slots, n_ff, n_ff, b + w.act_h, nullptr, nullptr, s, u, nullptr);
-    TokenMap down_map{r.items, r.n_items, nullptr, n_embd};
-    if (e == hipSuccess)
-        e = launch_gemv(wd, Ld, b + w.act_h, w.slots, w.slots, dn, n_embd, s, &down_map, w.item_tokens, w.max_items);
+    const TokenMap down_map{r.items, r.n_items, nullptr, n_embd};
+    if (e == hipSuccess) e = grouped(wd, Ld, b + w.act_h, w.slots, dn, n_embd, down_map);
     if (e == hipSuccess) e = launch_moe_combine(dn, r, n_tok, k, n_embd, out, s);
     return e;
 }
@@ -366,6 +379,14 @@ int fish_hip_moe_ffn(const float* x, const float* logits, int n_tok, int n_embd,
     const hipError_t e = moe_ffn(x, logits, n_tok, n_embd, n_ff, n_expert, k, norm, t_gate, w_gate, t_up, w_up,
                                  t_down, w_down, workspace, w, out, as_stream(stream));
     return e == hipSuccess ? 0 : hip_fail(e, "moe_ffn");
+}
+
+int fish_hip_moe_workspace_layout(int n_tok, int n_embd, int n_ff, int n_expert, int k, uint64_t* offsets) {
+    const MoeWork w = moe_work(n_tok, n_embd, n_ff, n_expert, k);
+    if (!w.total || !offsets) return fail(FISH_HIP_ERR_ARG, "moe_workspace_layout: bad arguments");
+    const size_t parts[FISH_HIP_MOE_PARTS] = {w.sel, w.wsel, w.tok_slot, w.slot_tok, w.g, w.u, w.dn};
+    for (int i = 0; i < FISH_HIP_MOE_PARTS; ++i) offsets[i] = parts[i];
+    return 0;
 }
 
 int fish_hip_moe_route(const float* logits, int n_tok, int n_expert, int k, int norm, void* workspace,

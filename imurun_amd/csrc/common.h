@@ -18,8 +18,13 @@
 //   q32  [M][K] int8   d32 [M][K/32] f32    s32 [M][K/32] int32   (Q8Act)
 //   q256 [M][K] int8   d256 [M][K/256] f32  s16 [M][K/16] int16   (Q8ActK)
 //   bsm  [M][K/256][16] int8: bytes 0..7 = bsum_g >> 6, 8..15 = bsum_g & 63
+//   m32, m256 [M][K] int8: the q32 / q256 codes in MFMA operand order
 // (bsum_g = the Q8ActK per-32 sum; s16 holds per-16 sums, two of which make
 // a bsum). The 256 planes exist only when K % 256 == 0.
+// MFMA operand order: within each 256-element unit (8 groups of 32), byte
+// q*64 + g*8 + i holds element 4q+i (i < 4) or 16+4q+(i-4) (i >= 4) of group
+// g, q < 4: the eight codes that lane quarter q of a 16x16x32 int8 MFMA
+// takes for group g, which matches one dword of a 16-byte nibble chunk.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -92,7 +97,7 @@ inline bool is_kquant(uint32_t type) { return type == kQ4_K || type == kQ6_K; }
 
 struct ActLayout {
     int n_tok = 0, n_in = 0;
-    size_t q32 = 0, d32 = 0, s32 = 0, q256 = 0, d256 = 0, s16 = 0, bsm = 0, total = 0;
+    size_t q32 = 0, d32 = 0, s32 = 0, q256 = 0, d256 = 0, s16 = 0, bsm = 0, m32 = 0, m256 = 0, total = 0;
     bool has256 = false;
 };
 
@@ -112,6 +117,8 @@ inline ActLayout act_layout(int n_tok, int n_in) {
         L.d256 = off; off = align256(off + M * (K / 256) * 4);
         L.s16 = off;  off = align256(off + M * (K / 16) * 2);
         L.bsm = off;  off = align256(off + M * (K / 256) * 16);
+        L.m32 = off;  off = align256(off + M * K);
+        L.m256 = off; off = align256(off + M * K);
     }
     L.total = off;
     return L;
@@ -126,6 +133,8 @@ struct ActPtrs {
     const float* d256;
     const int16_t* s16;
     const int8_t* bsm;
+    const int8_t* m32;
+    const int8_t* m256;
 };
 
 inline ActPtrs act_ptrs(const void* base, const ActLayout& L) {
@@ -138,6 +147,8 @@ inline ActPtrs act_ptrs(const void* base, const ActLayout& L) {
     p.d256 = L.has256 ? reinterpret_cast<const float*>(b + L.d256) : nullptr;
     p.s16 = L.has256 ? reinterpret_cast<const int16_t*>(b + L.s16) : nullptr;
     p.bsm = L.has256 ? reinterpret_cast<const int8_t*>(b + L.bsm) : nullptr;
+    p.m32 = L.has256 ? reinterpret_cast<const int8_t*>(b + L.m32) : nullptr;
+    p.m256 = L.has256 ? reinterpret_cast<const int8_t*>(b + L.m256) : nullptr;
     return p;
 }
 

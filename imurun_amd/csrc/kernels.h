@@ -59,6 +59,15 @@ hipError_t launch_gemv(const void* w, const WeightLayout& L, const void* act, in
                        int ldy, hipStream_t stream, const TokenMap* group = nullptr, int item_tokens = 0,
                        int max_items = 0);
 
+// Few-token matmul on int8 MFMA (16x16x32 tiles), same token mapping as
+// launch_gemv; work-list items of up to kBatchItemTokens tokens. Needs
+// n_in % 256 == 0.
+constexpr int kBatchItemTokens = 32;
+bool batch_mfma_supported(const WeightLayout& L);
+hipError_t launch_batch_mfma(const void* w, const WeightLayout& L, const void* act, int act_rows, int n_tok, float* y,
+                             int ldy, hipStream_t stream, const TokenMap* group = nullptr, int item_tokens = 0,
+                             int max_items = 0);
+
 // Many-token matmul on int8 MFMA (K-quants).
 hipError_t launch_gemm(const void* w, const WeightLayout& L, const void* act, int n_tok, float* y, int ldy,
                        hipStream_t stream);

@@ -147,9 +147,12 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
     }
     float acc = 0.0f;
     for (int q = 0; q < k; ++q) {
+        // w * down is rounded before the add: this file is built without
+        // multiply-add contraction
         const int j = order[q];
         const int slot = r.tok_slot[t * k + j];
-        acc = __fadd_rn(acc, __fmul_rn(r.wsel[t * k + j], down[size_t(slot) * n_embd + i]));
+        const float p = r.wsel[t * k + j] * down[size_t(slot) * n_embd + i];
+        acc = acc + p;
     }
     out[gid] = acc;
 }

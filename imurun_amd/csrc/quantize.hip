@@ -48,6 +48,7 @@ __device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
 struct QuantOut {
     int8_t* q32; float* d32; int32_t* s32;
     int8_t* q256; float* d256; int16_t* s16; int8_t* bsm;
+    int8_t* m32; int8_t* m256;  // MFMA operand order (rows of whole 256-element units)
     uint8_t* aos32;   // optional FISH Q8Act rows (40 B blocks)
     uint8_t* aos256;  // optional FISH Q8ActK rows (276 B blocks)
 };
@@ -57,6 +58,15 @@ struct QuantOut {
 __device__ __forceinline__ float silu_mul(float g, float u) {
     const float s = g / __fadd_rn(1.0f, expf(-g));
     return __fmul_rn(s, u);
+}
+
+// Byte offset, inside its 256-element unit, of the dword that holds this
+// lane's four codes in MFMA operand order: lane L of the unit holds elements
+// 4L..4L+3, i.e. dword L % 8 of group L / 8; dwords 0..3 of a group go to
+// quarter q = L % 8 (codes 0..3), dwords 4..7 to quarter L % 8 - 4 (codes 4..7).
+__device__ __forceinline__ int mfma_offset(int lane) {
+    const int g = lane >> 3, w = lane & 7;
+    return (w & 3) * 64 + g * 8 + (w >> 2) * 4;
 }
 
 __global__ __launch_bounds__(256) void quantize_kernel(const float* __restrict__ x, int n_tok, int n_in, int ldx,
@@ -90,6 +100,8 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float* __restrict__
         if (active) {
             const uint32_t packed = pack4(q0, q1, q2, q3);
             *reinterpret_cast<uint32_t*>(o.q32 + size_t(t) * n_in + k0) = packed;
+            if (o.m32)
+                *reinterpret_cast<uint32_t*>(o.m32 + size_t(t) * n_in + size_t(c) * 256 + mfma_offset(lane)) = packed;
             const size_t blk = size_t(t) * (n_in / 32) + k0 / 32;
             if ((lane & 7) == 0) {
                 o.d32[blk] = d;
@@ -120,6 +132,7 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float* __restrict__
         const int g32 = g16 + __shfl_xor(g16, 4);
         const uint32_t packed = pack4(q0, q1, q2, q3);
         *reinterpret_cast<uint32_t*>(o.q256 + size_t(t) * n_in + k0) = packed;
+        *reinterpret_cast<uint32_t*>(o.m256 + size_t(t) * n_in + size_t(c) * 256 + mfma_offset(lane)) = packed;
         const size_t sb = size_t(t) * (n_in / 256) + c;
         if (lane == 0) o.d256[sb] = d;
         if ((lane & 3) == 0) o.s16[size_t(t) * (n_in / 16) + k0 / 16] = int16_t(g16);
@@ -152,6 +165,8 @@ hipError_t launch_quantize(const float* x, int n_tok, int n_in, int ldx, void* a
     o.d256 = L.has256 ? reinterpret_cast<float*>(b + L.d256) : nullptr;
     o.s16 = L.has256 ? reinterpret_cast<int16_t*>(b + L.s16) : nullptr;
     o.bsm = L.has256 ? reinterpret_cast<int8_t*>(b + L.bsm) : nullptr;
+    o.m32 = L.has256 ? reinterpret_cast<int8_t*>(b + L.m32) : nullptr;
+    o.m256 = L.has256 ? reinterpret_cast<int8_t*>(b + L.m256) : nullptr;
     o.aos32 = static_cast<uint8_t*>(aos32);
     o.aos256 = L.has256 ? static_cast<uint8_t*>(aos256) : nullptr;
     const long waves = long(n_tok) * ((n_in + 255) / 256);

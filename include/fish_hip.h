@@ -113,6 +113,20 @@ FISH_HIP_API int fish_hip_moe_ffn(const float* x, const float* logits, int n_tok
                                   const void* w_up, uint32_t t_down, const void* w_down, void* workspace,
                                   uint64_t workspace_bytes, float* out, void* stream);
 
+/* Byte offsets, inside the fish_hip_moe_ffn workspace for these sizes, of
+ * the intermediate buffers a call leaves behind, in this order:
+ *   0 sel int32 [n_tok][k]      1 wsel f32 [n_tok][k]
+ *   2 tok_slot int32 [n_tok][k] 3 slot_tok int32 [n_tok * k]
+ *   4 gate f32 [n_tok * k][n_ff]  5 up f32 [n_tok * k][n_ff]
+ *   6 down f32 [n_tok * k][n_embd]
+ * (slot = one chosen (token, expert) pair; slots grouped by expert, tokens
+ * ascending). No counterpart in FISH, whose expert FFN keeps these in local
+ * vectors (model.cpp:1549-1579); here for stage-by-stage verification.
+ * Returns 0, or FISH_HIP_ERR_ARG for unsupported sizes. */
+#define FISH_HIP_MOE_PARTS 7
+FISH_HIP_API int fish_hip_moe_workspace_layout(int n_tok, int n_embd, int n_ff, int n_expert, int k,
+                                               uint64_t* offsets);
+
 /* The routing step alone (model.cpp:1528-1547): sel int32 [n_tok][k] and
  * wsel f32 [n_tok][k] in descending probability; workspace as for
  * fish_hip_moe_workspace_bytes(n_tok, 32, 32, n_expert, k). */

@@ -1,8 +1,17 @@
 """Expert-routed FFN on the GPU (fish_hip_moe_*) against the oracle and the golden layer.
 
-Routing (selected experts) must match exactly and weights within 1e-6; the
-silu*up requantization is checked per kernel (the GPU's own f32 h fed to the
-CPU quantizer must give the same bytes); layer outputs within 1e-4 * max|out|.
+Every stage of a layer is checked on the GPU's own inputs to that stage:
+routing (experts exact, weights within 1e-6), slot grouping (by expert,
+tokens ascending), the gate and up products within 1e-4 * max|ref|, the
+silu*up requantization bit-exact on the GPU's own f32 hidden values, the
+down product within 1e-4 * max|ref| on those codes, and the combine
+bit-exact (ascending expert order, separately rounded multiply and add).
+
+The end-to-end comparison with FISH's composed layer uses LAYER_TOL: the
+hidden state is requantized to int8 between the products, so f32 rounding
+differences of 1e-7 in gate/up may move one code by one step where
+silu(g)*u/d sits at a rounding midpoint, which shifts the layer output by
+about d_h * |w_down| (~1e-4 of max|out| for these weights).
 """
 import numpy as np
 import pytest
@@ -13,6 +22,7 @@ from imurun_amd.synth import normal
 pytestmark = pytest.mark.gpu
 
 TOL = 1e-4
+LAYER_TOL = 2e-3
 
 
 @pytest.fixture(scope="module")
@@ -28,10 +38,10 @@ def dev(torch_dev, a, dtype=None):
     return torch.from_numpy(np.ascontiguousarray(a)).to(d)
 
 
-def check_close(got, want, what):
+def check_close(got, want, what, tol=TOL):
     err = float(np.max(np.abs(got - want)))
     scale = float(np.max(np.abs(want)))
-    assert err <= TOL * scale, f"{what}: max err {err:.3e} vs {TOL} * {scale:.3e}"
+    assert err <= tol * scale, f"{what}: max err {err:.3e} vs {tol} * {scale:.3e}"
 
 
 @pytest.mark.parametrize("n_tok,n_expert,k", [(1, 8, 2), (64, 8, 2), (256, 128, 8), (7, 16, 4)])
@@ -70,16 +80,69 @@ def repacked_experts(torch_dev, oracle, t, n_expert, rows, n_in, seed, distinct=
     return packed, fh.repack(t, dev(torch_dev, packed), n_in, n_expert * rows)
 
 
+def check_stages(torch_dev, oracle, x, logits, parts, out, n_ff, k, types, packed):
+    """Each stage of one layer against the oracle on the GPU's own stage inputs."""
+    tg, tu, td = types
+    pg, pu, pd = packed
+    n_tok, n_embd = x.shape
+    p = {name: v.cpu().numpy() for name, v in parts.items()}
+    want_sel, want_w = oracle.route(logits, k, True)
+    assert np.array_equal(p["sel"], want_sel)
+    assert np.allclose(p["wsel"], want_w, rtol=0, atol=1e-6)
+    # slots: every (token, choice) once, grouped by expert, tokens ascending within an expert
+    tok_slot, slot_tok = p["tok_slot"], p["slot_tok"]
+    assert np.array_equal(np.sort(tok_slot.reshape(-1)), np.arange(n_tok * k))
+    assert np.array_equal(slot_tok[tok_slot], np.repeat(np.arange(n_tok)[:, None], k, axis=1))
+    exp_of = np.empty(n_tok * k, np.int64)
+    exp_of[tok_slot.reshape(-1)] = p["sel"].reshape(-1)
+    key = exp_of * n_tok + slot_tok
+    assert np.all(np.diff(key) > 0)
+    # gate / up products of each expert's tokens
+    bg, bu, bd = (fh.gguf_row_bytes(tg, n_embd) * n_ff, fh.gguf_row_bytes(tu, n_embd) * n_ff,
+                  fh.gguf_row_bytes(td, n_ff) * n_embd)
+    g_ref, u_ref = np.zeros_like(p["gate"]), np.zeros_like(p["up"])
+    experts = np.unique(exp_of)
+    for e in experts:
+        sl = np.nonzero(exp_of == e)[0]
+        g_ref[sl] = oracle.matmul_f32(tg, pg[e * bg:(e + 1) * bg], x[slot_tok[sl]], n_ff)
+        u_ref[sl] = oracle.matmul_f32(tu, pu[e * bu:(e + 1) * bu], x[slot_tok[sl]], n_ff)
+    check_close(p["gate"], g_ref, "gate products")
+    check_close(p["up"], u_ref, "up products")
+    # hidden rows: the requantization of the GPU's own silu(g)*u is FISH's, bit for bit
+    _, q256, h = fh.silu_mul_quantize(dev(torch_dev, p["gate"]), dev(torch_dev, p["up"]))
+    h = h.cpu().numpy()
+    if q256 is not None:
+        assert np.array_equal(q256.cpu().numpy(), oracle.quantize_acts_k(h))
+    d_ref = np.zeros_like(p["down"])
+    for e in experts:
+        sl = np.nonzero(exp_of == e)[0]
+        d_ref[sl] = oracle.matmul_f32(td, pd[e * bd:(e + 1) * bd], h[sl], n_embd)
+    check_close(p["down"], d_ref, "down products")
+    # combine in ascending expert order, w * down rounded, then added
+    want = np.zeros((n_tok, n_embd), np.float32)
+    for t in range(n_tok):
+        acc = np.zeros(n_embd, np.float32)
+        for i in np.argsort(p["sel"][t], kind="stable"):
+            acc = acc + p["wsel"][t, i] * p["down"][tok_slot[t, i]]
+        want[t] = acc
+    assert np.array_equal(out, want)
+
+
 def run_case(torch_dev, oracle, n_tok, n_embd, n_ff, n_expert, k, types, seed, distinct=None):
+    torch, d = torch_dev
     tg, tu, td = types
     pg, wg = repacked_experts(torch_dev, oracle, tg, n_expert, n_ff, n_embd, seed, distinct)
     pu, wu = repacked_experts(torch_dev, oracle, tu, n_expert, n_ff, n_embd, seed + 100, distinct)
     pd, wd = repacked_experts(torch_dev, oracle, td, n_expert, n_embd, n_ff, seed + 200, distinct)
     x = normal(seed + 300, (n_tok, n_embd))
     logits = normal(seed + 301, (n_tok, n_expert))
-    out = fh.moe_ffn(dev(torch_dev, x), dev(torch_dev, logits), n_ff, n_expert, k, True, tg, wg, tu, wu, td, wd)
+    ws = torch.empty(fh.moe_workspace_bytes(n_tok, n_embd, n_ff, n_expert, k), dtype=torch.uint8, device=d)
+    out = fh.moe_ffn(dev(torch_dev, x), dev(torch_dev, logits), n_ff, n_expert, k, True, tg, wg, tu, wu, td, wd,
+                     workspace=ws).cpu().numpy()
+    parts = fh.moe_parts(ws, n_tok, n_embd, n_ff, n_expert, k)
+    check_stages(torch_dev, oracle, x, logits, parts, out, n_ff, k, types, (pg, pu, pd))
     want = oracle.moe_ffn(x, logits, n_embd, n_ff, n_expert, k, True, tg, pg, tu, pu, td, pd)
-    check_close(out.cpu().numpy(), want, f"moe M={n_tok} E={n_embd} F={n_ff} NE={n_expert} k={k}")
+    check_close(out, want, f"moe M={n_tok} E={n_embd} F={n_ff} NE={n_expert} k={k}", LAYER_TOL)
 
 
 def test_moe_matches_reference_golden(torch_dev, golden):
@@ -93,7 +156,7 @@ def test_moe_matches_reference_golden(torch_dev, golden):
     check_close(out.cpu().numpy(), g["out"], "golden MoE layer")
 
 
-@pytest.mark.parametrize("n_tok", [1, 5, 20, 64])
+@pytest.mark.parametrize("n_tok", [1, 5, 20, 64, 160])
 def test_moe_mixtral_like(torch_dev, oracle, n_tok):
     run_case(torch_dev, oracle, n_tok, 512, 1024, 8, 2, (fh.Q4_K, fh.Q4_K, fh.Q4_K), 1000 + n_tok)
 

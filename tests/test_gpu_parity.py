@@ -125,6 +125,18 @@ def test_matmul_matches_oracle(torch_dev, oracle, t, n_tok):
 
 
 @pytest.mark.parametrize("t", TYPES)
+@pytest.mark.parametrize("n_tok", [5, 16, 17, 33, 64, 100])
+def test_batch_tiles_match_oracle(torch_dev, oracle, t, n_tok):
+    """Token counts across the MFMA batch kernel's 16/32/64-token workgroups
+    (and K split four or two ways), with 5 units of K and 80 rows."""
+    n_in, n_out = 1280, 80
+    rows = packed_weights(oracle, t, n_out, n_in, 800 + n_tok)
+    x = normal(900 + n_tok, (n_tok, n_in))
+    got = gpu_matmul(torch_dev, t, rows, x, n_out)
+    check_close(got, oracle.matmul_f32(t, rows, x, n_out), f"{fh.TYPE_NAMES[t]} batch M={n_tok}")
+
+
+@pytest.mark.parametrize("t", TYPES)
 def test_matmul_random_codes(torch_dev, oracle, t):
     n_in, n_out, n_tok = 1024, 80, 20
     rows = random_rows(t, n_out, n_in, 501)
@@ -150,6 +162,9 @@ def test_matmul_matches_reference_golden(torch_dev, golden, t, k):
     (fh.Q4_0, 4096, 14336, 1),
     (fh.Q4_K, 14336, 4096, 512),
     (fh.Q6_K, 4096, 14336, 512),
+    (fh.Q4_0, 14336, 4096, 512),
+    (fh.Q4_K, 14336, 4096, 64),
+    (fh.Q4_0, 32784, 512, 130),
 ])
 def test_full_size_shapes(torch_dev, oracle, t, n_out, n_in, n_tok):
     """Full-size shapes: all rows on the GPU; a row/token sample checked against
