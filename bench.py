@@ -1,8 +1,8 @@
 """Benchmark of the MI355X quantized-matmul path (one GPU).
 
 Workload (one step): the Llama-3-8B FFN at decode, Q4_0 weights, M = 1:
-  quantize x (1 x 4096) -> gate GEMV (14336 x 4096) -> up GEMV (14336 x 4096)
-  -> quantize h (1 x 14336) -> down GEMV (4096 x 14336)
+  gate + up GEMV (2 x 14336 x 4096) on x (1 x 4096, int8-quantized in the
+  same launch) -> down GEMV (4096 x 14336) on h (1 x 14336, likewise)
 Weights are f32 N(0, 0.02) packed to Q4_0 by FISH's block writer; inputs are
 N(0, 1); every step uses the next of several weight copies so the 256 MB
 Infinity Cache never holds the step's weights. value = algorithmic bytes of
@@ -20,7 +20,6 @@ import json
 
 import numpy as np
 import os
-import statistics
 import sys
 import time
 
@@ -35,11 +34,12 @@ E, F = 4096, 14336             # Llama-3-8B hidden / FFN width
 
 
 def gemv_step_bytes():
+    """Algorithmic bytes of the step and of its dominant launch (gate + up on one x)."""
     import imurun_amd as fh
     w = fh.gguf_row_bytes(fh.Q4_0, E) * F
-    gate = w + E * 4 + F * 4
+    gate_up = 2 * w + E * 4 + 2 * F * 4
     down = fh.gguf_row_bytes(fh.Q4_0, F) * E + F * 4 + E * 4
-    return 2 * gate + down, gate
+    return gate_up + down, gate_up
 
 
 def run_gemv(args, torch, fh, dev):
@@ -56,58 +56,61 @@ def run_gemv(args, torch, fh, dev):
                           for a, n_in, n_out in ((wg, E, F), (wu, E, F), (wd, F, E))))
     x = torch.from_numpy(normal(104, (1, E))).to(dev)
     h = torch.from_numpy(normal(105, (1, F))).to(dev)
-    ax = torch.empty(fh.act_bytes(1, E), dtype=torch.uint8, device=dev)
-    ah = torch.empty(fh.act_bytes(1, F), dtype=torch.uint8, device=dev)
     yg = torch.empty((1, F), dtype=torch.float32, device=dev)
     yu = torch.empty((1, F), dtype=torch.float32, device=dev)
     yd = torch.empty((1, E), dtype=torch.float32, device=dev)
 
     def step(c):
+        # matmul_tensors on f32 input: gate and up share one launch that
+        # quantizes x per workgroup; down quantizes h the same way
         g, u, d = sets[c]
-        fh.quantize(x, act=ax)
-        fh.matmul(t, g, ax, 1, E, F, y=yg)
-        fh.matmul(t, u, ax, 1, E, F, y=yu)
-        fh.quantize(h, act=ah)
-        fh.matmul(t, d, ah, 1, F, E, y=yd)
+        fh.matmul_tensors(t, [g, u], x, [F, F], ys=[yg, yu])
+        fh.matmul_tensors(t, [d], h, [E], ys=[yd])
 
-    # one HIP graph per weight copy: a step is one graph launch (5 kernels)
+    # HIP graphs of whole rotations: one graph runs `copies` consecutive steps
+    # (2 launches each) so host launch latency stays out of the GPU's way; a
+    # second graph runs the remaining K mod copies steps -> exactly K steps
     for c in range(copies):
         step(c)
     torch.cuda.synchronize()
-    graphs = []
     cs = torch.cuda.Stream()
-    with torch.cuda.stream(cs):
-        for c in range(copies):
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g, stream=cs):
-                step(c)
-            graphs.append(g)
-    torch.cuda.synchronize()
-    for i in range(args.warmup):
-        graphs[i % copies].replay()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        graphs[(args.warmup + i) % copies].replay()
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
 
-    # the dominant kernel alone: the gate GEMV, HIP events around each launch
-    ev = []
-    for i in range(max(50, args.steps)):
-        g = sets[i % copies][0]
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        fh.matmul(t, g, ax, 1, E, F, y=yg)
-        e1.record()
-        ev.append((e0, e1))
+    def capture(n_steps):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(cs):
+            with torch.cuda.graph(g, stream=cs):
+                for c in range(n_steps):
+                    step(c % copies)
+        return g
+
+    full = capture(copies)
+    rest = capture(args.steps % copies) if args.steps % copies else None
     torch.cuda.synchronize()
-    gate_us = statistics.median(a.elapsed_time(b) for a, b in ev) * 1e3
+    with torch.cuda.stream(cs):
+        for _ in range(max(1, args.warmup // copies)):
+            full.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps // copies):
+            full.replay()
+        if rest is not None:
+            rest.replay()
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+
+    # the dominant kernel alone: the fused gate+up GEMV, one graph of
+    # back-to-back launches over every weight copy, HIP events around the
+    # replays on the graph's stream -> average duration per launch
+    def gates():
+        for c in range(copies):
+            fh.matmul_tensors(t, [sets[c][0], sets[c][1]], x, [F, F], ys=[yg, yu])
+    gate_us = graph_time(torch, [gates], max(20, args.steps // 2)) / copies
     return elapsed, copies, gate_us
 
 
 def run_prefill(args, torch, fh, dev):
-    """One Llama-3-8B layer's projections at M = 512 (Q4_K; down in Q6_K)."""
+    """One Llama-3-8B layer's projections at M = 512 (Q4_K; down in Q6_K): q/k/v and
+    gate/up each as one grouped launch on the same activations, as FISH's matmul_tensors."""
     from imurun_amd.synth import normal
     M = 512
     shapes = [("q", fh.Q4_K, E, E), ("k", fh.Q4_K, 1024, E), ("v", fh.Q4_K, 1024, E), ("o", fh.Q4_K, E, E),
@@ -125,40 +128,28 @@ def run_prefill(args, torch, fh, dev):
     ys = {name: torch.empty((M, n_out), dtype=torch.float32, device=dev) for name, _, n_out, _ in shapes}
     ops = sum(2 * M * n_out * n_in for _, _, n_out, n_in in shapes)
 
-    def layer():
-        fh.quantize(x, act=ax)
-        for name in ("q", "k", "v", "o", "gate", "up"):
-            t, n_out, n_in, w = ws[name]
-            fh.matmul(t, w, ax, M, n_in, n_out, y=ys[name])
-        fh.quantize(hx, act=ah)
-        t, n_out, n_in, w = ws["down"]
-        fh.matmul(t, w, ah, M, n_in, n_out, y=ys["down"])
+    def group(names, act):
+        t, _, n_in, _ = ws[names[0]]
+        fh.matmul_group(t, [ws[n][3] for n in names], act, M, n_in, [ws[n][1] for n in names],
+                        ys=[ys[n] for n in names])
 
-    per = {}
-    for _ in range(2):
-        layer()
-    torch.cuda.synchronize()
-    reps = max(3, args.steps // 4)
-    t0 = time.perf_counter()
-    for _ in range(reps):
-        layer()
-    torch.cuda.synchronize()
-    layer_s = (time.perf_counter() - t0) / reps
-    for name in ("gate", "down"):
-        t, n_out, n_in, w = ws[name]
-        a = ax if n_in == E else ah
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(reps):
-            fh.matmul(t, w, a, M, n_in, n_out, y=ys[name])
-        e1.record()
-        torch.cuda.synchronize()
-        per[name] = e0.elapsed_time(e1) / reps * 1e3
-    return ops, layer_s, per
+    parts = {
+        "quantize_x": lambda: fh.quantize(x, act=ax),
+        "qkv": lambda: group(["q", "k", "v"], ax),
+        "o": lambda: group(["o"], ax),
+        "gate_up": lambda: group(["gate", "up"], ax),
+        "quantize_h": lambda: fh.quantize(hx, act=ah),
+        "down": lambda: group(["down"], ah),
+    }
+    reps = max(10, args.steps // 4)
+    layer_us = graph_time(torch, [lambda: [f() for f in parts.values()]], reps)
+    per = {name: graph_time(torch, [f], reps) for name, f in parts.items()}
+    return ops, layer_us, per
 
 
 def graph_time(torch, fns, reps):
-    """Median per-call time (us) of fns[i % len(fns)] captured as HIP graphs and replayed."""
+    """Average time (us) per replay of fns[i % len(fns)] captured as HIP graphs,
+    HIP events recorded on the stream the graphs replay on."""
     for f in fns:
         f()
     torch.cuda.synchronize()
@@ -171,16 +162,22 @@ def graph_time(torch, fns, reps):
                 f()
             graphs.append(g)
     torch.cuda.synchronize()
-    for g in graphs:
-        g.replay()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for i in range(reps):
-        graphs[i % len(graphs)].replay()
-    e1.record()
+    with torch.cuda.stream(cs):
+        for g in graphs:
+            g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(cs)
+        for i in range(reps):
+            graphs[i % len(graphs)].replay()
+        e1.record(cs)
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / reps * 1e3
+
+
+def graph_time_seq(torch, fns, reps):
+    """Average time (us) per call when all of fns run back to back in one HIP graph."""
+    return graph_time(torch, [lambda: [f() for f in fns]], reps) / len(fns)
 
 
 def run_q8_gemv(args, torch, fh, dev):
@@ -194,10 +191,10 @@ def run_q8_gemv(args, torch, fh, dev):
     x = torch.from_numpy(normal(122, (1, K))).to(dev)
     a = torch.empty(fh.act_bytes(1, K), dtype=torch.uint8, device=dev)
     y = torch.empty((1, N), dtype=torch.float32, device=dev)
-    fns = [lambda w=w: (fh.quantize(x, act=a), fh.matmul(t, w, a, 1, K, N, y=y)) for w in ws]
-    us = graph_time(torch, fns, 4 * copies * 10)
+    fns = [lambda w=w: fh.matmul_tensors(t, [w], x, [N], ys=[y]) for w in ws]
+    us = graph_time_seq(torch, fns, 40)
     b = p.size + K * 4 + N * 4
-    return {"workload": "Q8_0 GEMV 4096x4096, M=1, quantize + matmul", "us": round(us, 3),
+    return {"workload": "Q8_0 GEMV 4096x4096, M=1, f32 x quantized in-kernel", "us": round(us, 3),
             "gbs": round(b / us / 1e3, 1), "pct_hbm": round(100 * b / us / 1e3 / HBM_PEAK_GBS, 2)}
 
 
@@ -232,7 +229,7 @@ def run_moe(args, torch, fh, dev, name, NE, K, E, F_, types, cases):
             active = int(np.unique(sel.cpu().numpy()).size)
         fns = [lambda lg=lg: fh.moe_ffn(x, lg, F_, NE, K, True, tg, wg, tu, wu, td, wd, out=y, workspace=ws)
                for lg in logit_sets]
-        us = graph_time(torch, fns, max(20, 4 * len(fns)))
+        us = graph_time_seq(torch, fns, max(20, 80 // len(fns)))
         b = active * per_expert + M * E * 8
         ops = 2 * M * K * 3 * E * F_
         out[f"M{M}"] = {"us": round(us, 2), "active_experts": active, "bytes": b, "gbs": round(b / us / 1e3, 1),
@@ -324,10 +321,11 @@ def main() -> int:
         "dtype": "int8",
         "data": f"synthetic: W ~ N(0,0.02) packed to Q4_0 by FISH's block writer, x ~ N(0,1); "
                 f"{copies} weight copies rotated per step (> 2x the 256 MB MALL)",
-        "config": {"workload": "Llama-3-8B FFN decode, Q4_0, M=1: quantize + gate/up GEMV 14336x4096 + "
-                               "quantize + down GEMV 4096x14336", "n_tok": 1, "hidden": E, "ffn": F,
+        "config": {"workload": "Llama-3-8B FFN decode, Q4_0, M=1: gate+up GEMV 2x14336x4096 and down GEMV "
+                               "4096x14336, int8 activations quantized in the same launches",
+                   "n_tok": 1, "hidden": E, "ffn": F,
                    "weight_type": "Q4_0", "hbm_pct_of_peak": round(100 * value / HBM_PEAK_GBS, 2)},
-        "roofline": {"bound": "hbm", "kernel": "gemv_kernel<Q4_0> gate 14336x4096",
+        "roofline": {"bound": "hbm", "kernel": "gemv_x_kernel<Q4_0> gate+up 2 x 14336x4096, x quantized in-kernel",
                      "achieved": round(gate_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gate_gbs / HBM_PEAK_GBS, 4), "traffic": None,
                      "median_kernel_us": round(gate_us, 3), "algorithmic_bytes": gate_bytes},
@@ -339,15 +337,16 @@ def main() -> int:
         out["moe_qwen3"] = run_moe(args, torch, fh, dev, "Qwen3-30B-A3B", 128, 8, 2048, 768,
                                    (fh.Q4_K, fh.Q4_K, fh.Q6_K), (1, 256))
     if not args.no_prefill:
-        ops, layer_s, per = run_prefill(args, torch, fh, dev)
-        tops = ops / layer_s / 1e12
+        ops, layer_us, per = run_prefill(args, torch, fh, dev)
+        tops = ops / layer_us / 1e6
+        proj_ops = {"qkv": 2 * 512 * 6144 * E, "o": 2 * 512 * E * E, "gate_up": 2 * 512 * 2 * F * E,
+                    "down": 2 * 512 * E * F}
         out["prefill"] = {"workload": "Llama-3-8B layer projections, M=512 (q,k,v,o,gate,up Q4_K; down Q6_K) + "
-                                      "activation quantization", "int_ops": ops,
-                          "ms": round(layer_s * 1e3, 4), "tops": round(tops, 2),
+                                      "activation quantization; q/k/v and gate/up as grouped launches",
+                          "int_ops": ops, "us": round(layer_us, 2), "tops": round(tops, 2),
                           "pct_int8_peak": round(100 * tops / INT8_PEAK_TOPS, 2),
-                          "gate_q4k_us": round(per["gate"], 2), "down_q6k_us": round(per["down"], 2),
-                          "gate_q4k_tops": round(2 * 512 * F * E / (per["gate"] * 1e-6) / 1e12, 2),
-                          "down_q6k_tops": round(2 * 512 * F * E / (per["down"] * 1e-6) / 1e12, 2)}
+                          "parts_us": {k: round(v, 2) for k, v in per.items()},
+                          "parts_tops": {k: round(proj_ops[k] / per[k] / 1e6, 1) for k in proj_ops}}
     if not args.no_cpu:
         out["cpu_baseline"] = run_cpu_baseline(args, step_bytes)
     print(json.dumps(out))

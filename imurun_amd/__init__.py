@@ -56,6 +56,10 @@ def load() -> ctypes.CDLL:
         "fish_hip_quantize": ([_P, ctypes.c_int, ctypes.c_int, _P, _P, _P, _P], ctypes.c_int),
         "fish_hip_repack": ([ctypes.c_uint32, _P, ctypes.c_int, ctypes.c_int, _P, _P], ctypes.c_int),
         "fish_hip_matmul": ([ctypes.c_uint32, _P, _P, ctypes.c_int, ctypes.c_int, ctypes.c_int, _P, _P], ctypes.c_int),
+        "fish_hip_matmul_group": ([ctypes.c_uint32, ctypes.c_int, _P, _P, ctypes.c_int, ctypes.c_int, _P, _P, _P],
+                                  ctypes.c_int),
+        "fish_hip_matmul_tensors": ([ctypes.c_uint32, ctypes.c_int, _P, _P, ctypes.c_int, ctypes.c_int, _P, _P, _P,
+                                     ctypes.c_uint64, _P], ctypes.c_int),
         "fish_hip_block_ints": ([ctypes.c_uint32, _P, _P, ctypes.c_int, ctypes.c_int, _P, _P], ctypes.c_int),
         "fish_hip_quantize_rows": ([ctypes.c_uint32, _P, _P, ctypes.c_int, ctypes.c_int, ctypes.c_int], ctypes.c_int),
         "fish_hip_moe_workspace_bytes": ([ctypes.c_int] * 5, ctypes.c_uint64),
@@ -171,6 +175,55 @@ def matmul(t: int, w, act, n_tok: int, n_in: int, n_out: int, y=None, stream=Non
     _check(load().fish_hip_matmul(t, w.data_ptr(), act.data_ptr(), n_tok, n_in, n_out, y.data_ptr(),
                                   _stream(stream)), "matmul")
     return y
+
+
+def matmul_group(t: int, ws, act, n_tok: int, n_in: int, n_outs, ys=None, stream=None):
+    """Several repacked tensors of one type applied to the same activations (matmul_tensors)."""
+    import torch
+    n = len(ws)
+    if n != len(n_outs) or not 1 <= n <= 4:
+        raise FishHipError("matmul_group: 1..4 tensors with one n_out each")
+    for w, n_out in zip(ws, n_outs):
+        if w.numel() < weight_bytes(t, n_in, n_out):
+            raise FishHipError("matmul_group: weight buffer smaller than its layout")
+    if act.numel() < act_bytes(n_tok, n_in):
+        raise FishHipError("matmul_group: activation buffer smaller than its layout")
+    if ys is None:
+        ys = [torch.empty((n_tok, n_out), dtype=torch.float32, device=ws[0].device) for n_out in n_outs]
+    for y, n_out in zip(ys, n_outs):
+        assert y.numel() >= n_tok * n_out and y.is_contiguous()
+    wp = (ctypes.c_void_p * n)(*[w.data_ptr() for w in ws])
+    yp = (ctypes.c_void_p * n)(*[y.data_ptr() for y in ys])
+    no = (ctypes.c_int * n)(*n_outs)
+    _check(load().fish_hip_matmul_group(t, n, wp, act.data_ptr(), n_tok, n_in, no, yp, _stream(stream)),
+           "matmul_group")
+    return ys
+
+
+def matmul_tensors(t: int, ws, x, n_outs, ys=None, act=None, stream=None):
+    """f32 x [n_tok, n_in] quantized and multiplied by 1..4 tensors (matmul_tensors / the
+    convenience matmul_batch); one token runs as one fused launch without a workspace."""
+    import torch
+    assert x.is_cuda and x.dtype == torch.float32 and x.dim() == 2 and x.is_contiguous()
+    n_tok, n_in = x.shape
+    n = len(ws)
+    if n != len(n_outs) or not 1 <= n <= 4:
+        raise FishHipError("matmul_tensors: 1..4 tensors with one n_out each")
+    for w, n_out in zip(ws, n_outs):
+        if w.numel() < weight_bytes(t, n_in, n_out):
+            raise FishHipError("matmul_tensors: weight buffer smaller than its layout")
+    if ys is None:
+        ys = [torch.empty((n_tok, n_out), dtype=torch.float32, device=x.device) for n_out in n_outs]
+    for y, n_out in zip(ys, n_outs):
+        assert y.numel() >= n_tok * n_out and y.is_contiguous()
+    if act is None and n_tok > 1:
+        act = torch.empty(act_bytes(n_tok, n_in), dtype=torch.uint8, device=x.device)
+    wp = (ctypes.c_void_p * n)(*[w.data_ptr() for w in ws])
+    yp = (ctypes.c_void_p * n)(*[y.data_ptr() for y in ys])
+    no = (ctypes.c_int * n)(*n_outs)
+    _check(load().fish_hip_matmul_tensors(t, n, wp, x.data_ptr(), n_tok, n_in, no, yp, _ptr(act),
+                                          act.numel() if act is not None else 0, _stream(stream)), "matmul_tensors")
+    return ys
 
 
 def matmul_batch(t: int, w, x, n_out: int, stream=None):

@@ -48,11 +48,12 @@ bool type_ok(uint32_t type) { return type == kQ8_0 || type == kQ4_0 || type == k
 constexpr int kGemvMaxTok = 4;
 constexpr int kBatchMaxTok = 64;
 
+bool uses_gemm(const WeightLayout& L, int n_tok) { return n_tok > kBatchMaxTok && is_kquant(L.type); }
+
 hipError_t dispatch_matmul(const void* w, const WeightLayout& L, const void* act, int n_tok, float* y, int ldy,
                            hipStream_t s) {
-    if (n_tok > kGemvMaxTok && batch_mfma_supported(L) && (n_tok <= kBatchMaxTok || !is_kquant(L.type)))
-        return launch_batch_mfma(w, L, act, n_tok, n_tok, y, ldy, s);
-    if (n_tok > kGemvMaxTok && is_kquant(L.type)) return launch_gemm(w, L, act, n_tok, y, ldy, s);
+    if (uses_gemm(L, n_tok)) return launch_gemm(w, L, act, n_tok, y, ldy, s);
+    if (n_tok > kGemvMaxTok && batch_mfma_supported(L)) return launch_batch_mfma(w, L, act, n_tok, n_tok, y, ldy, s);
     return launch_gemv(w, L, act, n_tok, n_tok, y, ldy, s);
 }
 
@@ -78,7 +79,7 @@ MoeWork moe_work(int n_tok, int n_embd, int n_ff, int n_expert, int k) {
     const int avg = (w.slots + n_expert - 1) / n_expert;
     w.mfma = avg > 1 && n_embd % 256 == 0 && n_ff % 256 == 0;
     if (w.mfma) w.item_tokens = avg <= 12 ? 16 : kBatchItemTokens;
-    else w.item_tokens = avg <= 1 ? 1 : (avg <= 2 ? 2 : (avg <= 4 ? 4 : (avg <= 8 ? 8 : 16)));
+    else w.item_tokens = avg <= 1 ? 1 : (avg <= 2 ? 2 : kGemvItemTokens);
     w.max_items = std::min(n_expert, w.slots) + w.slots / w.item_tokens + 1;
     const ActLayout ax = act_layout(n_tok, n_embd), ah = act_layout(w.slots, n_ff);
     size_t off = 0;
@@ -250,14 +251,45 @@ public:
             if (is_kquant(rs[size_t(i)]->layout.type) && !AL.has256) return false;
         const size_t x_bytes = size_t(n_tok) * size_t(n_in) * 4;
         if (!reserve(x_bytes, AL.total, y_total * 4)) return false;
+        // one token, one type: each workgroup quantizes x itself (one launch)
+        bool fused = n_tok == 1 && n <= kGemmGroupMax && gemv_x_supported(rs[0]->layout);
+        for (int i = 1; i < n && fused; ++i) fused = rs[size_t(i)]->layout.type == rs[0]->layout.type;
         hipError_t e = hipMemcpyAsync(d_x_, x, x_bytes, hipMemcpyHostToDevice, stream_);
-        if (e == hipSuccess) e = launch_quantize(static_cast<const float*>(d_x_), n_tok, n_in, n_in, d_act_, nullptr,
-                                                 nullptr, stream_);
+        if (e == hipSuccess && !fused)
+            e = launch_quantize(static_cast<const float*>(d_x_), n_tok, n_in, n_in, d_act_, nullptr, nullptr, stream_);
+        // y_i at consecutive offsets of the staging buffer; tensors of one
+        // K-quant type go out as one grouped launch when the batch is GEMM-sized
+        std::vector<float*> dys(static_cast<size_t>(n));
         size_t off = 0;
-        for (int i = 0; i < n && e == hipSuccess; ++i) {
-            e = dispatch_matmul(rs[size_t(i)]->dev, rs[size_t(i)]->layout, d_act_, n_tok,
-                                static_cast<float*>(d_y_) + off, n_outs[i], stream_);
+        bool one_group = n <= kGemmGroupMax;
+        for (int i = 0; i < n; ++i) {
+            dys[size_t(i)] = static_cast<float*>(d_y_) + off;
             off += size_t(n_tok) * size_t(n_outs[i]);
+            one_group = one_group && rs[size_t(i)]->layout.type == rs[0]->layout.type &&
+                        uses_gemm(rs[size_t(i)]->layout, n_tok);
+        }
+        if (e == hipSuccess && fused) {
+            const void* ws[kGemmGroupMax];
+            WeightLayout Ls[kGemmGroupMax];
+            for (int i = 0; i < n; ++i) {
+                ws[i] = rs[size_t(i)]->dev;
+                Ls[i] = rs[size_t(i)]->layout;
+            }
+            e = launch_gemv_x(n, ws, Ls, static_cast<const float*>(d_x_), dys.data(), stream_);
+        } else if (e == hipSuccess && one_group) {
+            const void* ws[kGemmGroupMax];
+            WeightLayout Ls[kGemmGroupMax];
+            int ldy[kGemmGroupMax];
+            for (int i = 0; i < n; ++i) {
+                ws[i] = rs[size_t(i)]->dev;
+                Ls[i] = rs[size_t(i)]->layout;
+                ldy[i] = n_outs[i];
+            }
+            e = launch_gemm_group(n, ws, Ls, d_act_, n_tok, dys.data(), ldy, stream_);
+        } else {
+            for (int i = 0; i < n && e == hipSuccess; ++i)
+                e = dispatch_matmul(rs[size_t(i)]->dev, rs[size_t(i)]->layout, d_act_, n_tok, dys[size_t(i)],
+                                    n_outs[i], stream_);
         }
         if (e == hipSuccess) e = hipStreamSynchronize(stream_);
         if (e != hipSuccess) {
@@ -352,6 +384,54 @@ int fish_hip_matmul(uint32_t type, const void* w, const void* act, int n_tok, in
     if (is_kquant(type) && n_in % 256) return fail(FISH_HIP_ERR_ARG, "matmul: K-quant needs n_in % 256 == 0");
     const hipError_t e = dispatch_matmul(w, L, act, n_tok, y, n_out, as_stream(stream));
     return e == hipSuccess ? 0 : hip_fail(e, "matmul");
+}
+
+int fish_hip_matmul_group(uint32_t type, int n, const void* const* ws, const void* act, int n_tok, int n_in,
+                          const int* n_outs, float* const* ys, void* stream) {
+    if (n <= 0 || n > kGemmGroupMax || !ws || !act || !n_outs || !ys || n_tok <= 0)
+        return fail(FISH_HIP_ERR_ARG, "matmul_group: bad arguments");
+    if (is_kquant(type) && n_in % 256) return fail(FISH_HIP_ERR_ARG, "matmul_group: K-quant needs n_in % 256 == 0");
+    WeightLayout L[kGemmGroupMax];
+    int ldy[kGemmGroupMax];
+    for (int i = 0; i < n; ++i) {
+        L[i] = weight_layout(type, n_in, n_outs[i]);
+        ldy[i] = n_outs[i];
+        if (!ws[i] || !ys[i] || !L[i].total) return fail(FISH_HIP_ERR_ARG, "matmul_group: bad tensor");
+    }
+    hipError_t e = hipSuccess;
+    if (uses_gemm(L[0], n_tok)) {
+        e = launch_gemm_group(n, ws, L, act, n_tok, ys, ldy, as_stream(stream));
+    } else {
+        for (int i = 0; i < n && e == hipSuccess; ++i)
+            e = dispatch_matmul(ws[i], L[i], act, n_tok, ys[i], ldy[i], as_stream(stream));
+    }
+    return e == hipSuccess ? 0 : hip_fail(e, "matmul_group");
+}
+
+int fish_hip_matmul_tensors(uint32_t type, int n, const void* const* ws, const float* x, int n_tok, int n_in,
+                            const int* n_outs, float* const* ys, void* act_workspace, uint64_t act_workspace_bytes,
+                            void* stream) {
+    if (n <= 0 || n > kGemmGroupMax || !ws || !x || !n_outs || !ys || n_tok <= 0 || n_in <= 0 || n_in % 32)
+        return fail(FISH_HIP_ERR_ARG, "matmul_tensors: bad arguments");
+    if (is_kquant(type) && n_in % 256) return fail(FISH_HIP_ERR_ARG, "matmul_tensors: K-quant needs n_in % 256 == 0");
+    WeightLayout L[kGemmGroupMax];
+    for (int i = 0; i < n; ++i) {
+        L[i] = weight_layout(type, n_in, n_outs[i]);
+        if (!ws[i] || !ys[i] || !L[i].total) return fail(FISH_HIP_ERR_ARG, "matmul_tensors: bad tensor");
+    }
+    hipError_t e;
+    if (n_tok == 1 && gemv_x_supported(L[0])) {
+        e = launch_gemv_x(n, ws, L, x, ys, as_stream(stream));
+    } else {
+        if (!act_workspace || act_workspace_bytes < act_layout(n_tok, n_in).total)
+            return fail(FISH_HIP_ERR_ARG, "matmul_tensors: act_workspace missing or too small");
+        e = launch_quantize(x, n_tok, n_in, n_in, act_workspace, nullptr, nullptr, as_stream(stream));
+        if (e == hipSuccess) {
+            const int rc = fish_hip_matmul_group(type, n, ws, act_workspace, n_tok, n_in, n_outs, ys, stream);
+            if (rc != 0) return rc;
+        }
+    }
+    return e == hipSuccess ? 0 : hip_fail(e, "matmul_tensors");
 }
 
 int fish_hip_block_ints(uint32_t type, const void* w, const void* act, int n_in, int n_out, int32_t* out,

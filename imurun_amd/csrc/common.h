@@ -19,8 +19,17 @@
 //   q256 [M][K] int8   d256 [M][K/256] f32  s16 [M][K/16] int16   (Q8ActK)
 //   bsm  [M][K/256][16] int8: bytes 0..7 = bsum_g >> 6, 8..15 = bsum_g & 63
 //   m32, m256 [M][K] int8: the q32 / q256 codes in MFMA operand order
+//   gA   [M'/32][K/32][64][16] int8: q256 codes as A operands of
+//        v_mfma_i32_32x32x32_i8, one 1 KB piece per (32-token block, 32-value
+//        step): lane l holds token l % 32, values 16 (l / 32) .. +15 of the step
+//   gX   [M'/32][K/256][2][16] f32: Q8ActK d in the order of that MFMA's
+//        output registers: [h][i] is token 8 (i / 4) + 4 h + i % 4 of the block
+//   gJ   [M'/32][K/256][64][8] f16: A operands of v_mfma_f32_32x32x16_f16
+//        for the Q4_K mins term: lane l < 32 holds bsum_g >> 6 of token l,
+//        lane 32 + l holds bsum_g & 63, g = 0..7
 // (bsum_g = the Q8ActK per-32 sum; s16 holds per-16 sums, two of which make
-// a bsum). The 256 planes exist only when K % 256 == 0.
+// a bsum; M' = M rounded up to a multiple of 32, the extra tokens all zero).
+// The 256 planes exist only when K % 256 == 0.
 // MFMA operand order: within each 256-element unit (8 groups of 32), byte
 // q*64 + g*8 + i holds element 4q+i (i < 4) or 16+4q+(i-4) (i >= 4) of group
 // g, q < 4: the eight codes that lane quarter q of a 16x16x32 int8 MFMA
@@ -97,7 +106,9 @@ inline bool is_kquant(uint32_t type) { return type == kQ4_K || type == kQ6_K; }
 
 struct ActLayout {
     int n_tok = 0, n_in = 0;
-    size_t q32 = 0, d32 = 0, s32 = 0, q256 = 0, d256 = 0, s16 = 0, bsm = 0, m32 = 0, m256 = 0, total = 0;
+    size_t q32 = 0, d32 = 0, s32 = 0, q256 = 0, d256 = 0, s16 = 0, bsm = 0, m32 = 0, m256 = 0;
+    size_t gA = 0, gX = 0, gJ = 0, total = 0;
+    int n_tb = 0;  // 32-token blocks of the gA / gX / gJ planes
     bool has256 = false;
 };
 
@@ -119,6 +130,11 @@ inline ActLayout act_layout(int n_tok, int n_in) {
         L.bsm = off;  off = align256(off + M * (K / 256) * 16);
         L.m32 = off;  off = align256(off + M * K);
         L.m256 = off; off = align256(off + M * K);
+        L.n_tb = (n_tok + 31) / 32;
+        const size_t TB = size_t(L.n_tb), SB = K / 256;
+        L.gA = off;   off = align256(off + TB * 32 * K);
+        L.gX = off;   off = align256(off + TB * SB * 32 * 4);
+        L.gJ = off;   off = align256(off + TB * SB * 64 * 16);
     }
     L.total = off;
     return L;
@@ -135,6 +151,10 @@ struct ActPtrs {
     const int8_t* bsm;
     const int8_t* m32;
     const int8_t* m256;
+    const int8_t* gA;
+    const float* gX;
+    const uint16_t* gJ;
+    int n_tb;
 };
 
 inline ActPtrs act_ptrs(const void* base, const ActLayout& L) {
@@ -149,6 +169,10 @@ inline ActPtrs act_ptrs(const void* base, const ActLayout& L) {
     p.bsm = L.has256 ? reinterpret_cast<const int8_t*>(b + L.bsm) : nullptr;
     p.m32 = L.has256 ? reinterpret_cast<const int8_t*>(b + L.m32) : nullptr;
     p.m256 = L.has256 ? reinterpret_cast<const int8_t*>(b + L.m256) : nullptr;
+    p.gA = L.has256 ? reinterpret_cast<const int8_t*>(b + L.gA) : nullptr;
+    p.gX = L.has256 ? reinterpret_cast<const float*>(b + L.gX) : nullptr;
+    p.gJ = L.has256 ? reinterpret_cast<const uint16_t*>(b + L.gJ) : nullptr;
+    p.n_tb = L.n_tb;
     return p;
 }
 

@@ -1,26 +1,29 @@
 // Many-token matmul (prefill / batched experts) over repacked K-quant weights
-// on gfx950 int8 MFMA with i32 accumulation.
+// on gfx950 int8 MFMA (v_mfma_i32_32x32x32_i8) with i32 accumulation.
 //
-// Arithmetic (same integers as FISH's dot_q4_K_q8k / dot_q6_K_q8k,
-// quant_x86.cpp:346-382, :445-495), per output (token t, row i) and
-// super-block sb of 256 values:
+// Arithmetic (the integers of FISH's dot_q4_K_q8k / dot_q6_K_q8k,
+// quant_x86.cpp:346-382, :445-495), per output (token t, row r) and
+// super-block of 256 values:
 //   Q4_K  I = sum_g sc_g sum_l q x       J = sum_g m_g bsum_g
 //         y += xd * (d * I - dmin * J)
-//   Q6_K  I = sum_j sc_j sum_{16} (q - 32) x            y += d * xd * I
-// The per-group integer scale makes w' = sc * q (Q4_K, 0..945) or
-// sc * (q - 32) (Q6_K, -4064..4096) too wide for int8, so the dequantised
-// weight tile is stored in LDS as two int8 planes, w' = 2^s * hi + lo
-// (s = 5 for Q4_K, 6 for Q6_K; 0 <= lo < 2^s), and I = 2^s * (hi . x) +
-// (lo . x) comes out of two i8 MFMA accumulators with no per-group VALU
-// work. J is a K = 8 product per super-block; bsum = 64 * bh + bl (bh, bl
-// int8, written by the quantizer) turns it into two small 32x32x16 MFMAs.
+//   Q6_K  I = sum_j sc_j sum_{16} (q - 32) x            y += xd * (d * I)
+// A scaled code (sc * q up to 945, sc * (q - 32) up to 4096 in magnitude) does
+// not fit an int8 MFMA operand, so every weight is split into two int8 planes
+// that one MFMA each multiplies with the same activation operand:
+//   Q4_K  sc = 8 a + b (a, b in 0..7): planes a*q and b*q (<= 105), I = 8 H + L
+//         -- one packed 16-bit multiply makes four bytes of a plane;
+//   Q6_K  w' = sc * (q - 32) = 64 hi + lo (0 <= lo < 64): I = 64 H + L.
+// J is exact on one f16 MFMA per super-block: A = (bsum >> 6, bsum & 63) per
+// token (written by the quantizer), B = (64 m_g, m_g) per row, all small
+// integers, so every product and sum is exact in f32.
 //
-// Tiling: a workgroup of 4 wavefronts owns BN weight rows x BM tokens
-// (BN * BM = 4 * 64 * 64); each wavefront owns 64 rows x 64 tokens as 2 x 2
-// blocks of 32 x 32 (v_mfma_i32_32x32x32_i8). K advances 64 values (two
-// groups) per step through double-buffered LDS: while the MFMAs of step k
-// run, the global loads of step k+1 are in flight, and the weights of step
-// k+1 are dequantised into the hi/lo planes once for all BM tokens.
+// Tiling: a workgroup of WT x WR wavefronts owns 64 WT tokens x 32 WR rows;
+// a wavefront owns 64 tokens x 32 rows (two 32x32 blocks). The weight planes
+// of a 128-value stage are dequantised once per workgroup into a three-deep
+// LDS ring (one barrier per stage); activations go straight from HBM/L2 into
+// the A-operand registers (the quantizer writes them in operand order), one
+// stage ahead; two wavefronts per SIMD hide each other's latencies. The lane that owns an output owns its weight row, so row
+// scales are lane scalars; token scales come in output-register order.
 #include "common.h"
 #include "kernels.h"
 
@@ -30,298 +33,365 @@ namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef short v2s __attribute__((ext_vector_type(2)));
+typedef unsigned short v2us __attribute__((ext_vector_type(2)));
 
-constexpr int KS = 64;       // K values per step (two 32-groups)
-constexpr int P = KS + 16;   // LDS row pitch in bytes (16-byte skew: conflict-free 128-bit reads)
+constexpr int SSTEPS = 4;  // 32-value steps per stage
+constexpr int RING = 3;    // LDS stages in flight
 
-__device__ __forceinline__ v2s bytes_even(uint32_t v) { return __builtin_bit_cast(v2s, v & 0x00FF00FFu); }
-__device__ __forceinline__ v2s bytes_odd(uint32_t v) { return __builtin_bit_cast(v2s, (v >> 8) & 0x00FF00FFu); }
-
-// Four unsigned codes (bytes of v) -> w' = sc * (code - off) split into
-// (hi, lo) bytes with w' = 2^SHIFT * hi + lo, 0 <= lo < 2^SHIFT.
-template <int SHIFT>
-__device__ __forceinline__ void split4(uint32_t v, v2s offv, v2s scv, uint32_t& hi, uint32_t& lo) {
-    const v2s we = (bytes_even(v) - offv) * scv;
-    const v2s wo = (bytes_odd(v) - offv) * scv;
-    const v2s he = we >> SHIFT, ho = wo >> SHIFT;
-    const v2s mask = {short((1 << SHIFT) - 1), short((1 << SHIFT) - 1)};
-    const uint32_t he32 = __builtin_bit_cast(uint32_t, he) & 0x00FF00FFu;
-    const uint32_t ho32 = __builtin_bit_cast(uint32_t, ho) & 0x00FF00FFu;
-    hi = he32 | (ho32 << 8);
-    lo = __builtin_bit_cast(uint32_t, we & mask) | (__builtin_bit_cast(uint32_t, wo & mask) << 8);
-}
-
-// Global data of one step held in registers between its load and its LDS write.
-template <int BN, int BM>
-struct Stage {
-    static constexpr int A_VECS = BM * KS / 16 / 256;   // uint4 of activation codes per thread
-    static constexpr int W_HALVES = BN * 4 / 256;       // half-groups (16 values) per thread
-    uint4 act[A_VECS];
-    uint4 codes[W_HALVES];
-    uint32_t qh[W_HALVES];
-    int sc[W_HALVES];
-    float xd;      // first step of a super-block: this thread's token scale
-    uint4 bsm;     // and its bsum split (Q4_K)
+// Raw weight data of one (row, 32-value step) item, between its global load
+// and its dequantisation.
+struct Raw {
+    uint4 codes;   // 16 bytes: Q4 nibble chunk (Q6_K: the low nibbles)
+    uint4 meta;    // Q4_K: d, dmin, scales[12] of the super-block
+    uint2 qh;      // Q6_K: high bits
+    uint32_t sc2;  // Q6_K: the two 16-value scales of the step (bytes 0, 1)
 };
 
-template <uint32_t T, int BN, int BM>
-__global__ __launch_bounds__(256, 1) void gemm_kq_kernel(WeightPtrs W, ActPtrs A, int n_in, int n_out, int n_tok,
-                                                         float* __restrict__ y, int ldy) {
-    constexpr int SHIFT = (T == kQ4_K) ? 5 : 6;
-    constexpr int WN = BN / 64;  // wavefronts along rows
-    using S = Stage<BN, BM>;
-    __shared__ __attribute__((aligned(16))) uint8_t s_act[2][BM * P];
-    __shared__ __attribute__((aligned(16))) uint8_t s_hi[2][BN * P];
-    __shared__ __attribute__((aligned(16))) uint8_t s_lo[2][BN * P];
-    __shared__ float s_xd[2][BM];
-    __shared__ __attribute__((aligned(16))) int8_t s_bsm[2][BM * 16];
+template <uint32_t T>
+__device__ __forceinline__ void load_raw(Raw& r, const WeightPtrs& W, int row, int step, int n_in) {
+    const int groups = n_in / 32;
+    const size_t gi = size_t(row) * groups + step;
+    r.codes = *reinterpret_cast<const uint4*>(W.codes + gi * 16);
+    if constexpr (T == kQ4_K) {
+        r.meta = *reinterpret_cast<const uint4*>(W.aux + (size_t(row) * (n_in / 256) + (step >> 3)) * 16);
+    } else {
+        r.qh = *reinterpret_cast<const uint2*>(W.aux + gi * 8);
+        r.sc2 = *reinterpret_cast<const uint16_t*>(W.sc + size_t(row) * (n_in / 16) + 2 * step);
+    }
+}
+
+__device__ __forceinline__ uint32_t mul4(uint32_t codes, uint32_t s2) {
+    // four byte codes times a small factor; no byte overflows (<= 105)
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(v2us, codes) * __builtin_bit_cast(v2us, s2));
+}
+
+// Q6_K: four 6-bit codes (bytes) -> hi and lo bytes of sc * (q - 32).
+__device__ __forceinline__ void split6(uint32_t q, v2s sc, v2s off, uint32_t& hi, uint32_t& lo) {
+    const v2s e = __builtin_bit_cast(v2s, q & 0x00FF00FFu);
+    const v2s o = __builtin_bit_cast(v2s, (q >> 8) & 0x00FF00FFu);
+    const v2s we = e * sc + off, wo = o * sc + off;  // sc * q - 32 sc
+    const uint32_t he = __builtin_bit_cast(uint32_t, we >> 6), ho = __builtin_bit_cast(uint32_t, wo >> 6);
+    const uint32_t le = __builtin_bit_cast(uint32_t, we) & 0x003F003Fu, lo_ = __builtin_bit_cast(uint32_t, wo) & 0x003F003Fu;
+    hi = __builtin_amdgcn_perm(ho, he, 0x06020400u);
+    lo = __builtin_amdgcn_perm(lo_, le, 0x06020400u);
+}
+
+// Dequantise one item into the two planes x two halves (16 bytes each).
+template <uint32_t T>
+__device__ __forceinline__ void dequant(const Raw& r, int step, uint4 (&out)[2][2]) {
+    const uint4 c = r.codes;
+    const uint4 n0 = make_uint4(c.x & 0x0F0F0F0Fu, c.y & 0x0F0F0F0Fu, c.z & 0x0F0F0F0Fu, c.w & 0x0F0F0F0Fu);
+    const uint4 n1 = make_uint4((c.x >> 4) & 0x0F0F0F0Fu, (c.y >> 4) & 0x0F0F0F0Fu, (c.z >> 4) & 0x0F0F0F0Fu,
+                                (c.w >> 4) & 0x0F0F0F0Fu);
+    if constexpr (T == kQ4_K) {
+        int sc, mn;
+        k4_scale_min(r.meta.y, r.meta.z, r.meta.w, step & 7, sc, mn);
+        const uint32_t a = uint32_t(sc >> 3) * 0x00010001u, b = uint32_t(sc & 7) * 0x00010001u;
+        out[0][0] = make_uint4(mul4(n0.x, a), mul4(n0.y, a), mul4(n0.z, a), mul4(n0.w, a));
+        out[0][1] = make_uint4(mul4(n1.x, a), mul4(n1.y, a), mul4(n1.z, a), mul4(n1.w, a));
+        out[1][0] = make_uint4(mul4(n0.x, b), mul4(n0.y, b), mul4(n0.z, b), mul4(n0.w, b));
+        out[1][1] = make_uint4(mul4(n1.x, b), mul4(n1.y, b), mul4(n1.z, b), mul4(n1.w, b));
+    } else {
+        const uint4 nib[2] = {n0, n1};
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t qh = h ? r.qh.y : r.qh.x;
+            const uint4 q = make_uint4(nib[h].x | ((qh & 0x03030303u) << 4), nib[h].y | (((qh >> 2) & 0x03030303u) << 4),
+                                       nib[h].z | (((qh >> 4) & 0x03030303u) << 4),
+                                       nib[h].w | (((qh >> 6) & 0x03030303u) << 4));
+            const short s = short(int8_t((r.sc2 >> (8 * h)) & 0xFF));
+            const v2s scv = {s, s}, off = {short(-32 * s), short(-32 * s)};
+            split6(q.x, scv, off, out[0][h].x, out[1][h].x);
+            split6(q.y, scv, off, out[0][h].y, out[1][h].y);
+            split6(q.z, scv, off, out[0][h].z, out[1][h].z);
+            split6(q.w, scv, off, out[0][h].w, out[1][h].w);
+        }
+    }
+}
+
+template <uint32_t T, int WT, int WR>
+__global__ __launch_bounds__(64 * WT * WR) __attribute__((amdgpu_waves_per_eu(2))) void gemm_kq_kernel(
+    GemmGroup G, ActPtrs A, int n_in, int n_tok, int tok_tiles) {
+    constexpr int NW = WT * WR;
+    constexpr int RWG = 32 * WR;                      // rows per workgroup
+    constexpr int ITEMS = RWG * SSTEPS;               // (row, step) items per stage
+    constexpr int IPT = (ITEMS + 64 * NW - 1) / (64 * NW);
+    constexpr int SHIFT = (T == kQ4_K) ? 3 : 6;
+    // [stage][plane][step][half][row] of 16-byte pieces
+    __shared__ uint4 s_b[RING * 2 * SSTEPS * 2 * RWG];
+    // per super-block epilogue data, loaded during its first stage:
+    // row meta (Q4_K d, dmin, scales; Q6_K d in .x), token scales, mins operands
+    __shared__ uint4 s_meta[RWG];
+    __shared__ float4 s_xd[2 * WT * 2 * 4];
+    __shared__ uint4 s_j[(T == kQ4_K) ? 2 * WT * 64 : 1];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int l32 = lane & 31, half = lane >> 5;
-    const int row0 = int(blockIdx.x) * BN, tok0 = int(blockIdx.y) * BM;
-    const int wr0 = (wave % WN) * 64;  // wavefront's rows within the tile
-    const int wt0 = (wave / WN) * 64;  // wavefront's tokens within the tile
-    const int groups = n_in / 32, n_sb = n_in / 256;
-    const int steps = n_in / KS;
-    constexpr int SPS = 256 / KS;  // steps per super-block
+    const int wt = wave % WT, wr = wave / WT;
 
-    // ---- global -> registers for step k
-    auto load_stage = [&](int k, S& st) {
-        const int sb = k / SPS;
+    // tile of this workgroup: consecutive tiles of one row range share an XCD
+    // (workgroups are dealt to the eight XCDs round-robin)
+    const int n_wg = G.tiles_end[G.n - 1] * tok_tiles;
+    int lin = int(blockIdx.x);
+    if ((n_wg & 7) == 0) lin = (lin & 7) * (n_wg >> 3) + (lin >> 3);
+    int row_tile = lin / tok_tiles;
+    const int tok_tile = lin % tok_tiles;
+    // the group member this row tile belongs to
+    int gm = 0;
 #pragma unroll
-        for (int j = 0; j < S::A_VECS; ++j) {
-            const int idx = tid + 256 * j;           // 16-byte chunk of the BM x KS tile
-            const int tl = idx / (KS / 16), cb = (idx % (KS / 16)) * 16;
-            const int t = tok0 + tl;
-            st.act[j] = make_uint4(0, 0, 0, 0);
-            if (t < n_tok) st.act[j] = *reinterpret_cast<const uint4*>(A.q256 + size_t(t) * n_in + size_t(k) * KS + cb);
-        }
+    for (int j = 1; j < kGemmGroupMax; ++j)
+        if (j < G.n && row_tile >= G.tiles_end[j - 1]) gm = j;
+    if (gm > 0) row_tile -= G.tiles_end[gm - 1];
+    const WeightPtrs W = G.w[gm];
+    const int n_out = G.n_out[gm], ldy = G.ldy[gm];
+    float* __restrict__ y = G.y[gm];
+    const int row0 = row_tile * RWG;
+
+    const int steps = n_in / 32, stages = steps / SSTEPS, n_sb = n_in / 256;
+    const int tb0 = tok_tile * (2 * WT) + wt * 2;    // first 32-token block of the wavefront
+    int tb[2];
+    tb[0] = min(tb0, A.n_tb - 1);
+    tb[1] = min(tb0 + 1, A.n_tb - 1);
+    const int my_row = row0 + wr * 32 + l32;         // the lane's output row
+
+    // dequantisation items of this thread: item = tid + 64 NW j -> (row, step)
+    int it_row[IPT], it_step[IPT];
+    bool it_on[IPT];
 #pragma unroll
-        for (int j = 0; j < S::W_HALVES; ++j) {
-            const int u = tid + 256 * j;              // (row, group-in-step, half)
-            const int r = u >> 2, gl = (u >> 1) & 1, h = u & 1;
-            const int row = row0 + r, c = k * 2 + gl;
-            st.codes[j] = make_uint4(0, 0, 0, 0);
-            st.qh[j] = 0;
-            st.sc[j] = 0;
-            if (row < n_out) {
-                st.codes[j] = *reinterpret_cast<const uint4*>(W.codes + (size_t(row) * groups + c) * 16);
-                if constexpr (T == kQ4_K) {
-                    const uint4 m = *reinterpret_cast<const uint4*>(W.aux + (size_t(row) * n_sb + sb) * 16);
-                    int scv, mn;
-                    k4_scale_min(m.y, m.z, m.w, c & 7, scv, mn);
-                    st.sc[j] = scv;
-                } else {
-                    st.qh[j] = *reinterpret_cast<const uint32_t*>(W.aux + (size_t(row) * groups + c) * 8 + 4 * h);
-                    st.sc[j] = int(W.sc[size_t(row) * (n_in / 16) + 2 * c + h]);
-                }
+    for (int j = 0; j < IPT; ++j) {
+        const int item = tid + 64 * NW * j;
+        it_on[j] = item < ITEMS;
+        const int it = it_on[j] ? item : 0;
+        it_row[j] = it >> 2;
+        it_step[j] = it & 3;
+    }
+    auto lds_at = [&](int st, int plane, int s, int h, int r) {
+        return (((st * 2 + plane) * SSTEPS + s) * 2 + h) * RWG + (r ^ (s << 2));
+    };
+    auto load_stage = [&](Raw (&raw)[IPT], int stage) {
+#pragma unroll
+        for (int j = 0; j < IPT; ++j)
+            load_raw<T>(raw[j], W, min(row0 + it_row[j], n_out - 1), stage * SSTEPS + it_step[j], n_in);
+    };
+    auto store_stage = [&](const Raw (&raw)[IPT], int stage, int slot) {
+#pragma unroll
+        for (int j = 0; j < IPT; ++j) {
+            if constexpr (ITEMS % (64 * NW) != 0) {
+                if (!it_on[j]) continue;
             }
-        }
-        if (k % SPS == 0 && tid < BM) {
-            const int t = tok0 + tid;
-            st.xd = 0.0f;
-            st.bsm = make_uint4(0, 0, 0, 0);
-            if (t < n_tok) {
-                st.xd = A.d256[size_t(t) * n_sb + sb];
-                if constexpr (T == kQ4_K)
-                    st.bsm = *reinterpret_cast<const uint4*>(A.bsm + (size_t(t) * n_sb + sb) * 16);
-            }
+            uint4 o[2][2];
+            dequant<T>(raw[j], stage * SSTEPS + it_step[j], o);
+#pragma unroll
+            for (int p = 0; p < 2; ++p)
+#pragma unroll
+                for (int h = 0; h < 2; ++h) s_b[lds_at(slot, p, it_step[j], h, it_row[j])] = o[p][h];
         }
     };
-
-    // ---- registers -> LDS buffer b (weights dequantised to the hi/lo planes)
-    auto store_stage = [&](int k, const S& st, int b) {
+    // A operand of (block b, step s of a stage): 1 KB pieces, lane-contiguous;
+    // a uniform stage base plus a per-lane offset and an immediate
+    const uint4* gA = reinterpret_cast<const uint4*>(A.gA);
+    int a_off[2];
 #pragma unroll
-        for (int j = 0; j < S::A_VECS; ++j) {
-            const int idx = tid + 256 * j;
-            const int tl = idx / (KS / 16), cb = (idx % (KS / 16)) * 16;
-            *reinterpret_cast<uint4*>(&s_act[b][tl * P + cb]) = st.act[j];
-        }
+    for (int b = 0; b < 2; ++b) a_off[b] = tb[b] * steps * 64 + lane;
+    auto load_a = [&](v4i (&a)[2][SSTEPS], int stage) {
+        const uint4* base = gA + size_t(stage) * (SSTEPS * 64);
 #pragma unroll
-        for (int j = 0; j < S::W_HALVES; ++j) {
-            const int u = tid + 256 * j;
-            const int r = u >> 2, gl = (u >> 1) & 1, h = u & 1;
-            const uint4 w = st.codes[j];
-            uint4 n;  // the 16 codes of this half, element order
-            if (h == 0) n = make_uint4(w.x & 0x0F0F0F0Fu, w.y & 0x0F0F0F0Fu, w.z & 0x0F0F0F0Fu, w.w & 0x0F0F0F0Fu);
-            else n = make_uint4((w.x >> 4) & 0x0F0F0F0Fu, (w.y >> 4) & 0x0F0F0F0Fu, (w.z >> 4) & 0x0F0F0F0Fu,
-                                (w.w >> 4) & 0x0F0F0F0Fu);
-            short off = 0;
-            if constexpr (T == kQ6_K) {
-                const uint32_t q = st.qh[j];
-                n.x |= (q & 0x03030303u) << 4;
-                n.y |= ((q >> 2) & 0x03030303u) << 4;
-                n.z |= ((q >> 4) & 0x03030303u) << 4;
-                n.w |= ((q >> 6) & 0x03030303u) << 4;
-                off = 32;
-            }
-            const v2s offv = {off, off}, scv = {short(st.sc[j]), short(st.sc[j])};
-            uint4 hi, lo;
-            split4<SHIFT>(n.x, offv, scv, hi.x, lo.x);
-            split4<SHIFT>(n.y, offv, scv, hi.y, lo.y);
-            split4<SHIFT>(n.z, offv, scv, hi.z, lo.z);
-            split4<SHIFT>(n.w, offv, scv, hi.w, lo.w);
-            *reinterpret_cast<uint4*>(&s_hi[b][r * P + gl * 32 + h * 16]) = hi;
-            *reinterpret_cast<uint4*>(&s_lo[b][r * P + gl * 32 + h * 16]) = lo;
-        }
-        if (k % SPS == 0 && tid < BM) {
-            const int p = (k / SPS) & 1;
-            s_xd[p][tid] = st.xd;
-            *reinterpret_cast<uint4*>(&s_bsm[p][tid * 16]) = st.bsm;
-        }
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int s = 0; s < SSTEPS; ++s) a[b][s] = __builtin_bit_cast(v4i, base[a_off[b] + s * 64]);
     };
 
-    float facc[2][2][16];
+    v16i accH[2], accL[2];
+    v16f accY[2];
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
-#pragma unroll
-        for (int c = 0; c < 2; ++c)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) facc[a][c][r] = 0.0f;
-    v16i cH[2][2], cL[2][2];
-
-    S st;
-    load_stage(0, st);
-    store_stage(0, st, 0);
-    __syncthreads();
-
-    for (int k = 0; k < steps; ++k) {
-        const int b = k & 1;
-        if (k % SPS == 0) {
-#pragma unroll
-            for (int a = 0; a < 2; ++a)
-#pragma unroll
-                for (int c = 0; c < 2; ++c) {
-                    cH[a][c] = v16i{};
-                    cL[a][c] = v16i{};
-                }
-        }
-        if (k + 1 < steps) load_stage(k + 1, st);  // in flight during the MFMAs below
-
-#pragma unroll
-        for (int gl = 0; gl < 2; ++gl) {
-            const int ko = gl * 32 + half * 16;
-            v4i av[2], bh[2], bl[2];
-#pragma unroll
-            for (int tb = 0; tb < 2; ++tb)
-                av[tb] = *reinterpret_cast<const v4i*>(&s_act[b][(wt0 + 32 * tb + l32) * P + ko]);
-#pragma unroll
-            for (int rb = 0; rb < 2; ++rb) {
-                bh[rb] = *reinterpret_cast<const v4i*>(&s_hi[b][(wr0 + 32 * rb + l32) * P + ko]);
-                bl[rb] = *reinterpret_cast<const v4i*>(&s_lo[b][(wr0 + 32 * rb + l32) * P + ko]);
-            }
-#pragma unroll
-            for (int tb = 0; tb < 2; ++tb)
-#pragma unroll
-                for (int rb = 0; rb < 2; ++rb) {
-                    cH[tb][rb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[tb], bh[rb], cH[tb][rb], 0, 0, 0);
-                    cL[tb][rb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[tb], bl[rb], cL[tb][rb], 0, 0, 0);
-                }
-        }
-
-        if (k % SPS == SPS - 1) {
-            // super-block epilogue. C layout (32x32 i32): lane l, register r
-            // -> token 8*(r/4) + 4*(l/32) + r%4 of the block, row l%32.
-            const int sb = k / SPS, p = sb & 1;
-#pragma unroll
-            for (int rb = 0; rb < 2; ++rb) {
-                const int row = row0 + wr0 + 32 * rb + l32;
-                float d = 0.0f, dmin = 0.0f;
-                uint64_t mins = 0;
-                if (row < n_out) {
-                    if constexpr (T == kQ4_K) {
-                        const uint4 m = *reinterpret_cast<const uint4*>(W.aux + (size_t(row) * n_sb + sb) * 16);
-                        d = f16_bits_to_f32(uint16_t(m.x & 0xFFFF));
-                        dmin = f16_bits_to_f32(uint16_t(m.x >> 16));
-#pragma unroll
-                        for (int g = 0; g < 8; ++g) {
-                            int scv, mn;
-                            k4_scale_min(m.y, m.z, m.w, g, scv, mn);
-                            mins |= uint64_t(mn) << (8 * g);
-                        }
-                    } else {
-                        d = f16_bits_to_f32(W.d[size_t(row) * n_sb + sb]);
-                    }
-                }
-#pragma unroll
-                for (int tb = 0; tb < 2; ++tb) {
-                    v16i I;
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) I[r] = (cH[tb][rb][r] << SHIFT) + cL[tb][rb][r];
-                    if constexpr (T == kQ4_K) {
-                        const long aj = *reinterpret_cast<const long*>(&s_bsm[p][(wt0 + 32 * tb + l32) * 16 + 8 * half]);
-                        const long bjh = half ? 0 : long(mins);
-                        const long bjl = half ? long(mins) : 0;
-                        v16i J = __builtin_amdgcn_mfma_i32_32x32x16_i8(aj, bjh, v16i{}, 0, 0, 0);
-#pragma unroll
-                        for (int r = 0; r < 16; ++r) J[r] <<= 6;
-                        J = __builtin_amdgcn_mfma_i32_32x32x16_i8(aj, bjl, J, 0, 0, 0);
-#pragma unroll
-                        for (int r = 0; r < 16; ++r) {
-                            const int tl = wt0 + 32 * tb + 8 * (r >> 2) + 4 * half + (r & 3);
-                            facc[tb][rb][r] += s_xd[p][tl] * (d * float(I[r]) - dmin * float(J[r]));
-                        }
-                    } else {
-#pragma unroll
-                        for (int r = 0; r < 16; ++r) {
-                            const int tl = wt0 + 32 * tb + 8 * (r >> 2) + 4 * half + (r & 3);
-                            facc[tb][rb][r] += (d * s_xd[p][tl]) * float(I[r]);
-                        }
-                    }
-                }
-            }
-        }
-
-        if (k + 1 < steps) store_stage(k + 1, st, b ^ 1);
-        __syncthreads();
+    for (int b = 0; b < 2; ++b) {
+        accH[b] = v16i{};
+        accL[b] = v16i{};
+        accY[b] = v16f{};
     }
 
+    // MFMAs of one stage; each step's A registers are refilled with the same
+    // step of stage `next` as soon as its MFMAs are issued (one A buffer)
+    auto compute_stage = [&](v4i (&a)[2][SSTEPS], int slot, int next) {
+        const uint4* base = gA + size_t(next) * (SSTEPS * 64);
 #pragma unroll
-    for (int tb = 0; tb < 2; ++tb)
+        for (int s = 0; s < SSTEPS; ++s) {
+            const v4i bh = __builtin_bit_cast(v4i, s_b[lds_at(slot, 0, s, half, wr * 32 + l32)]);
+            const v4i bl = __builtin_bit_cast(v4i, s_b[lds_at(slot, 1, s, half, wr * 32 + l32)]);
 #pragma unroll
-        for (int rb = 0; rb < 2; ++rb) {
-            const int row = row0 + wr0 + 32 * rb + l32;
-            if (row >= n_out) continue;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int t = tok0 + wt0 + 32 * tb + 8 * (r >> 2) + 4 * half + (r & 3);
-                if (t < n_tok) y[size_t(t) * ldy + row] = facc[tb][rb][r];
+            for (int b = 0; b < 2; ++b) {
+                accH[b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[b][s], bh, accH[b], 0, 0, 0);
+                accL[b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[b][s], bl, accL[b], 0, 0, 0);
+                a[b][s] = __builtin_bit_cast(v4i, base[a_off[b] + s * 64]);
             }
         }
+    };
+
+    // epilogue data of super-block sb: global -> registers (issued with its
+    // first stage) -> LDS (after that stage's MFMAs)
+    constexpr int EJ = (T == kQ4_K) ? 2 * WT * 64 : 0;  // mins-operand pieces
+    constexpr int EX = 2 * WT * 2 * 4;                   // token-scale pieces
+    uint4 e_meta = make_uint4(0, 0, 0, 0), e_j = make_uint4(0, 0, 0, 0);
+    float4 e_x = make_float4(0.f, 0.f, 0.f, 0.f);
+    const int e_tb = min(tok_tile * (2 * WT) + (tid >> 6) % (2 * WT), A.n_tb - 1);
+    // every thread loads and stores (duplicate copies of the same values):
+    // no divergent branch, so no wait for all outstanding loads
+    auto load_epi = [&](int sb) {
+        const size_t r = size_t(min(row0 + tid % RWG, n_out - 1));
+        if constexpr (T == kQ4_K) e_meta = *reinterpret_cast<const uint4*>(W.aux + (r * n_sb + sb) * 16);
+        else e_meta.x = W.d[r * n_sb + sb];
+        if constexpr (T == kQ4_K)
+            e_j = *reinterpret_cast<const uint4*>(A.gJ + ((size_t(e_tb) * n_sb + sb) * 64 + lane) * 8);
+        const int xi = tid % EX, b = xi >> 3, q = xi & 7;  // block of the workgroup, 16-byte piece of its 128 bytes
+        const int tbb = min(tok_tile * (2 * WT) + b, A.n_tb - 1);
+        e_x = reinterpret_cast<const float4*>(A.gX + (size_t(tbb) * n_sb + sb) * 32)[q];
+    };
+    auto store_epi = [&]() {
+        s_meta[tid % RWG] = e_meta;
+        if constexpr (T == kQ4_K) s_j[tid % EJ] = e_j;
+        s_xd[tid % EX] = e_x;
+    };
+
+    // super-block epilogue: y += xd * (d * I - dmin * J)   (Q6_K: y += xd * (d * I))
+    auto epilogue = [&]() {
+        float d, dmin = 0.0f;
+        v8h bj;
+        const uint4 m = s_meta[wr * 32 + l32];
+        if constexpr (T == kQ4_K) {
+            d = f16_bits_to_f32(uint16_t(m.x & 0xFFFF));
+            dmin = f16_bits_to_f32(uint16_t(m.x >> 16));
+            const _Float16 f = half ? _Float16(1.0f) : _Float16(64.0f);
+#pragma unroll
+            for (int g = 0; g < 8; ++g) {
+                int scv, mn;
+                k4_scale_min(m.y, m.z, m.w, g, scv, mn);
+                bj[g] = _Float16(float(mn)) * f;
+            }
+        } else {
+            d = f16_bits_to_f32(uint16_t(m.x));
+        }
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            const int wb = wt * 2 + b;  // block index within the workgroup
+            float xd[16];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float4 v = s_xd[wb * 8 + half * 4 + q];
+                xd[4 * q] = v.x; xd[4 * q + 1] = v.y; xd[4 * q + 2] = v.z; xd[4 * q + 3] = v.w;
+            }
+            v16f J = v16f{};
+            if constexpr (T == kQ4_K) {
+                const v8h aj = __builtin_bit_cast(v8h, s_j[wb * 64 + lane]);
+                J = __builtin_amdgcn_mfma_f32_32x32x16_f16(aj, bj, v16f{}, 0, 0, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const float fi = float((accH[b][i] << SHIFT) + accL[b][i]);
+                float t = d * fi;
+                if constexpr (T == kQ4_K) t = fmaf(-dmin, J[i], t);
+                accY[b][i] = fmaf(xd[i], t, accY[b][i]);
+            }
+            accH[b] = v16i{};
+            accL[b] = v16i{};
+        }
+    };
+
+    // ---- prologue: stages 0 and 1 into the ring, stage 2 raw in registers
+    Raw raw0[IPT], raw1[IPT];
+    load_stage(raw0, 0);
+    load_stage(raw1, min(1, stages - 1));
+    store_stage(raw0, 0, 0);
+    store_stage(raw1, 1, 1);
+    load_stage(raw0, min(2, stages - 1));
+    v4i a0[2][SSTEPS];
+    load_a(a0, 0);
+
+    // ---- main loop, one super-block (two stages) per iteration; stage i
+    // computes from slot i % 3, prefetches raw(i + 3) and A(i + 1), and
+    // dequantises raw(i + 2) into slot (i + 2) % 3.
+    int slot = 0;
+    for (int i = 0; i < stages; i += 2) {
+        // even stage i: raw0 holds stage i + 2
+        __syncthreads();
+        load_epi(i >> 1);
+        load_stage(raw1, min(i + 3, stages - 1));
+        compute_stage(a0, slot, i + 1);
+        {
+            const int ns = slot + 2 >= RING ? slot + 2 - RING : slot + 2;
+            store_stage(raw0, i + 2, ns);
+        }
+        store_epi();
+        slot = slot + 1 == RING ? 0 : slot + 1;
+        // odd stage i + 1: raw1 holds stage i + 3
+        __syncthreads();
+        load_stage(raw0, min(i + 4, stages - 1));
+        compute_stage(a0, slot, min(i + 2, stages - 1));
+        {
+            const int ns = slot + 2 >= RING ? slot + 2 - RING : slot + 2;
+            store_stage(raw1, i + 3, ns);
+        }
+        slot = slot + 1 == RING ? 0 : slot + 1;
+        epilogue();
+    }
+
+    // ---- store: lane owns row my_row, register i of block b is token 8 (i / 4) + 4 half + i % 4
+    if (my_row < n_out) {
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int t = (tb0 + b) * 32 + 8 * (i >> 2) + 4 * half + (i & 3);
+                if (t < n_tok) y[size_t(t) * ldy + my_row] = accY[b][i];
+            }
+    }
 }
 
-template <uint32_t T, int BN, int BM>
-hipError_t gemm_launch(const WeightPtrs& W, const ActPtrs& A, int n_in, int n_out, int n_tok, float* y, int ldy,
-                       hipStream_t s) {
-    const dim3 grid(unsigned((n_out + BN - 1) / BN), unsigned((n_tok + BM - 1) / BM));
-    hipLaunchKernelGGL((gemm_kq_kernel<T, BN, BM>), grid, dim3(256), 0, s, W, A, n_in, n_out, n_tok, y, ldy);
+template <uint32_t T, int WT, int WR>
+hipError_t gemm_launch(GemmGroup G, const int* n_outs, const ActPtrs& A, int n_in, int n_tok, hipStream_t s) {
+    int tiles = 0;
+    for (int j = 0; j < G.n; ++j) {
+        tiles += (n_outs[j] + 32 * WR - 1) / (32 * WR);
+        G.tiles_end[j] = tiles;
+    }
+    const int tok_tiles = (n_tok + 64 * WT - 1) / (64 * WT);
+    hipLaunchKernelGGL((gemm_kq_kernel<T, WT, WR>), dim3(unsigned(tiles * tok_tiles)), dim3(64 * WT * WR), 0, s, G, A,
+                       n_in, n_tok, tok_tiles);
     return hipGetLastError();
-}
-
-// Tile choice: 64 rows x 256 tokens shares each dequantised weight tile with
-// the most tokens; 128 x 128 when that would leave too few workgroups.
-template <uint32_t T>
-hipError_t gemm_pick(const WeightPtrs& W, const ActPtrs& A, int n_in, int n_out, int n_tok, float* y, int ldy,
-                     hipStream_t s) {
-    const long wide = long((n_out + 63) / 64) * ((n_tok + 255) / 256);
-    if (n_tok > 128 && wide >= 384) return gemm_launch<T, 64, 256>(W, A, n_in, n_out, n_tok, y, ldy, s);
-    return gemm_launch<T, 128, 128>(W, A, n_in, n_out, n_tok, y, ldy, s);
 }
 
 }  // namespace
 
-hipError_t launch_gemm(const void* w, const WeightLayout& WL, const void* act, int n_tok, float* y, int ldy,
-                       hipStream_t s) {
-    const ActLayout AL = act_layout(n_tok, WL.n_in);
-    if (!WL.total || !AL.total || !AL.has256 || n_tok <= 0) return hipErrorInvalidValue;
-    const WeightPtrs W = weight_ptrs(w, WL);
+hipError_t launch_gemm_group(int n, const void* const* ws, const WeightLayout* WLs, const void* act, int n_tok,
+                             float* const* ys, const int* ldys, hipStream_t s) {
+    if (n <= 0 || n > kGemmGroupMax || n_tok <= 0) return hipErrorInvalidValue;
+    const uint32_t type = WLs[0].type;
+    const int n_in = WLs[0].n_in;
+    const ActLayout AL = act_layout(n_tok, n_in);
+    if (!AL.total || !AL.has256) return hipErrorInvalidValue;
+    GemmGroup G{};
+    G.n = n;
+    int n_outs[kGemmGroupMax];
+    for (int j = 0; j < n; ++j) {
+        if (!WLs[j].total || WLs[j].type != type || WLs[j].n_in != n_in) return hipErrorInvalidValue;
+        G.w[j] = weight_ptrs(ws[j], WLs[j]);
+        G.n_out[j] = n_outs[j] = WLs[j].n_out;
+        G.y[j] = ys[j];
+        G.ldy[j] = ldys[j];
+    }
     const ActPtrs A = act_ptrs(act, AL);
-    switch (WL.type) {
-        case kQ4_K: return gemm_pick<kQ4_K>(W, A, WL.n_in, WL.n_out, n_tok, y, ldy, s);
-        case kQ6_K: return gemm_pick<kQ6_K>(W, A, WL.n_in, WL.n_out, n_tok, y, ldy, s);
+    switch (type) {
+        case kQ4_K: return gemm_launch<kQ4_K, 2, 2>(G, n_outs, A, n_in, n_tok, s);
+        case kQ6_K: return gemm_launch<kQ6_K, 2, 2>(G, n_outs, A, n_in, n_tok, s);
         default: return hipErrorInvalidValue;
     }
+}
+
+hipError_t launch_gemm(const void* w, const WeightLayout& WL, const void* act, int n_tok, float* y, int ldy,
+                       hipStream_t s) {
+    return launch_gemm_group(1, &w, &WL, act, n_tok, &y, &ldy, s);
 }
 
 }  // namespace fishhip

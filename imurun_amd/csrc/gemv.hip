@@ -6,16 +6,15 @@
 // row's 32-element groups sub, sub+LPR, ... so one load instruction of the
 // wavefront covers LPR consecutive 16-byte chunks of a row. The lane computes
 // each group's exact integer dot (dots.h) and scales it in f32; the LPR
-// partial sums are reduced with cross-lane shuffles at the end. Each
-// wavefront walks several rows with their loads issued together; for a single
-// token its activation groups are loaded once into registers, otherwise they
-// are read through the caches. The weights stream past once.
+// partial sums are reduced with cross-lane shuffles at the end. A wavefront
+// reads its rows once, with every load issued before the first use.
 //
 // Also here: the per-block integer dump used by the parity tests, built from
 // the same dots.h functions.
 #include "common.h"
 #include "dots.h"
 #include "kernels.h"
+#include "qact.h"
 
 namespace fishhip {
 
@@ -106,29 +105,33 @@ __device__ __forceinline__ float group_dot(const Frag& f, const ActFrag& a) {
     }
 }
 
-// Wavefront-row scheme: LPR lanes per row; a wavefront owns RPW = 64/LPR
-// interleaved rows per pass and `rpw` passes, RB passes at a time with all of
-// their weight loads in flight together. Lane `sub` covers groups
-// sub, sub + LPR, ... (at most MAXC of them). For one token the lane's
-// activation groups stay in registers for every row of the wavefront.
-// blockIdx.y selects up to NT tokens: consecutive rows of the batch, or one
-// item of an expert work list (TokenMap).
+// One-shot wavefront scheme: LPR lanes per row; a wavefront owns RB passes of
+// RPP = 64/LPR interleaved rows and reads each of them exactly once. Lane
+// `sub` covers groups sub, sub + LPR, ... (MAXC of them). Every load of the
+// wavefront is unconditional -- out-of-range rows and groups read a clamped,
+// valid address and their contribution is zeroed with a select -- so all of
+// its weight (and, for one token, activation) loads are in flight together
+// instead of being serialised by per-load branches. For one token the lane's
+// activation groups are loaded once into registers; for more tokens they are
+// read per token through the caches. blockIdx.y selects up to NT tokens:
+// consecutive rows of the batch, or one item of an expert work list (TokenMap).
 template <uint32_t T, int NT, int LPR, int MAXC, int RB>
-__global__ __launch_bounds__(256) void gemv_kernel(WeightPtrs W, ActPtrs A, int n_in, int n_out, int n_tok, int rpw,
+__global__ __launch_bounds__(256) void gemv_kernel(WeightPtrs W, ActPtrs A, int n_in, int n_out, int n_tok,
                                                    TokenMap map, float* __restrict__ y, int ldy) {
-    constexpr int RPW = 64 / LPR;
+    constexpr int RPP = 64 / LPR;
     const int lane = threadIdx.x & 63;
     const int sub = lane % LPR;
     const int wave_id = int(blockIdx.x) * 4 + int(threadIdx.x >> 6);
-    const int row_base = wave_id * rpw * RPW + lane / LPR;
+    const int row_base = wave_id * (RPP * RB) + lane / LPR;
+    if (wave_id * (RPP * RB) >= n_out) return;  // uniform over the wavefront
     const int groups = n_in / 32;
 
     int s0, cnt;
-    size_t wrow0 = 0;  // first weight row of the expert
+    int wrow0 = 0;  // first weight row of the expert
     if (map.items) {
         const int it = int(blockIdx.y);
         if (it >= *map.n_items) return;
-        wrow0 = size_t(map.items[3 * it]) * size_t(n_out);
+        wrow0 = map.items[3 * it] * n_out;
         s0 = map.items[3 * it + 1];
         cnt = map.items[3 * it + 2];
     } else {
@@ -137,59 +140,52 @@ __global__ __launch_bounds__(256) void gemv_kernel(WeightPtrs W, ActPtrs A, int 
     }
     int arow[NT];
 #pragma unroll
-    for (int t = 0; t < NT; ++t) arow[t] = (t < cnt) ? (map.act_row ? map.act_row[s0 + t] : s0 + t) : 0;
+    for (int t = 0; t < NT; ++t) arow[t] = map.act_row ? map.act_row[s0 + min(t, cnt - 1)] : s0 + min(t, cnt - 1);
 
-    ActFrag ac[NT == 1 ? MAXC : 1];
-    if constexpr (NT == 1) {
+    int cg[MAXC];    // clamped group index
+    bool cv[MAXC];   // group exists
 #pragma unroll
-        for (int k = 0; k < MAXC; ++k) {
-            const int c = sub + k * LPR;
-            if (c < groups) ac[k] = load_act<T>(A, arow[0], c, n_in);
-        }
+    for (int k = 0; k < MAXC; ++k) {
+        const int c = sub + k * LPR;
+        cv[k] = c < groups;
+        cg[k] = cv[k] ? c : groups - 1;
     }
 
-    for (int p0 = 0; p0 < rpw; p0 += RB) {
-        Frag f[RB][MAXC];
+    Frag f[RB][MAXC];
 #pragma unroll
-        for (int rb = 0; rb < RB; ++rb) {
-            const int row = row_base + (p0 + rb) * RPW;
+    for (int rb = 0; rb < RB; ++rb) {
+        const int row = wrow0 + min(row_base + rb * RPP, n_out - 1);
+#pragma unroll
+        for (int k = 0; k < MAXC; ++k) f[rb][k] = load_group<T>(W, row, cg[k], n_in);
+    }
+
+    float acc[RB][NT];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[rb][t] = 0.0f;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        ActFrag ac[MAXC];
+#pragma unroll
+        for (int k = 0; k < MAXC; ++k) ac[k] = load_act<T>(A, arow[t], cg[k], n_in);
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
             for (int k = 0; k < MAXC; ++k) {
-                const int c = sub + k * LPR;
-                if (row < n_out && c < groups) f[rb][k] = load_group<T>(W, int(wrow0) + row, c, n_in);
+                const float v = group_dot<T>(f[rb][k], ac[k]);
+                acc[rb][t] += cv[k] ? v : 0.0f;
             }
-        }
+    }
 #pragma unroll
-        for (int rb = 0; rb < RB; ++rb) {
-            const int row = row_base + (p0 + rb) * RPW;
-            float acc[NT];
+    for (int rb = 0; rb < RB; ++rb) {
+        const int row = row_base + rb * RPP;
 #pragma unroll
-            for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
+        for (int t = 0; t < NT; ++t) {
+            float v = acc[rb][t];
 #pragma unroll
-            for (int k = 0; k < MAXC; ++k) {
-                const int c = sub + k * LPR;
-                if (row < n_out && c < groups) {
-                    if constexpr (NT == 1) {
-                        acc[0] += group_dot<T>(f[rb][k], ac[k]);
-                    } else {
-#pragma unroll
-                        for (int t = 0; t < NT; ++t)
-                            if (t < cnt) acc[t] += group_dot<T>(f[rb][k], load_act<T>(A, arow[t], c, n_in));
-                    }
-                }
-            }
-#pragma unroll
-            for (int t = 0; t < NT; ++t) {
-                float v = acc[t];
-#pragma unroll
-                for (int off = LPR / 2; off > 0; off >>= 1) v += __shfl_xor(v, off);
-                acc[t] = v;
-            }
-            if (sub == 0 && row < n_out) {
-#pragma unroll
-                for (int t = 0; t < NT; ++t)
-                    if (t < cnt) y[size_t(s0 + t) * ldy + row] = acc[t];
-            }
+            for (int off = LPR / 2; off > 0; off >>= 1) v += __shfl_xor(v, off);
+            if (sub == 0 && row < n_out && t < cnt) y[size_t(s0 + t) * ldy + row] = v;
         }
     }
 }
@@ -230,19 +226,24 @@ __global__ void block_ints_kernel(WeightPtrs W, ActPtrs A, int n_in, int n_out, 
     }
 }
 
+// Rows per wavefront: about BYTES of weights in flight per lane.
+template <uint32_t T, int MAXC, int BYTES = 64>
+constexpr int gemv_rb() {
+    constexpr int per_group = (T == kQ8_0) ? 32 : 16;
+    constexpr int rb = BYTES / (per_group * MAXC);
+    return rb < 1 ? 1 : (rb > 8 ? 8 : rb);
+}
+
 template <uint32_t T, int NT, int LPR, int MAXC>
 hipError_t gemv_launch(const WeightPtrs& W, const ActPtrs& A, int n_in, int n_out, int n_tok, const TokenMap& map,
                        int y_blocks, float* y, int ldy, hipStream_t s) {
-    constexpr int RPW = 64 / LPR;
-    constexpr int RB = (NT == 1) ? (MAXC <= 2 ? 4 : (MAXC <= 4 ? 2 : 2)) : 1;
-    // passes per wavefront: enough rows that ~4096 wavefronts cover the matrix
-    const int row_groups = (n_out + RPW - 1) / RPW;
-    const int rpw = RB * ((row_groups + RB * 4096 - 1) / (RB * 4096));
-    const int waves = (row_groups + rpw - 1) / rpw;
+    constexpr int RB = gemv_rb<T, MAXC>();
+    constexpr int RPW = (64 / LPR) * RB;
+    const int waves = (n_out + RPW - 1) / RPW;
     const unsigned gy = map.items ? unsigned(y_blocks) : unsigned((n_tok + NT - 1) / NT);
     const dim3 grid(unsigned((waves + 3) / 4), gy);
-    hipLaunchKernelGGL((gemv_kernel<T, NT, LPR, MAXC, RB>), grid, dim3(256), 0, s, W, A, n_in, n_out, n_tok, rpw, map,
-                       y, ldy);
+    hipLaunchKernelGGL((gemv_kernel<T, NT, LPR, MAXC, RB>), grid, dim3(256), 0, s, W, A, n_in, n_out, n_tok, map, y,
+                       ldy);
     return hipGetLastError();
 }
 
@@ -251,34 +252,228 @@ hipError_t gemv_launch(const WeightPtrs& W, const ActPtrs& A, int n_in, int n_ou
     const WeightPtrs &W, const ActPtrs &A, int n_in, int n_out, int n_tok, const TokenMap &map, int y_blocks, \
         float *y, int ldy, hipStream_t s
 
+// groups per lane, rounded up to an instantiated count (extra groups are masked)
 template <uint32_t T, int NT, int LPR>
 hipError_t gemv_pick_maxc(GEMV_PARAMS) {
     const int per_lane = (n_in / 32 + LPR - 1) / LPR;
-    if (per_lane <= 1) return gemv_launch<T, NT, LPR, 1>(GEMV_ARGS);
-    if (per_lane <= 2) return gemv_launch<T, NT, LPR, 2>(GEMV_ARGS);
-    if (per_lane <= 4) return gemv_launch<T, NT, LPR, 4>(GEMV_ARGS);
-    if (per_lane <= 8) return gemv_launch<T, NT, LPR, 8>(GEMV_ARGS);
-    return gemv_launch<T, NT, LPR, 16>(GEMV_ARGS);
+    switch (per_lane) {
+        case 1: return gemv_launch<T, NT, LPR, 1>(GEMV_ARGS);
+        case 2: return gemv_launch<T, NT, LPR, 2>(GEMV_ARGS);
+        case 3: return gemv_launch<T, NT, LPR, 3>(GEMV_ARGS);
+        case 4: return gemv_launch<T, NT, LPR, 4>(GEMV_ARGS);
+        default: break;
+    }
+    if constexpr (LPR == 64) {
+        if (per_lane <= 6) return gemv_launch<T, NT, LPR, 6>(GEMV_ARGS);
+        if (per_lane <= 8) return gemv_launch<T, NT, LPR, 8>(GEMV_ARGS);
+        if (per_lane <= 12) return gemv_launch<T, NT, LPR, 12>(GEMV_ARGS);
+        if (per_lane <= 16) return gemv_launch<T, NT, LPR, 16>(GEMV_ARGS);
+    }
+    return hipErrorInvalidValue;
 }
 
+// lanes per row: all 64 for rows of >= 64 groups, else 16 or 8
 template <uint32_t T, int NT>
 hipError_t gemv_pick_lpr(GEMV_PARAMS) {
     const int groups = n_in / 32;
     if (groups >= 64) return gemv_pick_maxc<T, NT, 64>(GEMV_ARGS);
-    if (groups >= 32) return gemv_pick_maxc<T, NT, 32>(GEMV_ARGS);
     if (groups >= 16) return gemv_pick_maxc<T, NT, 16>(GEMV_ARGS);
     return gemv_pick_maxc<T, NT, 8>(GEMV_ARGS);
 }
 
 // nt: tokens per block (the batch size for plain launches, the item size for
-// expert work lists)
+// expert work lists); larger batches take blocks of four tokens
 template <uint32_t T>
 hipError_t gemv_pick_nt(int nt, GEMV_PARAMS) {
     if (nt <= 1) return gemv_pick_lpr<T, 1>(GEMV_ARGS);
     if (nt <= 2) return gemv_pick_lpr<T, 2>(GEMV_ARGS);
-    if (nt <= 4) return gemv_pick_lpr<T, 4>(GEMV_ARGS);
-    if (nt <= 8) return gemv_pick_lpr<T, 8>(GEMV_ARGS);
-    return gemv_pick_lpr<T, 16>(GEMV_ARGS);
+    return gemv_pick_lpr<T, 4>(GEMV_ARGS);
+}
+
+// ---------------------------------------------------------------- one token, f32 input
+
+// matmul_batch's convenience form (ops.cpp:254-264) for one token: every
+// workgroup (kGemvXWaves wavefronts) quantizes x itself into LDS -- with the
+// quantize kernel's exact arithmetic, so the int8 codes, scales and sums are
+// the same bytes -- and then runs the one-shot GEMV above on them. The x loads go out first, then
+// the workgroup's weight loads, so the quantization waits only for x (from
+// L2) while the weights stream in; no separate quantize launch. Up to
+// kGemmGroupMax tensors on the same x share the grid (gate and up).
+constexpr int kGemvXWaves = 16;
+
+struct GemvXGroup {
+    WeightPtrs w[kGemmGroupMax];
+    float* y[kGemmGroupMax];
+    int n_out[kGemmGroupMax];
+    int wg_end[kGemmGroupMax];  // cumulative workgroups
+    int n;
+};
+
+template <uint32_t T, int LPR, int MAXC, int RB, int XV>
+__global__ __launch_bounds__(64 * kGemvXWaves) void gemv_x_kernel(GemvXGroup G, const float* __restrict__ x,
+                                                                  int n_in) {
+    constexpr bool kq = (T == kQ4_K || T == kQ6_K);
+    constexpr int RPP = 64 / LPR;
+    __shared__ uint4 s_codes[2 * kGemvXMaxGroups];  // [half][group]: elements 16 h .. 16 h + 15
+    __shared__ float s_d[kGemvXMaxGroups];           // Q8Act d per group / Q8ActK d per super-block
+    __shared__ int s_s[kGemvXMaxGroups];             // Q8Act sum per group / the group's two per-16 sums
+
+    const int tid = threadIdx.x, lane = tid & 63, sub = lane % LPR;
+    int gm = 0;
+#pragma unroll
+    for (int j = 1; j < kGemmGroupMax; ++j)
+        if (j < G.n && int(blockIdx.x) >= G.wg_end[j - 1]) gm = j;
+    const int wg = int(blockIdx.x) - (gm ? G.wg_end[gm - 1] : 0);
+    const WeightPtrs W = G.w[gm];
+    const int n_out = G.n_out[gm];
+    const int wave_id = wg * kGemvXWaves + (tid >> 6);
+    const int row_base = wave_id * (RPP * RB) + lane / LPR;
+    const int groups = n_in / 32;
+
+    // x loads first
+    float4 xv[XV];
+#pragma unroll
+    for (int i = 0; i < XV; ++i) {
+        const int k0 = 4 * (tid + 64 * kGemvXWaves * i);
+        xv[i] = k0 < n_in ? *reinterpret_cast<const float4*>(x + k0) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    // then every weight load of the wavefront (clamped, unconditional)
+    int cg[MAXC];
+    bool cv[MAXC];
+#pragma unroll
+    for (int k = 0; k < MAXC; ++k) {
+        const int c = sub + k * LPR;
+        cv[k] = c < groups;
+        cg[k] = cv[k] ? c : groups - 1;
+    }
+    Frag f[RB][MAXC];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+        const int row = min(row_base + rb * RPP, n_out - 1);
+#pragma unroll
+        for (int k = 0; k < MAXC; ++k) f[rb][k] = load_group<T>(W, row, cg[k], n_in);
+    }
+
+    // quantize x into LDS: thread tid takes 4-value chunks tid + 64 kGemvXWaves i
+    uint8_t* codes = reinterpret_cast<uint8_t*>(s_codes);
+#pragma unroll
+    for (int i = 0; i < XV; ++i) {
+        const int k0 = 4 * (tid + 64 * kGemvXWaves * i);
+        const bool active = k0 < n_in;  // whole 32- (K-quants: 256-) value blocks switch together
+        const float4 v = xv[i];
+        const float a = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+        const int g = k0 >> 5, o = k0 & 31;
+        if constexpr (!kq) {
+            const float d = block_d(wave_max8(a)), id = block_id(d);
+            const int q0 = code(v.x, id), q1 = code(v.y, id), q2 = code(v.z, id), q3 = code(v.w, id);
+            const int sum = wave_sum8(q0 + q1 + q2 + q3);
+            if (active) {
+                *reinterpret_cast<uint32_t*>(codes + (size_t((o >> 4) * kGemvXMaxGroups + g) * 16) + (o & 15)) =
+                    pack4(q0, q1, q2, q3);
+                if ((lane & 7) == 0) {
+                    s_d[g] = d;
+                    s_s[g] = sum;
+                }
+            }
+        } else {
+            const float d = block_d(wave_max64(a)), id = block_id(d);
+            const int q0 = code(v.x, id), q1 = code(v.y, id), q2 = code(v.z, id), q3 = code(v.w, id);
+            int g16 = q0 + q1 + q2 + q3;
+            g16 += __shfl_xor(g16, 1);
+            g16 += __shfl_xor(g16, 2);
+            const int g16b = __shfl_xor(g16, 4);
+            if (active) {
+                *reinterpret_cast<uint32_t*>(codes + (size_t((o >> 4) * kGemvXMaxGroups + g) * 16) + (o & 15)) =
+                    pack4(q0, q1, q2, q3);
+                if (lane == 0) s_d[k0 >> 8] = d;
+                if ((lane & 7) == 0) s_s[g] = (g16 & 0xFFFF) | (g16b << 16);
+            }
+        }
+    }
+    __syncthreads();
+    if (wave_id * (RPP * RB) >= n_out) return;  // uniform over the wavefront
+
+    float acc[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) acc[rb] = 0.0f;
+#pragma unroll
+    for (int k = 0; k < MAXC; ++k) {
+        ActFrag ac;
+        ac.a0 = s_codes[cg[k]];
+        ac.a1 = s_codes[kGemvXMaxGroups + cg[k]];
+        if constexpr (!kq) {
+            ac.d = s_d[cg[k]];
+            ac.s = s_s[cg[k]];
+            ac.s2 = 0;
+        } else {
+            ac.d = s_d[cg[k] >> 3];
+            const int s2 = s_s[cg[k]];
+            ac.s = int(int16_t(s2 & 0xFFFF));
+            ac.s2 = s2 >> 16;
+        }
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+            const float v = group_dot<T>(f[rb][k], ac);
+            acc[rb] += cv[k] ? v : 0.0f;
+        }
+    }
+    float* __restrict__ y = G.y[gm];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+        float v = acc[rb];
+#pragma unroll
+        for (int off = LPR / 2; off > 0; off >>= 1) v += __shfl_xor(v, off);
+        const int row = row_base + rb * RPP;
+        if (sub == 0 && row < n_out) y[row] = v;
+    }
+}
+
+template <uint32_t T, int LPR, int MAXC>
+hipError_t gemv_x_launch(GemvXGroup G, const float* x, int n_in, hipStream_t s) {
+    // the plain GEMV's rows per wavefront; one quantization of x serves the
+    // kGemvXWaves wavefronts of a workgroup
+    constexpr int RB = gemv_rb<T, MAXC>();
+    constexpr int RPW = (64 / LPR) * RB;
+    constexpr int TH = 64 * kGemvXWaves;
+    // 4-value chunks per thread: >= n_in / (4 TH) for every n_in of this (LPR, MAXC)
+    constexpr int XV = LPR == 64 ? (64 * 32 * MAXC / 4 + TH - 1) / TH : 1;
+    int wgs = 0;
+    for (int j = 0; j < G.n; ++j) {
+        wgs += ((G.n_out[j] + RPW - 1) / RPW + kGemvXWaves - 1) / kGemvXWaves;
+        G.wg_end[j] = wgs;
+    }
+    hipLaunchKernelGGL((gemv_x_kernel<T, LPR, MAXC, RB, XV>), dim3(unsigned(wgs)), dim3(TH), 0, s, G, x, n_in);
+    return hipGetLastError();
+}
+
+template <uint32_t T, int LPR>
+hipError_t gemv_x_pick_maxc(GemvXGroup G, const float* x, int n_in, hipStream_t s) {
+    const int per_lane = (n_in / 32 + LPR - 1) / LPR;
+    switch (per_lane) {
+        case 1: return gemv_x_launch<T, LPR, 1>(G, x, n_in, s);
+        case 2: return gemv_x_launch<T, LPR, 2>(G, x, n_in, s);
+        case 3: return gemv_x_launch<T, LPR, 3>(G, x, n_in, s);
+        case 4: return gemv_x_launch<T, LPR, 4>(G, x, n_in, s);
+        default: break;
+    }
+    if constexpr (LPR == 64) {
+        switch (per_lane) {
+            case 5: return gemv_x_launch<T, LPR, 5>(G, x, n_in, s);
+            case 6: return gemv_x_launch<T, LPR, 6>(G, x, n_in, s);
+            case 7: return gemv_x_launch<T, LPR, 7>(G, x, n_in, s);
+            case 8: return gemv_x_launch<T, LPR, 8>(G, x, n_in, s);
+            default: break;
+        }
+    }
+    return hipErrorInvalidValue;
+}
+
+template <uint32_t T>
+hipError_t gemv_x_pick(GemvXGroup G, const float* x, int n_in, hipStream_t s) {
+    const int groups = n_in / 32;
+    if (groups >= 64) return gemv_x_pick_maxc<T, 64>(G, x, n_in, s);
+    if (groups >= 16) return gemv_x_pick_maxc<T, 16>(G, x, n_in, s);
+    return gemv_x_pick_maxc<T, 8>(G, x, n_in, s);
 }
 
 }  // namespace
@@ -294,6 +489,7 @@ hipError_t launch_gemv(const void* w, const WeightLayout& WL, const void* act, i
     int nt = n_tok, yb = 0;
     int n_out = WL.n_out;
     if (group) {
+        if (item_tokens <= 0 || item_tokens > kGemvItemTokens) return hipErrorInvalidValue;
         map = *group;
         nt = item_tokens;
         yb = max_items;
@@ -324,6 +520,34 @@ hipError_t launch_block_ints(const void* w, const WeightLayout& WL, const void* 
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
+}
+
+}  // namespace fishhip
+
+namespace fishhip {
+
+bool gemv_x_supported(const WeightLayout& L) {
+    return L.total && L.n_in <= 32 * kGemvXMaxGroups && (!is_kquant(L.type) || L.n_in % 256 == 0);
+}
+
+hipError_t launch_gemv_x(int n, const void* const* ws, const WeightLayout* WLs, const float* x, float* const* ys,
+                         hipStream_t s) {
+    if (n <= 0 || n > kGemmGroupMax || !gemv_x_supported(WLs[0])) return hipErrorInvalidValue;
+    GemvXGroup G{};
+    G.n = n;
+    for (int j = 0; j < n; ++j) {
+        if (!WLs[j].total || WLs[j].type != WLs[0].type || WLs[j].n_in != WLs[0].n_in) return hipErrorInvalidValue;
+        G.w[j] = weight_ptrs(ws[j], WLs[j]);
+        G.y[j] = ys[j];
+        G.n_out[j] = WLs[j].n_out;
+    }
+    switch (WLs[0].type) {
+        case kQ8_0: return gemv_x_pick<kQ8_0>(G, x, WLs[0].n_in, s);
+        case kQ4_0: return gemv_x_pick<kQ4_0>(G, x, WLs[0].n_in, s);
+        case kQ4_K: return gemv_x_pick<kQ4_K>(G, x, WLs[0].n_in, s);
+        case kQ6_K: return gemv_x_pick<kQ6_K>(G, x, WLs[0].n_in, s);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 }  // namespace fishhip

@@ -54,10 +54,19 @@ struct TokenMap {
 
 // Few-token matmul: y[t * ldy + i] for t < n_tok, i < n_out. `act` holds
 // act_rows rows. With `group`, blocks walk at most max_items work-list items
-// of up to item_tokens tokens each.
+// of up to item_tokens (<= kGemvItemTokens) tokens each.
+constexpr int kGemvItemTokens = 4;
 hipError_t launch_gemv(const void* w, const WeightLayout& L, const void* act, int act_rows, int n_tok, float* y,
                        int ldy, hipStream_t stream, const TokenMap* group = nullptr, int item_tokens = 0,
                        int max_items = 0);
+
+// One token, f32 input (matmul_batch's convenience form, ops.cpp:254-264):
+// every workgroup quantizes x into LDS and runs the GEMV on it; n <= 4
+// tensors of one type and n_in on the same x in one launch; y_i [n_out_i].
+constexpr int kGemvXMaxGroups = 512;  // n_in <= 16384
+bool gemv_x_supported(const WeightLayout& L);
+hipError_t launch_gemv_x(int n, const void* const* ws, const WeightLayout* WLs, const float* x, float* const* ys,
+                         hipStream_t stream);
 
 // Few-token matmul on int8 MFMA (16x16x32 tiles), same token mapping as
 // launch_gemv; work-list items of up to kBatchItemTokens tokens. Needs
@@ -71,6 +80,21 @@ hipError_t launch_batch_mfma(const void* w, const WeightLayout& L, const void* a
 // Many-token matmul on int8 MFMA (K-quants).
 hipError_t launch_gemm(const void* w, const WeightLayout& L, const void* act, int n_tok, float* y, int ldy,
                        hipStream_t stream);
+
+// Up to kGemmGroupMax weight tensors of one type and n_in applied to the same
+// activations in one launch (matmul_tensors, ops.cpp:283-299): their row
+// tiles share one grid, so small tensors (k, v) ride along with large ones.
+constexpr int kGemmGroupMax = 4;
+struct GemmGroup {
+    WeightPtrs w[kGemmGroupMax];
+    float* y[kGemmGroupMax];
+    int n_out[kGemmGroupMax];
+    int ldy[kGemmGroupMax];
+    int tiles_end[kGemmGroupMax];  // cumulative row tiles
+    int n;
+};
+hipError_t launch_gemm_group(int n, const void* const* ws, const WeightLayout* WLs, const void* act, int n_tok,
+                             float* const* ys, const int* ldys, hipStream_t stream);
 
 // Per-block integer dots of every row with token 0 of `act`.
 hipError_t launch_block_ints(const void* w, const WeightLayout& L, const void* act, int32_t* out, hipStream_t stream);

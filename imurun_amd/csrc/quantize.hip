@@ -16,39 +16,17 @@
 // values. Lanes 8j..8j+7 form the 32-block j of the chunk.
 #include "common.h"
 #include "kernels.h"
+#include "qact.h"
 
 namespace fishhip {
 
 namespace {
 
-__device__ __forceinline__ float wave_max8(float v) {
-    v = fmaxf(v, __shfl_xor(v, 1));
-    v = fmaxf(v, __shfl_xor(v, 2));
-    v = fmaxf(v, __shfl_xor(v, 4));
-    return v;
-}
-
-__device__ __forceinline__ int wave_sum8(int v) {
-    v += __shfl_xor(v, 1);
-    v += __shfl_xor(v, 2);
-    v += __shfl_xor(v, 4);
-    return v;
-}
-
-__device__ __forceinline__ int code(float x, float id) {
-    const float p = __fmul_rn(x, id);
-    const int q = static_cast<int>(__builtin_rintf(p));
-    return q < -127 ? -127 : (q > 127 ? 127 : q);
-}
-
-__device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
-    return (uint32_t(a) & 0xFF) | ((uint32_t(b) & 0xFF) << 8) | ((uint32_t(c) & 0xFF) << 16) | (uint32_t(d) << 24);
-}
-
 struct QuantOut {
     int8_t* q32; float* d32; int32_t* s32;
     int8_t* q256; float* d256; int16_t* s16; int8_t* bsm;
     int8_t* m32; int8_t* m256;  // MFMA operand order (rows of whole 256-element units)
+    int8_t* gA; float* gX; uint16_t* gJ;  // 32x32x32 MFMA planes (rows padded to 32-token blocks)
     uint8_t* aos32;   // optional FISH Q8Act rows (40 B blocks)
     uint8_t* aos256;  // optional FISH Q8ActK rows (276 B blocks)
 };
@@ -75,10 +53,13 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float* __restrict__
     const int lane = threadIdx.x & 63;
     const int chunks = (n_in + 255) / 256;
     const long wave = long(blockIdx.x) * 4 + (threadIdx.x >> 6);
-    if (wave >= long(n_tok) * chunks) return;
+    // rows beyond n_tok (up to the next 32-token block) only zero-fill the gA/gX/gJ planes
+    const int rows = o.gA ? (n_tok + 31) / 32 * 32 : n_tok;
+    if (wave >= long(rows) * chunks) return;
     const int t = int(wave / chunks), c = int(wave % chunks);
     const int k0 = c * 256 + lane * 4;
-    const bool active = k0 < n_in;  // n_in % 32 == 0: whole 8-lane groups switch together
+    const bool real = t < n_tok;
+    const bool active = real && k0 < n_in;  // n_in % 32 == 0: whole 8-lane groups switch together
     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
     if (active) {
         v = *reinterpret_cast<const float4*>(x + size_t(t) * ldx + k0);
@@ -131,6 +112,21 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float* __restrict__
         g16 += __shfl_xor(g16, 2);
         const int g32 = g16 + __shfl_xor(g16, 4);
         const uint32_t packed = pack4(q0, q1, q2, q3);
+        {
+            // 32x32x32 MFMA planes: token block tb, step k0 / 32, half h, 4-byte slot of the lane
+            const int n_sb = n_in / 256, tb = t >> 5, tt = t & 31;
+            const size_t step = size_t(k0 >> 5), h = size_t((lane & 7) >> 2);
+            *reinterpret_cast<uint32_t*>(o.gA + ((size_t(tb) * (n_in / 32) + step) * 64 + h * 32 + tt) * 16 +
+                                         (lane & 3) * 4) = packed;
+            const size_t blk = size_t(tb) * n_sb + c;
+            if (lane == 0) o.gX[(blk * 2 + ((tt >> 2) & 1)) * 16 + (tt >> 3) * 4 + (tt & 3)] = d;
+            if ((lane & 7) == 0) {
+                const int g = lane >> 3;
+                o.gJ[(blk * 64 + tt) * 8 + g] = __builtin_bit_cast(uint16_t, _Float16(float(g32 >> 6)));
+                o.gJ[(blk * 64 + 32 + tt) * 8 + g] = __builtin_bit_cast(uint16_t, _Float16(float(g32 & 63)));
+            }
+        }
+        if (!real) return;
         *reinterpret_cast<uint32_t*>(o.q256 + size_t(t) * n_in + k0) = packed;
         *reinterpret_cast<uint32_t*>(o.m256 + size_t(t) * n_in + size_t(c) * 256 + mfma_offset(lane)) = packed;
         const size_t sb = size_t(t) * (n_in / 256) + c;
@@ -167,9 +163,12 @@ hipError_t launch_quantize(const float* x, int n_tok, int n_in, int ldx, void* a
     o.bsm = L.has256 ? reinterpret_cast<int8_t*>(b + L.bsm) : nullptr;
     o.m32 = L.has256 ? reinterpret_cast<int8_t*>(b + L.m32) : nullptr;
     o.m256 = L.has256 ? reinterpret_cast<int8_t*>(b + L.m256) : nullptr;
+    o.gA = L.has256 ? reinterpret_cast<int8_t*>(b + L.gA) : nullptr;
+    o.gX = L.has256 ? reinterpret_cast<float*>(b + L.gX) : nullptr;
+    o.gJ = L.has256 ? reinterpret_cast<uint16_t*>(b + L.gJ) : nullptr;
     o.aos32 = static_cast<uint8_t*>(aos32);
     o.aos256 = L.has256 ? static_cast<uint8_t*>(aos256) : nullptr;
-    const long waves = long(n_tok) * ((n_in + 255) / 256);
+    const long waves = long(L.has256 ? L.n_tb * 32 : n_tok) * ((n_in + 255) / 256);
     const unsigned blocks = unsigned((waves + 3) / 4);
     hipLaunchKernelGGL(quantize_kernel, dim3(blocks), dim3(256), 0, stream, x, n_tok, n_in, ldx, o, u, h_out);
     return hipGetLastError();

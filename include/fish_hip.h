@@ -86,6 +86,25 @@ FISH_HIP_API int fish_hip_repack(uint32_t type, const void* gguf, int n_in, int 
 FISH_HIP_API int fish_hip_matmul(uint32_t type, const void* w, const void* act, int n_tok, int n_in, int n_out,
                                  float* y, void* stream);
 
+/* matmul_tensors (ops.cpp:283-299) and ComputeBackend::matmul_group
+ * (backend.h:81-87) on the device: n (<= 4) repacked tensors ws[i] of one
+ * type and n_in applied to the same quantized activations (the q/k/v or
+ * gate/up projections of a layer); ys[i] f32 [n_tok][n_outs[i]]. Many-token
+ * K-quant batches run as one launch whose grid spans all n tensors. */
+FISH_HIP_API int fish_hip_matmul_group(uint32_t type, int n, const void* const* ws, const void* act, int n_tok,
+                                       int n_in, const int* n_outs, float* const* ys, void* stream);
+
+/* matmul_tensors on f32 input (ops.cpp:283-299 with the quantize-then-
+ * multiply of the convenience matmul_batch, ops.cpp:254-264): x f32
+ * [n_tok][n_in] is quantized like ActBatch::quantize and multiplied by the n
+ * (<= 4) tensors ws[i]. One token with n_in <= 16384 is a single launch in
+ * which every workgroup quantizes x itself (no workspace; act_workspace may
+ * be NULL); otherwise act_workspace (fish_hip_act_bytes(n_tok, n_in) bytes)
+ * receives the quantized activations first. */
+FISH_HIP_API int fish_hip_matmul_tensors(uint32_t type, int n, const void* const* ws, const float* x, int n_tok,
+                                         int n_in, const int* n_outs, float* const* ys, void* act_workspace,
+                                         uint64_t act_workspace_bytes, void* stream);
+
 /* The per-block integers of FISH's AVX2 kernels (quant_x86.cpp:280-495) for
  * every row of w against token 0 of act: Q8_0/Q4_0 one int32 per 32-block,
  * Q4_K two per super-block (sum sc*dot, sum m*bsum), Q6_K one per super-block. */

@@ -186,7 +186,75 @@ def test_full_size_shapes(torch_dev, oracle, t, n_out, n_in, n_tok):
     assert np.array_equal(y_part, y[:, :1024])
 
 
+@pytest.mark.parametrize("t,n_tok", [(fh.Q4_K, 130), (fh.Q6_K, 200), (fh.Q4_K, 512), (fh.Q4_K, 3), (fh.Q4_0, 70)])
+def test_matmul_group_matches_single(torch_dev, oracle, t, n_tok):
+    """matmul_group over tensors of different heights (one grouped GEMM launch
+    for many-token K-quants, per-tensor launches otherwise): every output is
+    bit-identical to its own matmul and close to the oracle."""
+    n_in, n_outs = 768, [96, 32, 32, 160]
+    rows = [packed_weights(oracle, t, n, n_in, 1000 + i) for i, n in enumerate(n_outs)]
+    x = normal(1100 + n_tok, (n_tok, n_in))
+    act = fh.quantize(dev_f32(torch_dev, x))
+    ws = [fh.repack(t, dev_u8(torch_dev, r), n_in, n) for r, n in zip(rows, n_outs)]
+    ys = fh.matmul_group(t, ws, act, n_tok, n_in, n_outs)
+    for w, r, n, y in zip(ws, rows, n_outs, ys):
+        single = fh.matmul(t, w, act, n_tok, n_in, n).cpu().numpy()
+        got = y.cpu().numpy()
+        assert np.array_equal(got, single)
+        check_close(got, oracle.matmul_f32(t, r, x, n), f"{fh.TYPE_NAMES[t]} group n_out={n} M={n_tok}")
+
+
+@pytest.mark.parametrize("t", TYPES)
+@pytest.mark.parametrize("n_in", [96, 768, 2048, 4096, 14336])
+def test_matmul_tensors_one_token_fused(torch_dev, oracle, t, n_in):
+    """One token on f32 input: every workgroup quantizes x itself; the outputs
+    are bit-identical to quantize + matmul and close to the oracle."""
+    if t in (fh.Q4_K, fh.Q6_K) and n_in % 256:
+        pytest.skip("K-quants need n_in % 256 == 0")
+    n_outs = [200, 64]
+    rows = [packed_weights(oracle, t, n, n_in, 1400 + i) for i, n in enumerate(n_outs)]
+    x = normal(1500 + n_in, (1, n_in))
+    xd = dev_f32(torch_dev, x)
+    ws = [fh.repack(t, dev_u8(torch_dev, r), n_in, n) for r, n in zip(rows, n_outs)]
+    ys = fh.matmul_tensors(t, ws, xd, n_outs)
+    act = fh.quantize(xd)
+    for w, r, n, y in zip(ws, rows, n_outs, ys):
+        got = y.cpu().numpy()
+        assert np.array_equal(got, fh.matmul(t, w, act, 1, n_in, n).cpu().numpy())
+        check_close(got, oracle.matmul_f32(t, r, x, n), f"{fh.TYPE_NAMES[t]} fused K={n_in}")
+
+
+@pytest.mark.parametrize("t", [fh.Q4_0, fh.Q4_K])
+@pytest.mark.parametrize("n_tok", [3, 130])
+def test_matmul_tensors_batches(torch_dev, oracle, t, n_tok):
+    """More tokens: quantized into the caller's workspace, then the group matmul."""
+    n_in, n_outs = 512, [64, 32]
+    rows = [packed_weights(oracle, t, n, n_in, 1600 + i) for i, n in enumerate(n_outs)]
+    x = normal(1700 + n_tok, (n_tok, n_in))
+    ws = [fh.repack(t, dev_u8(torch_dev, r), n_in, n) for r, n in zip(rows, n_outs)]
+    ys = fh.matmul_tensors(t, ws, dev_f32(torch_dev, x), n_outs)
+    for r, n, y in zip(rows, n_outs, ys):
+        check_close(y.cpu().numpy(), oracle.matmul_f32(t, r, x, n), f"{fh.TYPE_NAMES[t]} tensors M={n_tok}")
+
+
 # ------------------------------------------------------------------ backend surface
+
+def test_backend_matmul_group_grouped_gemm(torch_dev, oracle):
+    """q/k/v-shaped Q4_K tensors at a prefill batch: the backend's grouped launch."""
+    be = fh.HipBackend()
+    n_in, n_outs = 512, {"gq": 128, "gk": 32, "gv": 32}
+    packed = {}
+    for i, (name, n_out) in enumerate(n_outs.items()):
+        packed[name] = packed_weights(oracle, fh.Q4_K, n_out, n_in, 1200 + i)
+        assert be.upload(name, fh.Q4_K, packed[name], n_in, n_out)
+    x = normal(1300, (150, n_in))
+    ys = be.matmul_group(list(n_outs), x, list(n_outs.values()))
+    for (name, n_out), y in zip(n_outs.items(), ys):
+        check_close(y, oracle.matmul_f32(fh.Q4_K, packed[name], x, n_out), f"backend group {name}")
+        assert np.array_equal(be.matmul(name, x, n_out), y)
+    for name in n_outs:
+        be.release(name)
+
 
 def test_backend_upload_matmul_group(torch_dev, oracle):
     be = fh.HipBackend()
