@@ -280,6 +280,45 @@ def run_cpu_baseline(args, step_bytes):
                       f"quantized per call) over {copies} weight copies, {el:.1f} s"}
 
 
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
+COPY_BYTES = 256 << 20
+
+
+def run_kernel_only(args, torch, fh, dev):
+    """For rocprofv3 counter passes: the dominant launch (gate + up on one x,
+    rotating weight copies past the MALL) `--steps` times, then a plain device
+    copy of COPY_BYTES that calibrates FETCH_SIZE / WRITE_SIZE against known bytes."""
+    from imurun_amd.synth import normal
+    t = fh.Q4_0
+    wg = fh.quantize_rows(t, normal(101, (F, E), 0.02))
+    wu = fh.quantize_rows(t, normal(102, (F, E), 0.02))
+    copies = max(2, int(2 * MALL_BYTES // (wg.size + wu.size)) + 2)
+    sets = [tuple(fh.repack(t, torch.from_numpy(a).to(dev), E, F) for a in (wg, wu)) for _ in range(copies)]
+    x = torch.from_numpy(normal(104, (1, E))).to(dev)
+    yg = torch.empty((1, F), dtype=torch.float32, device=dev)
+    yu = torch.empty((1, F), dtype=torch.float32, device=dev)
+    for i in range(args.steps):
+        g, u = sets[i % copies]
+        fh.matmul_tensors(t, [g, u], x, [F, F], ys=[yg, yu])
+    src = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device=dev).fill_(1.0)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"kernel_only": "gemv_x_kernel<Q4_0> gate+up", "launches": args.steps,
+                      "copy_bytes": COPY_BYTES}))
+    return 0
+
+
+def measured_traffic():
+    """HBM bytes per launch of the dominant kernel from the committed counter passes, or None."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            return json.load(f).get("bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -289,6 +328,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
+    ap.add_argument("--kernel-only", action="store_true",
+                    help="run only the dominant launch and a calibration copy (for rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the path shards by rows/experts "
@@ -300,6 +341,8 @@ def main() -> int:
     assert torch.cuda.is_available(), "bench needs a ROCm GPU"
     dev = torch.device("cuda:0")
     fh.load()
+    if args.kernel_only:
+        return run_kernel_only(args, torch, fh, dev)
 
     step_bytes, gate_bytes = gemv_step_bytes()
     elapsed, copies, gate_us = run_gemv(args, torch, fh, dev)
@@ -327,7 +370,7 @@ def main() -> int:
                    "weight_type": "Q4_0", "hbm_pct_of_peak": round(100 * value / HBM_PEAK_GBS, 2)},
         "roofline": {"bound": "hbm", "kernel": "gemv_x_kernel<Q4_0> gate+up 2 x 14336x4096, x quantized in-kernel",
                      "achieved": round(gate_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gate_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(gate_gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "median_kernel_us": round(gate_us, 3), "algorithmic_bytes": gate_bytes},
     }
     if not args.no_extras:
