@@ -64,7 +64,7 @@ struct MoeWork {
     int slots = 0, item_tokens = 1, max_items = 0;
     bool mfma = false;  // expert products on the MFMA batch kernel (else the GEMV)
     size_t sel = 0, wsel = 0, counts = 0, offsets = 0, slot_tok = 0, tok_slot = 0, items = 0, n_items = 0;
-    size_t act_x = 0, g = 0, u = 0, act_h = 0, dn = 0, total = 0;
+    size_t act_x = 0, g = 0, u = 0, act_h = 0, h = 0, dn = 0, total = 0;
 };
 
 MoeWork moe_work(int n_tok, int n_embd, int n_ff, int n_expert, int k) {
@@ -100,6 +100,7 @@ MoeWork moe_work(int n_tok, int n_embd, int n_ff, int n_expert, int k) {
     w.g = take(size_t(w.slots) * n_ff * 4);
     w.u = take(size_t(w.slots) * n_ff * 4);
     w.act_h = take(ah.total);
+    w.h = take(size_t(w.slots) * n_ff * 4);
     w.dn = take(size_t(w.slots) * n_embd * 4);
     w.total = off;
     return w;
@@ -133,6 +134,11 @@ hipError_t moe_ffn(const float* x, const float* logits, int n_tok, int n_embd, i
     float* g = reinterpret_cast<float*>(b + w.g);
     float* u = reinterpret_cast<float*>(b + w.u);
     float* dn = reinterpret_cast<float*>(b + w.dn);
+    if (n_tok == 1 && moe1_supported(tg, tu, n_embd, n_ff, n_expert, k)) {
+        float* h = reinterpret_cast<float*>(b + w.h);
+        return launch_moe1(x, logits, n_embd, n_ff, n_expert, k, norm, tg, wg, tu, wu, td, wd, r, g, u, h,
+                           b + w.act_h, dn, out, s);
+    }
     hipError_t e = launch_moe_route(logits, n_tok, n_expert, k, norm, w.item_tokens, r, s);
     if (e == hipSuccess) e = launch_quantize(x, n_tok, n_embd, n_embd, b + w.act_x, nullptr, nullptr, s);
     auto grouped = [&](const void* wt, const WeightLayout& L, const void* act, int act_rows, float* y, int ldy,

@@ -15,95 +15,11 @@
 #include "dots.h"
 #include "kernels.h"
 #include "qact.h"
+#include "rowdot.h"
 
 namespace fishhip {
 
 namespace {
-
-struct Frag {
-    uint4 w0, w1;   // codes (Q8_0 uses both)
-    uint4 meta;     // Q4_K: d, dmin, scales[12]
-    uint2 qh;       // Q6_K high bits
-    float d, dmin;  // f32 weight scales
-    int sca, scb;   // integer group scales (Q4_K: sc, min; Q6_K: two 16-group scales)
-};
-
-template <uint32_t T>
-__device__ __forceinline__ Frag load_group(const WeightPtrs& W, int row, int c, int n_in) {
-    Frag f{};
-    const int groups = n_in / 32;
-    const size_t gi = size_t(row) * groups + c;
-    if constexpr (T == kQ8_0) {
-        const uint4* p = reinterpret_cast<const uint4*>(W.codes + size_t(row) * n_in + size_t(c) * 32);
-        f.w0 = p[0];
-        f.w1 = p[1];
-        f.d = f16_bits_to_f32(W.d[gi]);
-    } else if constexpr (T == kQ4_0) {
-        f.w0 = *reinterpret_cast<const uint4*>(W.codes + gi * 16);
-        f.d = f16_bits_to_f32(W.d[gi]);
-    } else if constexpr (T == kQ4_K) {
-        f.w0 = *reinterpret_cast<const uint4*>(W.codes + gi * 16);
-        f.meta = *reinterpret_cast<const uint4*>(W.aux + (size_t(row) * (n_in / 256) + (c >> 3)) * 16);
-        f.d = f16_bits_to_f32(uint16_t(f.meta.x & 0xFFFF));
-        f.dmin = f16_bits_to_f32(uint16_t(f.meta.x >> 16));
-        k4_scale_min(f.meta.y, f.meta.z, f.meta.w, c & 7, f.sca, f.scb);
-    } else {
-        f.w0 = *reinterpret_cast<const uint4*>(W.codes + gi * 16);
-        f.qh = *reinterpret_cast<const uint2*>(W.aux + gi * 8);
-        const uint16_t s2 = *reinterpret_cast<const uint16_t*>(W.sc + size_t(row) * (n_in / 16) + 2 * c);
-        f.sca = int(int8_t(s2 & 0xFF));
-        f.scb = int(int8_t(s2 >> 8));
-        f.d = f16_bits_to_f32(W.d[size_t(row) * (n_in / 256) + (c >> 3)]);
-    }
-    return f;
-}
-
-// Activation side of one 32-element group for one token.
-struct ActFrag {
-    uint4 a0, a1;  // 32 int8 codes
-    float d;       // Q8Act d (32-layouts) or Q8ActK d of the super-block
-    int s, s2;     // Q4_0: block sum; K-quants: the two per-16 sums
-};
-
-template <uint32_t T>
-__device__ __forceinline__ ActFrag load_act(const ActPtrs& A, int t, int c, int n_in) {
-    ActFrag a;
-    if constexpr (T == kQ8_0 || T == kQ4_0) {
-        const uint4* p = reinterpret_cast<const uint4*>(A.q32 + size_t(t) * n_in + size_t(c) * 32);
-        a.a0 = p[0];
-        a.a1 = p[1];
-        const size_t bi = size_t(t) * (n_in / 32) + c;
-        a.d = A.d32[bi];
-        a.s = (T == kQ4_0) ? A.s32[bi] : 0;
-        a.s2 = 0;
-    } else {
-        const uint4* p = reinterpret_cast<const uint4*>(A.q256 + size_t(t) * n_in + size_t(c) * 32);
-        a.a0 = p[0];
-        a.a1 = p[1];
-        a.d = A.d256[size_t(t) * (n_in / 256) + (c >> 3)];
-        const uint32_t s2 = *reinterpret_cast<const uint32_t*>(A.s16 + size_t(t) * (n_in / 16) + 2 * c);
-        a.s = int(int16_t(s2 & 0xFFFF));
-        a.s2 = int(int16_t(s2 >> 16));
-    }
-    return a;
-}
-
-// f32 contribution of one group (weights f, activations a).
-template <uint32_t T>
-__device__ __forceinline__ float group_dot(const Frag& f, const ActFrag& a) {
-    if constexpr (T == kQ8_0) {
-        return float(isum_q8_0(f.w0, f.w1, a.a0, a.a1)) * (f.d * a.d);
-    } else if constexpr (T == kQ4_0) {
-        return float(isum_q4_0(f.w0, a.a0, a.a1, a.s)) * (f.d * a.d);
-    } else if constexpr (T == kQ4_K) {
-        const int sumi = f.sca * dot_q4_k(f.w0, a.a0, a.a1);
-        const int mins = f.scb * (a.s + a.s2);
-        return a.d * (f.d * float(sumi) - f.dmin * float(mins));
-    } else {
-        const int sumi = isum_q6_k(f.w0, f.qh, a.a0, a.a1, a.s, a.s2, f.sca, f.scb);
-        return (f.d * a.d) * float(sumi);
-    }
-}
 
 // One-shot wavefront scheme: LPR lanes per row; a wavefront owns RB passes of
 // RPP = 64/LPR interleaved rows and reads each of them exactly once. Lane
@@ -156,7 +72,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(WeightPtrs W, ActPtrs A, int 
     for (int rb = 0; rb < RB; ++rb) {
         const int row = wrow0 + min(row_base + rb * RPP, n_out - 1);
 #pragma unroll
-        for (int k = 0; k < MAXC; ++k) f[rb][k] = load_group<T>(W, row, cg[k], n_in);
+        for (int k = 0; k < MAXC; ++k) f[rb][k] = load_group_wave<T>(W, row, cg[k], n_in, lane);
     }
 
     float acc[RB][NT];
@@ -224,14 +140,6 @@ __global__ void block_ints_kernel(WeightPtrs W, ActPtrs A, int n_in, int n_out, 
             out[gid] = sumi;
         }
     }
-}
-
-// Rows per wavefront: about BYTES of weights in flight per lane.
-template <uint32_t T, int MAXC, int BYTES = 64>
-constexpr int gemv_rb() {
-    constexpr int per_group = (T == kQ8_0) ? 32 : 16;
-    constexpr int rb = BYTES / (per_group * MAXC);
-    return rb < 1 ? 1 : (rb > 8 ? 8 : rb);
 }
 
 template <uint32_t T, int NT, int LPR, int MAXC>
@@ -351,45 +259,11 @@ __global__ __launch_bounds__(64 * kGemvXWaves) void gemv_x_kernel(GemvXGroup G, 
     for (int rb = 0; rb < RB; ++rb) {
         const int row = min(row_base + rb * RPP, n_out - 1);
 #pragma unroll
-        for (int k = 0; k < MAXC; ++k) f[rb][k] = load_group<T>(W, row, cg[k], n_in);
+        for (int k = 0; k < MAXC; ++k) f[rb][k] = load_group_wave<T>(W, row, cg[k], n_in, lane);
     }
 
-    // quantize x into LDS: thread tid takes 4-value chunks tid + 64 kGemvXWaves i
-    uint8_t* codes = reinterpret_cast<uint8_t*>(s_codes);
-#pragma unroll
-    for (int i = 0; i < XV; ++i) {
-        const int k0 = 4 * (tid + 64 * kGemvXWaves * i);
-        const bool active = k0 < n_in;  // whole 32- (K-quants: 256-) value blocks switch together
-        const float4 v = xv[i];
-        const float a = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-        const int g = k0 >> 5, o = k0 & 31;
-        if constexpr (!kq) {
-            const float d = block_d(wave_max8(a)), id = block_id(d);
-            const int q0 = code(v.x, id), q1 = code(v.y, id), q2 = code(v.z, id), q3 = code(v.w, id);
-            const int sum = wave_sum8(q0 + q1 + q2 + q3);
-            if (active) {
-                *reinterpret_cast<uint32_t*>(codes + (size_t((o >> 4) * kGemvXMaxGroups + g) * 16) + (o & 15)) =
-                    pack4(q0, q1, q2, q3);
-                if ((lane & 7) == 0) {
-                    s_d[g] = d;
-                    s_s[g] = sum;
-                }
-            }
-        } else {
-            const float d = block_d(wave_max64(a)), id = block_id(d);
-            const int q0 = code(v.x, id), q1 = code(v.y, id), q2 = code(v.z, id), q3 = code(v.w, id);
-            int g16 = q0 + q1 + q2 + q3;
-            g16 += __shfl_xor(g16, 1);
-            g16 += __shfl_xor(g16, 2);
-            const int g16b = __shfl_xor(g16, 4);
-            if (active) {
-                *reinterpret_cast<uint32_t*>(codes + (size_t((o >> 4) * kGemvXMaxGroups + g) * 16) + (o & 15)) =
-                    pack4(q0, q1, q2, q3);
-                if (lane == 0) s_d[k0 >> 8] = d;
-                if ((lane & 7) == 0) s_s[g] = (g16 & 0xFFFF) | (g16b << 16);
-            }
-        }
-    }
+    const LdsAct L{s_codes, s_d, s_s, kGemvXMaxGroups};
+    quantize_to_lds<kq, XV, 64 * kGemvXWaves>(xv, n_in, tid, L);
     __syncthreads();
     if (wave_id * (RPP * RB) >= n_out) return;  // uniform over the wavefront
 
@@ -398,19 +272,7 @@ __global__ __launch_bounds__(64 * kGemvXWaves) void gemv_x_kernel(GemvXGroup G, 
     for (int rb = 0; rb < RB; ++rb) acc[rb] = 0.0f;
 #pragma unroll
     for (int k = 0; k < MAXC; ++k) {
-        ActFrag ac;
-        ac.a0 = s_codes[cg[k]];
-        ac.a1 = s_codes[kGemvXMaxGroups + cg[k]];
-        if constexpr (!kq) {
-            ac.d = s_d[cg[k]];
-            ac.s = s_s[cg[k]];
-            ac.s2 = 0;
-        } else {
-            ac.d = s_d[cg[k] >> 3];
-            const int s2 = s_s[cg[k]];
-            ac.s = int(int16_t(s2 & 0xFFFF));
-            ac.s2 = s2 >> 16;
-        }
+        const ActFrag ac = lds_act<T>(L, cg[k]);
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) {
             const float v = group_dot<T>(f[rb][k], ac);

@@ -31,6 +31,17 @@ struct MoeRouting {
 hipError_t launch_moe_route(const float* logits, int n_tok, int n_expert, int k, int norm, int item_tokens,
                             const MoeRouting& r, hipStream_t stream);
 
+// The expert FFN of one token: gate+up (routing and x quantization
+// in-kernel; writes the routing, gate, up and h = silu(gate)*up rows), then
+// down+combine (h quantized in-kernel for small experts, else by one quantize
+// launch into act_h first; writes the down rows and out).
+// Slots as the grouped path's: the chosen experts ascending.
+bool moe1_supported(uint32_t tg, uint32_t tu, int n_embd, int n_ff, int n_expert, int k);
+hipError_t launch_moe1(const float* x, const float* logits, int n_embd, int n_ff, int n_expert, int k, int norm,
+                       uint32_t tg, const void* wg, uint32_t tu, const void* wu, uint32_t td, const void* wd,
+                       const MoeRouting& r, float* g, float* u, float* h, void* act_h, float* dn, float* out,
+                       hipStream_t stream);
+
 // out[t][i] = sum over the token's experts in ascending expert order of
 // w * down[slot][i] (model.cpp:1574-1579).
 hipError_t launch_moe_combine(const float* down, const MoeRouting& r, int n_tok, int k, int n_embd, float* out,

@@ -12,6 +12,8 @@
 // FISH's separate multiply and add.
 #include "common.h"
 #include "kernels.h"
+#include "qact.h"
+#include "rowdot.h"
 
 namespace fishhip {
 
@@ -20,37 +22,36 @@ namespace {
 constexpr int kMaxExperts = 256;
 constexpr int kMaxK = 16;
 constexpr int kMaxTok = 2048;  // grouping bitmap: kMaxExperts x kMaxTok bits in LDS
+constexpr int kMoe1UpWaves = 16;      // wavefronts per workgroup: one-token gate+up
+constexpr int kMoe1Waves = 8;         // and down (its k * groups fragments need the registers)
+constexpr int kMoe1MaxGroups = 1024;  // k * n_ff <= 32768 hidden values in LDS
 
-// One wavefront per token: softmax over the experts in FISH's order (max,
-// then exp(x - max) summed left to right, then times 1/sum), the k most
-// probable by k wavefront argmax rounds (ties: lower expert), renormalised.
-__global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ logits, int n_tok, int n_expert, int k,
-                                                   int norm, MoeRouting r) {
-    __shared__ float s_p[4][kMaxExperts];
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int t = int(blockIdx.x) * 4 + w;
-    if (t >= n_tok) return;
-    const float* lg = logits + size_t(t) * n_expert;
+// One token's routing by one wavefront (model.cpp:1528-1547): softmax over
+// the experts in FISH's order (max, then exp(x - max) summed left to right,
+// then times 1/sum), the k most probable by k wavefront argmax rounds (ties:
+// lower expert), renormalised by their sum when norm. Every lane ends with
+// chosen[j] / prob[j], j < k, in descending probability. s_p: LDS scratch
+// of kMaxExperts floats owned by this wavefront.
+__device__ void route_token(const float* __restrict__ lg, int n_expert, int k, int norm, float* s_p, int lane,
+                            int (&chosen)[kMaxK], float (&prob)[kMaxK]) {
     float m = -INFINITY;
     for (int e = lane; e < n_expert; e += 64) m = fmaxf(m, lg[e]);
     for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-    for (int e = lane; e < n_expert; e += 64) s_p[w][e] = expf(__fsub_rn(lg[e], m));
+    for (int e = lane; e < n_expert; e += 64) s_p[e] = expf(__fsub_rn(lg[e], m));
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     float sum = 0.0f;
     if (lane == 0)
-        for (int e = 0; e < n_expert; ++e) sum = __fadd_rn(sum, s_p[w][e]);
+        for (int e = 0; e < n_expert; ++e) sum = __fadd_rn(sum, s_p[e]);
     sum = __shfl(sum, 0);
     const bool uniform = !(sum > 0.0f);
     const float inv = uniform ? 0.0f : 1.0f / sum;
     float p[kMaxExperts / 64];
     for (int q = 0; q < kMaxExperts / 64; ++q) {
         const int e = lane + 64 * q;
-        p[q] = (e < n_expert) ? (uniform ? 1.0f / float(n_expert) : __fmul_rn(s_p[w][e], inv)) : -1.0f;
+        p[q] = (e < n_expert) ? (uniform ? 1.0f / float(n_expert) : __fmul_rn(s_p[e], inv)) : -1.0f;
     }
     float wsum = 0.0f;
-    float prob[kMaxK];
-    int chosen[kMaxK];
     for (int j = 0; j < k; ++j) {
         float bp = -1.0f;
         int be = 0x7fffffff;
@@ -69,10 +70,24 @@ __global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ log
         for (int q = 0; q < kMaxExperts / 64; ++q)
             if (lane + 64 * q == be) p[q] = -2.0f;  // taken
     }
+    if (norm && wsum > 0.0f)
+        for (int j = 0; j < k; ++j) prob[j] = prob[j] / wsum;
+}
+
+// One wavefront per token.
+__global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ logits, int n_tok, int n_expert, int k,
+                                                   int norm, MoeRouting r) {
+    __shared__ float s_p[4][kMaxExperts];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int t = int(blockIdx.x) * 4 + w;
+    if (t >= n_tok) return;
+    int chosen[kMaxK];
+    float prob[kMaxK];
+    route_token(logits + size_t(t) * n_expert, n_expert, k, norm, s_p[w], lane, chosen, prob);
     if (lane == 0)
         for (int j = 0; j < k; ++j) {
             r.sel[t * k + j] = chosen[j];
-            r.wsel[t * k + j] = (norm && wsum > 0.0f) ? prob[j] / wsum : prob[j];
+            r.wsel[t * k + j] = prob[j];
         }
 }
 
@@ -157,6 +172,220 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
     out[gid] = acc;
 }
 
+// ---------------------------------------------------------------- one token
+
+// The expert FFN of a single token in two launches (decode). The slot order
+// is the workspace's: the k chosen experts ascending (model.cpp:1551-1561).
+//
+// Launch 1, gate and up: every workgroup routes the token itself (wavefront
+// 0, route_token), quantizes x into LDS while its weight loads are in
+// flight, and for rows i of its slot's expert e computes gate_e[i], up_e[i]
+// (the same lanes, so h = silu(gate) * up is formed in place) and writes
+// gate, up and h. Workgroup 0 also writes the routing (sel, wsel, tok_slot,
+// slot_tok).
+template <uint32_t T, int LPR, int MAXC, int RB, int XV>
+__global__ __launch_bounds__(64 * kMoe1UpWaves) void moe1_gate_up_kernel(
+    const float* __restrict__ x, const float* __restrict__ logits, int n_embd, int n_ff, int n_expert, int k,
+    int norm, WeightPtrs Wg, WeightPtrs Wu, int wgs_per_slot, MoeRouting r, float* __restrict__ g_out,
+    float* __restrict__ u_out, float* __restrict__ h_out) {
+    constexpr bool kq = (T == kQ4_K || T == kQ6_K);
+    constexpr int RPP = 64 / LPR, TH = 64 * kMoe1UpWaves;
+    __shared__ uint4 s_codes[2 * kGemvXMaxGroups];
+    __shared__ float s_d[kGemvXMaxGroups];
+    __shared__ int s_s[kGemvXMaxGroups];
+    __shared__ float s_p[kMaxExperts];
+    __shared__ int s_exp[kMaxK];
+
+    const int tid = threadIdx.x, lane = tid & 63, sub = lane % LPR;
+    float4 xv[XV];
+#pragma unroll
+    for (int i = 0; i < XV; ++i) {
+        const int k0 = 4 * (tid + TH * i);
+        xv[i] = k0 < n_embd ? *reinterpret_cast<const float4*>(x + k0) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    if (tid < 64) {
+        int chosen[kMaxK];
+        float prob[kMaxK];
+        route_token(logits, n_expert, k, norm, s_p, lane, chosen, prob);
+        if (lane < k) {
+            int me = 0, rank = 0;
+            float mw = 0.0f;
+            for (int j = 0; j < k; ++j)
+                if (j == lane) {
+                    me = chosen[j];
+                    mw = prob[j];
+                }
+            for (int j = 0; j < k; ++j) rank += chosen[j] < me;
+            s_exp[rank] = me;
+            if (blockIdx.x == 0) {
+                r.sel[lane] = me;
+                r.wsel[lane] = mw;
+                r.tok_slot[lane] = rank;
+                r.slot_tok[rank] = 0;
+            }
+        }
+    }
+    __syncthreads();
+    const int slot = int(blockIdx.x) / wgs_per_slot, wg = int(blockIdx.x) % wgs_per_slot;
+    const int e = s_exp[slot];
+    const int wave_id = wg * kMoe1UpWaves + (tid >> 6);
+    const int row_base = wave_id * (RPP * RB) + lane / LPR;
+    const int groups = n_embd / 32;
+    int cg[MAXC];
+    bool cv[MAXC];
+#pragma unroll
+    for (int q = 0; q < MAXC; ++q) {
+        const int c = sub + q * LPR;
+        cv[q] = c < groups;
+        cg[q] = cv[q] ? c : groups - 1;
+    }
+    Frag fg[RB][MAXC], fu[RB][MAXC];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+        const int row = e * n_ff + min(row_base + rb * RPP, n_ff - 1);
+#pragma unroll
+        for (int q = 0; q < MAXC; ++q) {
+            fg[rb][q] = load_group_wave<T>(Wg, row, cg[q], n_embd, lane);
+            fu[rb][q] = load_group_wave<T>(Wu, row, cg[q], n_embd, lane);
+        }
+    }
+    const LdsAct L{s_codes, s_d, s_s, kGemvXMaxGroups};
+    quantize_to_lds<kq, XV, TH>(xv, n_embd, tid, L);
+    __syncthreads();
+    if (wave_id * (RPP * RB) >= n_ff) return;  // uniform over the wavefront
+    float ag[RB], au[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) ag[rb] = au[rb] = 0.0f;
+#pragma unroll
+    for (int q = 0; q < MAXC; ++q) {
+        const ActFrag ac = lds_act<T>(L, cg[q]);
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+            const float vg = group_dot<T>(fg[rb][q], ac), vu = group_dot<T>(fu[rb][q], ac);
+            ag[rb] += cv[q] ? vg : 0.0f;
+            au[rb] += cv[q] ? vu : 0.0f;
+        }
+    }
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+        float g = ag[rb], u = au[rb];
+#pragma unroll
+        for (int off = LPR / 2; off > 0; off >>= 1) {
+            g += __shfl_xor(g, off);
+            u += __shfl_xor(u, off);
+        }
+        const int row = row_base + rb * RPP;
+        if (sub == 0 && row < n_ff) {
+            const size_t o = size_t(slot) * n_ff + row;
+            g_out[o] = g;
+            u_out[o] = u;
+            h_out[o] = silu_mul(g, u);
+        }
+    }
+}
+
+// Launch 2, down and combine: every workgroup quantizes the k hidden rows
+// (each row on its own, as ActBatch::quantize does per expert batch) into
+// LDS, and for rows i computes down_e[i] for the k experts in ascending
+// order, writing them and out[i] = sum of w_e * down_e[i] with FISH's
+// separate multiply and add, in that order (model.cpp:1574-1579).
+// XV > 0: the workgroup quantizes the k * n_ff <= 4 * 64 * kMoe1Waves * XV
+// hidden values itself (small experts); XV == 0: they were quantized by the
+// quantize kernel into `act` (one row per slot) and the workgroup copies
+// them into the same LDS layout.
+template <uint32_t T, int LPR, int MAXC, int KMAX, int XV>
+__global__ __launch_bounds__(64 * kMoe1Waves) void moe1_down_kernel(const float* __restrict__ h, ActPtrs act,
+                                                                    int n_embd, int n_ff, int k, WeightPtrs Wd,
+                                                                    MoeRouting r, float* __restrict__ dn,
+                                                                    float* __restrict__ out) {
+    constexpr bool kq = (T == kQ4_K || T == kQ6_K);
+    constexpr int RPP = 64 / LPR, TH = 64 * kMoe1Waves;
+    constexpr int MG = XV > 0 ? XV * TH * 4 / 32 : kMoe1MaxGroups;  // LDS groups
+    __shared__ uint4 s_codes[2 * MG];
+    __shared__ float s_d[MG];
+    __shared__ int s_s[MG];
+    __shared__ int s_exp[kMaxK];
+    __shared__ float s_w[kMaxK];
+
+    const int tid = threadIdx.x, lane = tid & 63, sub = lane % LPR;
+    const int n_h = k * n_ff;
+    float4 xv[XV > 0 ? XV : 1];
+#pragma unroll
+    for (int i = 0; i < XV; ++i) {
+        const int k0 = 4 * (tid + TH * i);
+        xv[i] = k0 < n_h ? *reinterpret_cast<const float4*>(h + k0) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    if (tid < k) {
+        const int s = r.tok_slot[tid];
+        s_exp[s] = r.sel[tid];
+        s_w[s] = r.wsel[tid];
+    }
+    __syncthreads();
+    const int wave_id = int(blockIdx.x) * kMoe1Waves + (tid >> 6);
+    const int row = wave_id * RPP + lane / LPR;
+    const int rowc = min(row, n_embd - 1);
+    const int groups = n_ff / 32;
+    int cg[MAXC];
+    bool cv[MAXC];
+#pragma unroll
+    for (int q = 0; q < MAXC; ++q) {
+        const int c = sub + q * LPR;
+        cv[q] = c < groups;
+        cg[q] = cv[q] ? c : groups - 1;
+    }
+    Frag f[KMAX][MAXC];
+#pragma unroll
+    for (int s = 0; s < KMAX; ++s) {
+        const int e = s_exp[min(s, k - 1)];
+#pragma unroll
+        for (int q = 0; q < MAXC; ++q) f[s][q] = load_group_wave<T>(Wd, e * n_embd + rowc, cg[q], n_ff, lane);
+    }
+    const LdsAct L{s_codes, s_d, s_s, MG};
+    if constexpr (XV > 0) {
+        quantize_to_lds<kq, XV, TH>(xv, n_h, tid, L);
+    } else {
+        const int ng = n_h / 32;  // groups of all k rows (rows are contiguous in act)
+        const int8_t* q = kq ? act.q256 : act.q32;
+#pragma unroll 4
+        for (int i = tid; i < 2 * ng; i += TH) {
+            const int hh = i / ng, g = i - hh * ng;
+            s_codes[hh * MG + g] = *reinterpret_cast<const uint4*>(q + size_t(g) * 32 + hh * 16);
+        }
+#pragma unroll 2
+        for (int i = tid; i < ng; i += TH) {
+            if constexpr (kq) {
+                s_s[i] = *reinterpret_cast<const int*>(act.s16 + 2 * i);
+                if (i < n_h / 256) s_d[i] = act.d256[i];
+            } else {
+                s_s[i] = act.s32[i];
+                s_d[i] = act.d32[i];
+            }
+        }
+    }
+    __syncthreads();
+    if (wave_id * RPP >= n_embd) return;  // uniform over the wavefront
+    float acc = 0.0f;
+#pragma unroll
+    for (int s = 0; s < KMAX; ++s) {
+        float d = 0.0f;
+        const int sc = min(s, k - 1);  // slots past k compute on the last slot's rows and are discarded
+#pragma unroll
+        for (int q = 0; q < MAXC; ++q) {
+            const float v = group_dot<T>(f[s][q], lds_act<T>(L, sc * groups + cg[q]));
+            d += cv[q] ? v : 0.0f;
+        }
+#pragma unroll
+        for (int off = LPR / 2; off > 0; off >>= 1) d += __shfl_xor(d, off);
+        if (s < k) {
+            // w * down rounded, then added: this file is built without contraction
+            const float p = s_w[s] * d;
+            acc = acc + p;
+            if (sub == 0 && row < n_embd) dn[size_t(s) * n_embd + row] = d;
+        }
+    }
+    if (sub == 0 && row < n_embd) out[row] = acc;
+}
+
 }  // namespace
 
 hipError_t launch_moe_route(const float* logits, int n_tok, int n_expert, int k, int norm, int item_tokens,
@@ -178,6 +407,112 @@ hipError_t launch_moe_combine(const float* down, const MoeRouting& r, int n_tok,
     hipLaunchKernelGGL(combine_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0, stream, down, r, n_tok, k,
                        n_embd, out);
     return hipGetLastError();
+}
+
+}  // namespace fishhip
+
+namespace fishhip {
+
+namespace {
+
+template <uint32_t T, int LPR, int MAXC>
+hipError_t moe1_gate_up_launch(const float* x, const float* logits, int n_embd, int n_ff, int n_expert, int k,
+                               int norm, const WeightPtrs& Wg, const WeightPtrs& Wu, const MoeRouting& r, float* g,
+                               float* u, float* h, hipStream_t s) {
+    constexpr int RB = gemv_rb<T, MAXC>();
+    constexpr int RPW = (64 / LPR) * RB;
+    constexpr int TH = 64 * kMoe1UpWaves;
+    constexpr int XV = LPR == 64 ? (64 * 32 * MAXC / 4 + TH - 1) / TH : 1;
+    const int wgs_per_slot = ((n_ff + RPW - 1) / RPW + kMoe1UpWaves - 1) / kMoe1UpWaves;
+    hipLaunchKernelGGL((moe1_gate_up_kernel<T, LPR, MAXC, RB, XV>), dim3(unsigned(wgs_per_slot * k)), dim3(TH), 0, s,
+                       x, logits, n_embd, n_ff, n_expert, k, norm, Wg, Wu, wgs_per_slot, r, g, u, h);
+    return hipGetLastError();
+}
+
+// hidden values a workgroup quantizes itself: up to 4 chunks per thread
+constexpr int kMoe1LdsHidden = 4 * 64 * kMoe1Waves * 4;
+
+template <uint32_t T, int LPR, int MAXC>
+hipError_t moe1_down_launch(const float* h, const ActPtrs& act, int n_embd, int n_ff, int k, const WeightPtrs& Wd,
+                            const MoeRouting& r, float* dn, float* out, hipStream_t s) {
+    const int waves = (n_embd + 64 / LPR - 1) / (64 / LPR);
+    const dim3 grid(unsigned((waves + kMoe1Waves - 1) / kMoe1Waves)), block(64 * kMoe1Waves);
+    const bool lds = k * n_ff <= kMoe1LdsHidden;
+    if (k <= 2) {
+        if (lds) hipLaunchKernelGGL((moe1_down_kernel<T, LPR, MAXC, 2, 4>), grid, block, 0, s, h, act, n_embd, n_ff, k, Wd, r, dn, out);
+        else hipLaunchKernelGGL((moe1_down_kernel<T, LPR, MAXC, 2, 0>), grid, block, 0, s, h, act, n_embd, n_ff, k, Wd, r, dn, out);
+    } else {
+        if (lds) hipLaunchKernelGGL((moe1_down_kernel<T, LPR, MAXC, 8, 4>), grid, block, 0, s, h, act, n_embd, n_ff, k, Wd, r, dn, out);
+        else hipLaunchKernelGGL((moe1_down_kernel<T, LPR, MAXC, 8, 0>), grid, block, 0, s, h, act, n_embd, n_ff, k, Wd, r, dn, out);
+    }
+    return hipGetLastError();
+}
+
+// (LPR, groups per lane) as the GEMV picks them
+template <uint32_t T, bool DOWN>
+hipError_t moe1_pick(int n_in, const float* a, const ActPtrs& act, const float* logits, int n_embd, int n_ff,
+                     int n_expert, int k, int norm, const WeightPtrs& W0, const WeightPtrs& W1, const MoeRouting& r,
+                     float* o0, float* o1, float* o2, hipStream_t s) {
+    const int groups = n_in / 32;
+    const int lpr = groups >= 64 ? 64 : (groups >= 16 ? 16 : 8);
+    const int per_lane = (groups + lpr - 1) / lpr;
+#define MOE1_CASE(LPR_, MAXC_)                                                                                  \
+    if (lpr == LPR_ && per_lane == MAXC_) {                                                                     \
+        if constexpr (DOWN) return moe1_down_launch<T, LPR_, MAXC_>(a, act, n_embd, n_ff, k, W0, r, o0, o1, s); \
+        else return moe1_gate_up_launch<T, LPR_, MAXC_>(a, logits, n_embd, n_ff, n_expert, k, norm, W0, W1, r, \
+                                                        o0, o1, o2, s);                                      \
+    }
+    MOE1_CASE(64, 1) MOE1_CASE(64, 2) MOE1_CASE(64, 3) MOE1_CASE(64, 4)
+    MOE1_CASE(64, 5) MOE1_CASE(64, 6) MOE1_CASE(64, 7) MOE1_CASE(64, 8)
+    MOE1_CASE(16, 1) MOE1_CASE(16, 2) MOE1_CASE(16, 3) MOE1_CASE(16, 4)
+    MOE1_CASE(8, 1) MOE1_CASE(8, 2)
+#undef MOE1_CASE
+    return hipErrorInvalidValue;
+}
+
+template <bool DOWN>
+hipError_t moe1_type(uint32_t t, int n_in, const float* a, const ActPtrs& act, const float* logits, int n_embd,
+                     int n_ff, int n_expert, int k, int norm, const WeightPtrs& W0, const WeightPtrs& W1,
+                     const MoeRouting& r, float* o0, float* o1, float* o2, hipStream_t s) {
+#define MOE1_TYPE(T_) moe1_pick<T_, DOWN>(n_in, a, act, logits, n_embd, n_ff, n_expert, k, norm, W0, W1, r, o0, o1, o2, s)
+    switch (t) {
+        case kQ8_0: return MOE1_TYPE(kQ8_0);
+        case kQ4_0: return MOE1_TYPE(kQ4_0);
+        case kQ4_K: return MOE1_TYPE(kQ4_K);
+        case kQ6_K: return MOE1_TYPE(kQ6_K);
+        default: return hipErrorInvalidValue;
+    }
+#undef MOE1_TYPE
+}
+
+}  // namespace
+
+bool moe1_supported(uint32_t tg, uint32_t tu, int n_embd, int n_ff, int n_expert, int k) {
+    const int g_in = n_embd / 32, g_ff = n_ff / 32;
+    auto fits = [](int groups) {
+        const int lpr = groups >= 64 ? 64 : (groups >= 16 ? 16 : 8);
+        return (groups + lpr - 1) / lpr <= (lpr == 64 ? 8 : (lpr == 16 ? 4 : 2));
+    };
+    return tg == tu && n_embd <= 32 * kGemvXMaxGroups && k <= 8 && k * n_ff <= 32 * kMoe1MaxGroups &&
+           n_expert <= kMaxExperts && fits(g_in) && fits(g_ff);
+}
+
+hipError_t launch_moe1(const float* x, const float* logits, int n_embd, int n_ff, int n_expert, int k, int norm,
+                       uint32_t tg, const void* wg, uint32_t tu, const void* wu, uint32_t td, const void* wd,
+                       const MoeRouting& r, float* g, float* u, float* h, void* act_h, float* dn, float* out,
+                       hipStream_t s) {
+    if (!moe1_supported(tg, tu, n_embd, n_ff, n_expert, k)) return hipErrorInvalidValue;
+    const WeightPtrs Wg = weight_ptrs(wg, weight_layout(tg, n_embd, n_expert * n_ff));
+    const WeightPtrs Wu = weight_ptrs(wu, weight_layout(tu, n_embd, n_expert * n_ff));
+    const WeightPtrs Wd = weight_ptrs(wd, weight_layout(td, n_ff, n_expert * n_embd));
+    const ActPtrs A = act_ptrs(act_h, act_layout(k, n_ff));
+    hipError_t e = moe1_type<false>(tg, n_embd, x, A, logits, n_embd, n_ff, n_expert, k, norm, Wg, Wu, r, g, u, h, s);
+    // large hidden rows: quantized once here rather than by every down workgroup
+    if (e == hipSuccess && k * n_ff > kMoe1LdsHidden)
+        e = launch_quantize(h, k, n_ff, n_ff, act_h, nullptr, nullptr, s);
+    if (e == hipSuccess)
+        e = moe1_type<true>(td, n_ff, h, A, logits, n_embd, n_ff, n_expert, k, norm, Wd, Wd, r, dn, out, nullptr, s);
+    return e;
 }
 
 }  // namespace fishhip

@@ -43,4 +43,66 @@ __device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
 __device__ __forceinline__ float block_d(float amax) { return amax / 127.0f; }
 __device__ __forceinline__ float block_id(float d) { return d > 0.0f ? 1.0f / d : 0.0f; }
 
+// One token's activations quantized by a workgroup into LDS, in the layout
+// the decode kernels read: codes [2][maxg] 16-byte pieces (piece h of group
+// g = elements 16 h .. 16 h + 15), and per group either Q8Act (d, sum) or,
+// for K-quants, the super-block's Q8ActK d (at [g >> 3]) and the group's two
+// per-16 sums packed as int16 pairs.
+struct LdsAct {
+    uint4* codes;
+    float* d;
+    int* s;
+    int maxg;
+};
+
+// Quantizes n_in values held as float4 chunks j = tid + TH i (i < XV) of
+// the calling thread; the caller synchronises before reading. Whole 32-value
+// (K-quants: 256-value) blocks are in one wavefront, so the reductions are
+// wavefront shuffles, and inactive chunks switch whole blocks off together.
+template <bool KQ, int XV, int TH>
+__device__ __forceinline__ void quantize_to_lds(const float4 (&xv)[XV], int n_in, int tid, const LdsAct& L) {
+    const int lane = tid & 63;
+    uint8_t* codes = reinterpret_cast<uint8_t*>(L.codes);
+#pragma unroll
+    for (int i = 0; i < XV; ++i) {
+        const int k0 = 4 * (tid + TH * i);
+        const bool active = k0 < n_in;
+        const float4 v = xv[i];
+        const float a = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+        const int g = k0 >> 5, o = k0 & 31;
+        uint8_t* dst = codes + (size_t((o >> 4) * L.maxg + g) * 16) + (o & 15);
+        if constexpr (!KQ) {
+            const float d = block_d(wave_max8(a)), id = block_id(d);
+            const int q0 = code(v.x, id), q1 = code(v.y, id), q2 = code(v.z, id), q3 = code(v.w, id);
+            const int sum = wave_sum8(q0 + q1 + q2 + q3);
+            if (active) {
+                *reinterpret_cast<uint32_t*>(dst) = pack4(q0, q1, q2, q3);
+                if ((lane & 7) == 0) {
+                    L.d[g] = d;
+                    L.s[g] = sum;
+                }
+            }
+        } else {
+            const float d = block_d(wave_max64(a)), id = block_id(d);
+            const int q0 = code(v.x, id), q1 = code(v.y, id), q2 = code(v.z, id), q3 = code(v.w, id);
+            int g16 = q0 + q1 + q2 + q3;
+            g16 += __shfl_xor(g16, 1);
+            g16 += __shfl_xor(g16, 2);
+            const int g16b = __shfl_xor(g16, 4);
+            if (active) {
+                *reinterpret_cast<uint32_t*>(dst) = pack4(q0, q1, q2, q3);
+                if (lane == 0) L.d[k0 >> 8] = d;
+                if ((lane & 7) == 0) L.s[g] = (g16 & 0xFFFF) | (g16b << 16);
+            }
+        }
+    }
+}
+
+// silu(g) * u in FISH's float order: g / (1 + exp(-g)), then times u
+// (silu_inplace, ops.cpp:25-30; model.cpp:1504-1508).
+__device__ __forceinline__ float silu_mul(float g, float u) {
+    const float s = g / __fadd_rn(1.0f, expf(-g));
+    return __fmul_rn(s, u);
+}
+
 }  // namespace fishhip

@@ -31,12 +31,6 @@ struct QuantOut {
     uint8_t* aos256;  // optional FISH Q8ActK rows (276 B blocks)
 };
 
-// silu(g) * u in FISH's float order: g / (1 + exp(-g)), then times u
-// (silu_inplace, ops.cpp:25-30; model.cpp:1504-1508).
-__device__ __forceinline__ float silu_mul(float g, float u) {
-    const float s = g / __fadd_rn(1.0f, expf(-g));
-    return __fmul_rn(s, u);
-}
 
 // Byte offset, inside its 256-element unit, of the dword that holds this
 // lane's four codes in MFMA operand order: lane L of the unit holds elements

@@ -1,0 +1,152 @@
+// One weight row's 32-element groups against one token's int8 activations,
+// for the decode-shape kernels (GEMV, fused GEMV, single-token expert FFN):
+// loading a group of the repacked weights, loading the token's matching
+// activation group, and the group's f32 contribution from its exact integer
+// dot (dots.h).
+#pragma once
+
+#include "common.h"
+#include "dots.h"
+#include "qact.h"
+
+namespace fishhip {
+
+struct Frag {
+    uint4 w0, w1;   // codes (Q8_0 uses both)
+    uint4 meta;     // Q4_K: d, dmin, scales[12]
+    uint2 qh;       // Q6_K high bits
+    float d, dmin;  // f32 weight scales
+    int sca, scb;   // integer group scales (Q4_K: sc, min; Q6_K: two 16-group scales)
+};
+
+
+template <uint32_t T>
+__device__ __forceinline__ Frag load_group(const WeightPtrs& W, int row, int c, int n_in) {
+    Frag f{};
+    const int groups = n_in / 32;
+    const size_t gi = size_t(row) * groups + c;
+    if constexpr (T == kQ8_0) {
+        const uint4* p = reinterpret_cast<const uint4*>(W.codes + size_t(row) * n_in + size_t(c) * 32);
+        f.w0 = p[0];
+        f.w1 = p[1];
+        f.d = f16_bits_to_f32(W.d[gi]);
+    } else if constexpr (T == kQ4_0) {
+        f.w0 = *reinterpret_cast<const uint4*>(W.codes + gi * 16);
+        f.d = f16_bits_to_f32(W.d[gi]);
+    } else if constexpr (T == kQ4_K) {
+        f.w0 = *reinterpret_cast<const uint4*>(W.codes + gi * 16);
+        f.meta = *reinterpret_cast<const uint4*>(W.aux + (size_t(row) * (n_in / 256) + (c >> 3)) * 16);
+        f.d = f16_bits_to_f32(uint16_t(f.meta.x & 0xFFFF));
+        f.dmin = f16_bits_to_f32(uint16_t(f.meta.x >> 16));
+        k4_scale_min(f.meta.y, f.meta.z, f.meta.w, c & 7, f.sca, f.scb);
+    } else {
+        f.w0 = *reinterpret_cast<const uint4*>(W.codes + gi * 16);
+        f.qh = *reinterpret_cast<const uint2*>(W.aux + gi * 8);
+        const uint16_t s2 = *reinterpret_cast<const uint16_t*>(W.sc + size_t(row) * (n_in / 16) + 2 * c);
+        f.sca = int(int8_t(s2 & 0xFF));
+        f.scb = int(int8_t(s2 >> 8));
+        f.d = f16_bits_to_f32(W.d[size_t(row) * (n_in / 256) + (c >> 3)]);
+    }
+    return f;
+}
+
+// load_group for wavefront-synchronous callers whose lanes 8j..8j+7 hold the
+// eight groups of one super-block (lane sub takes groups sub, sub + LPR, ...
+// with LPR a multiple of 8): the Q4_K meta is loaded as one dword per lane
+// and assembled with four shuffles, so a wavefront moves 4 instead of 16
+// meta bytes per lane. Other types load as load_group.
+template <uint32_t T>
+__device__ __forceinline__ Frag load_group_wave(const WeightPtrs& W, int row, int c, int n_in, int lane) {
+    if constexpr (T != kQ4_K) {
+        return load_group<T>(W, row, c, n_in);
+    } else {
+        Frag f{};
+        const size_t gi = size_t(row) * (n_in / 32) + c;
+        f.w0 = *reinterpret_cast<const uint4*>(W.codes + gi * 16);
+        const uint32_t part = reinterpret_cast<const uint32_t*>(W.aux + (size_t(row) * (n_in / 256) + (c >> 3)) * 16)
+            [lane & 3];
+        const int base = lane & ~7;
+        f.meta = make_uint4(__shfl(part, base), __shfl(part, base + 1), __shfl(part, base + 2), __shfl(part, base + 3));
+        f.d = f16_bits_to_f32(uint16_t(f.meta.x & 0xFFFF));
+        f.dmin = f16_bits_to_f32(uint16_t(f.meta.x >> 16));
+        k4_scale_min(f.meta.y, f.meta.z, f.meta.w, c & 7, f.sca, f.scb);
+        return f;
+    }
+}
+
+// Activation side of one 32-element group for one token.
+struct ActFrag {
+    uint4 a0, a1;  // 32 int8 codes
+    float d;       // Q8Act d (32-layouts) or Q8ActK d of the super-block
+    int s, s2;     // Q4_0: block sum; K-quants: the two per-16 sums
+};
+
+template <uint32_t T>
+__device__ __forceinline__ ActFrag load_act(const ActPtrs& A, int t, int c, int n_in) {
+    ActFrag a;
+    if constexpr (T == kQ8_0 || T == kQ4_0) {
+        const uint4* p = reinterpret_cast<const uint4*>(A.q32 + size_t(t) * n_in + size_t(c) * 32);
+        a.a0 = p[0];
+        a.a1 = p[1];
+        const size_t bi = size_t(t) * (n_in / 32) + c;
+        a.d = A.d32[bi];
+        a.s = (T == kQ4_0) ? A.s32[bi] : 0;
+        a.s2 = 0;
+    } else {
+        const uint4* p = reinterpret_cast<const uint4*>(A.q256 + size_t(t) * n_in + size_t(c) * 32);
+        a.a0 = p[0];
+        a.a1 = p[1];
+        a.d = A.d256[size_t(t) * (n_in / 256) + (c >> 3)];
+        const uint32_t s2 = *reinterpret_cast<const uint32_t*>(A.s16 + size_t(t) * (n_in / 16) + 2 * c);
+        a.s = int(int16_t(s2 & 0xFFFF));
+        a.s2 = int(int16_t(s2 >> 16));
+    }
+    return a;
+}
+
+// f32 contribution of one group (weights f, activations a).
+template <uint32_t T>
+__device__ __forceinline__ float group_dot(const Frag& f, const ActFrag& a) {
+    if constexpr (T == kQ8_0) {
+        return float(isum_q8_0(f.w0, f.w1, a.a0, a.a1)) * (f.d * a.d);
+    } else if constexpr (T == kQ4_0) {
+        return float(isum_q4_0(f.w0, a.a0, a.a1, a.s)) * (f.d * a.d);
+    } else if constexpr (T == kQ4_K) {
+        const int sumi = f.sca * dot_q4_k(f.w0, a.a0, a.a1);
+        const int mins = f.scb * (a.s + a.s2);
+        return a.d * (f.d * float(sumi) - f.dmin * float(mins));
+    } else {
+        const int sumi = isum_q6_k(f.w0, f.qh, a.a0, a.a1, a.s, a.s2, f.sca, f.scb);
+        return (f.d * a.d) * float(sumi);
+    }
+}
+
+// Rows per wavefront: about BYTES of weights in flight per lane.
+template <uint32_t T, int MAXC, int BYTES = 64>
+constexpr int gemv_rb() {
+    constexpr int per_group = (T == kQ8_0) ? 32 : 16;
+    constexpr int rb = BYTES / (per_group * MAXC);
+    return rb < 1 ? 1 : (rb > 8 ? 8 : rb);
+}
+
+
+// The activation side of group c from a workgroup's LDS copy (qact.h).
+template <uint32_t T>
+__device__ __forceinline__ ActFrag lds_act(const LdsAct& L, int c) {
+    ActFrag a;
+    a.a0 = L.codes[c];
+    a.a1 = L.codes[L.maxg + c];
+    if constexpr (T == kQ8_0 || T == kQ4_0) {
+        a.d = L.d[c];
+        a.s = L.s[c];
+        a.s2 = 0;
+    } else {
+        a.d = L.d[c >> 3];
+        const int s2 = L.s[c];
+        a.s = int(int16_t(s2 & 0xFFFF));
+        a.s2 = s2 >> 16;
+    }
+    return a;
+}
+
+}  // namespace fishhip

@@ -166,6 +166,17 @@ def test_moe_qwen3_like(torch_dev, oracle, n_tok):
     run_case(torch_dev, oracle, n_tok, 512, 256, 32, 8, (fh.Q4_K, fh.Q4_K, fh.Q6_K), 2000 + n_tok)
 
 
+@pytest.mark.parametrize("n_embd,n_ff,k,types", [
+    (512, 4096, 4, (fh.Q4_K, fh.Q4_K, fh.Q6_K)),
+    (256, 2560, 4, (fh.Q4_0, fh.Q4_0, fh.Q8_0)),
+    (256, 512, 8, (fh.Q8_0, fh.Q8_0, fh.Q4_0)),
+])
+def test_moe_decode_hidden_sizes(torch_dev, oracle, n_embd, n_ff, k, types):
+    """One token: hidden rows quantized by the down workgroups themselves
+    (k * n_ff <= 8192) or once by the quantize kernel (larger)."""
+    run_case(torch_dev, oracle, 1, n_embd, n_ff, 8, k, types, 6000 + n_ff + k)
+
+
 def test_moe_mixed_types(torch_dev, oracle):
     run_case(torch_dev, oracle, 9, 256, 512, 4, 2, (fh.Q8_0, fh.Q4_0, fh.Q6_K), 3000)
 
