@@ -140,7 +140,8 @@ hipError_t moe_ffn(const float* x, const float* logits, int n_tok, int n_embd, i
                            b + w.act_h, dn, out, s);
     }
     hipError_t e = launch_moe_route(logits, n_tok, n_expert, k, norm, w.item_tokens, r, s);
-    if (e == hipSuccess) e = launch_quantize(x, n_tok, n_embd, n_embd, b + w.act_x, nullptr, nullptr, s);
+    const unsigned planes = w.mfma ? (kPlanesBatch32 | kPlanesBatch256) : kPlanesGemv;
+    if (e == hipSuccess) e = launch_quantize(x, n_tok, n_embd, n_embd, b + w.act_x, nullptr, nullptr, s, planes);
     auto grouped = [&](const void* wt, const WeightLayout& L, const void* act, int act_rows, float* y, int ldy,
                        const TokenMap& map) {
         if (w.mfma) return launch_batch_mfma(wt, L, act, act_rows, w.slots, y, ldy, s, &map, w.item_tokens, w.max_items);
@@ -149,7 +150,8 @@ hipError_t moe_ffn(const float* x, const float* logits, int n_tok, int n_embd, i
     const TokenMap up_map{r.items, r.n_items, r.slot_tok, n_ff};
     if (e == hipSuccess) e = grouped(wg, Lg, b + w.act_x, n_tok, g, n_ff, up_map);
     if (e == hipSuccess) e = grouped(wu, Lu, b + w.act_x, n_tok, u, n_ff, up_map);
-    if (e == hipSuccess) e = launch_quantize(g, w.slots, n_ff, n_ff, b + w.act_h, nullptr, nullptr, s, u, nullptr);
+    if (e == hipSuccess)
+        e = launch_quantize(g, w.slots, n_ff, n_ff, b + w.act_h, nullptr, nullptr, s, planes, u, nullptr);
     const TokenMap down_map{r.items, r.n_items, nullptr, n_embd};
     if (e == hipSuccess) e = grouped(wd, Ld, b + w.act_h, w.slots, dn, n_embd, down_map);
     if (e == hipSuccess) e = launch_moe_combine(dn, r, n_tok, k, n_embd, out, s);
@@ -262,7 +264,8 @@ public:
         for (int i = 1; i < n && fused; ++i) fused = rs[size_t(i)]->layout.type == rs[0]->layout.type;
         hipError_t e = hipMemcpyAsync(d_x_, x, x_bytes, hipMemcpyHostToDevice, stream_);
         if (e == hipSuccess && !fused)
-            e = launch_quantize(static_cast<const float*>(d_x_), n_tok, n_in, n_in, d_act_, nullptr, nullptr, stream_);
+            e = launch_quantize(static_cast<const float*>(d_x_), n_tok, n_in, n_in, d_act_, nullptr, nullptr, stream_,
+                                planes_for_tokens(n_tok, n_in));
         // y_i at consecutive offsets of the staging buffer; tensors of one
         // K-quant type go out as one grouped launch when the batch is GEMM-sized
         std::vector<float*> dys(static_cast<size_t>(n));
@@ -373,7 +376,8 @@ uint64_t fish_hip_act_bytes(int n_tok, int n_in) { return act_layout(n_tok, n_in
 
 int fish_hip_quantize(const float* x, int n_tok, int n_in, void* act, void* q32_fish, void* q256_fish, void* stream) {
     if (!x || !act || n_tok <= 0 || n_in <= 0 || n_in % 32) return fail(FISH_HIP_ERR_ARG, "quantize: bad arguments");
-    const hipError_t e = launch_quantize(x, n_tok, n_in, n_in, act, q32_fish, q256_fish, as_stream(stream));
+    const hipError_t e =
+        launch_quantize(x, n_tok, n_in, n_in, act, q32_fish, q256_fish, as_stream(stream), planes_for_tokens(n_tok, n_in));
     return e == hipSuccess ? 0 : hip_fail(e, "quantize");
 }
 
@@ -431,7 +435,8 @@ int fish_hip_matmul_tensors(uint32_t type, int n, const void* const* ws, const f
     } else {
         if (!act_workspace || act_workspace_bytes < act_layout(n_tok, n_in).total)
             return fail(FISH_HIP_ERR_ARG, "matmul_tensors: act_workspace missing or too small");
-        e = launch_quantize(x, n_tok, n_in, n_in, act_workspace, nullptr, nullptr, as_stream(stream));
+        e = launch_quantize(x, n_tok, n_in, n_in, act_workspace, nullptr, nullptr, as_stream(stream),
+                            planes_for_tokens(n_tok, n_in));
         if (e == hipSuccess) {
             const int rc = fish_hip_matmul_group(type, n, ws, act_workspace, n_tok, n_in, n_outs, ys, stream);
             if (rc != 0) return rc;
@@ -491,7 +496,8 @@ int fish_hip_silu_mul_quantize(const float* g, const float* u, int n_rows, int n
                                float* h, void* stream) {
     if (!g || !u || !act || n_rows <= 0 || n_ff <= 0 || n_ff % 32)
         return fail(FISH_HIP_ERR_ARG, "silu_mul_quantize: bad arguments");
-    const hipError_t e = launch_quantize(g, n_rows, n_ff, n_ff, act, nullptr, q256_fish, as_stream(stream), u, h);
+    const hipError_t e =
+        launch_quantize(g, n_rows, n_ff, n_ff, act, nullptr, q256_fish, as_stream(stream), kPlanesAll, u, h);
     return e == hipSuccess ? 0 : hip_fail(e, "silu_mul_quantize");
 }
 

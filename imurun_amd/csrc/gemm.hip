@@ -112,6 +112,61 @@ __device__ __forceinline__ void dequant(const Raw& r, int step, uint4 (&out)[2][
     }
 }
 
+// Dequantisation in parts, so that it can be spread over a stage's MFMAs:
+// prep once per item, then part j (0..3) writes its 16-byte pieces.
+//   Q4_K: part j = plane j >> 1 of half j & 1;  Q6_K: parts 0, 1 = both planes of half j.
+struct DqPrep {
+    uint32_t f[2];   // Q4_K: packed 16-bit factors a, b of the two planes
+    short s6[2];     // Q6_K: the two 16-value scales
+};
+
+template <uint32_t T>
+__device__ __forceinline__ DqPrep dequant_prep(const Raw& r, int step) {
+    DqPrep p{};
+    if constexpr (T == kQ4_K) {
+        int sc, mn;
+        k4_scale_min(r.meta.y, r.meta.z, r.meta.w, step & 7, sc, mn);
+        p.f[0] = uint32_t(sc >> 3) * 0x00010001u;
+        p.f[1] = uint32_t(sc & 7) * 0x00010001u;
+    } else {
+        p.s6[0] = short(int8_t(r.sc2 & 0xFF));
+        p.s6[1] = short(int8_t((r.sc2 >> 8) & 0xFF));
+    }
+    return p;
+}
+
+// Writes part j of an item to LDS through put(plane, half, piece).
+template <uint32_t T, typename Put>
+__device__ __forceinline__ void dequant_part(const Raw& r, const DqPrep& p, int j, Put put) {
+    const uint4 c = r.codes;
+    if constexpr (T == kQ4_K) {
+        const int plane = j >> 1, h = j & 1;
+        const uint4 n = h ? make_uint4((c.x >> 4) & 0x0F0F0F0Fu, (c.y >> 4) & 0x0F0F0F0Fu, (c.z >> 4) & 0x0F0F0F0Fu,
+                                       (c.w >> 4) & 0x0F0F0F0Fu)
+                          : make_uint4(c.x & 0x0F0F0F0Fu, c.y & 0x0F0F0F0Fu, c.z & 0x0F0F0F0Fu, c.w & 0x0F0F0F0Fu);
+        const uint32_t f = p.f[plane];
+        put(plane, h, make_uint4(mul4(n.x, f), mul4(n.y, f), mul4(n.z, f), mul4(n.w, f)));
+    } else {
+        if (j >= 2) return;
+        const int h = j;
+        const uint4 n = h ? make_uint4((c.x >> 4) & 0x0F0F0F0Fu, (c.y >> 4) & 0x0F0F0F0Fu, (c.z >> 4) & 0x0F0F0F0Fu,
+                                       (c.w >> 4) & 0x0F0F0F0Fu)
+                          : make_uint4(c.x & 0x0F0F0F0Fu, c.y & 0x0F0F0F0Fu, c.z & 0x0F0F0F0Fu, c.w & 0x0F0F0F0Fu);
+        const uint32_t qh = h ? r.qh.y : r.qh.x;
+        const uint4 q = make_uint4(n.x | ((qh & 0x03030303u) << 4), n.y | (((qh >> 2) & 0x03030303u) << 4),
+                                   n.z | (((qh >> 4) & 0x03030303u) << 4), n.w | (((qh >> 6) & 0x03030303u) << 4));
+        const short s = p.s6[h];
+        const v2s scv = {s, s}, off = {short(-32 * s), short(-32 * s)};
+        uint4 hi, lo;
+        split6(q.x, scv, off, hi.x, lo.x);
+        split6(q.y, scv, off, hi.y, lo.y);
+        split6(q.z, scv, off, hi.z, lo.z);
+        split6(q.w, scv, off, hi.w, lo.w);
+        put(0, h, hi);
+        put(1, h, lo);
+    }
+}
+
 template <uint32_t T, int WT, int WR>
 __global__ __launch_bounds__(64 * WT * WR) __attribute__((amdgpu_waves_per_eu(2))) void gemm_kq_kernel(
     GemmGroup G, ActPtrs A, int n_in, int n_tok, int tok_tiles) {
@@ -215,18 +270,44 @@ __global__ __launch_bounds__(64 * WT * WR) __attribute__((amdgpu_waves_per_eu(2)
 
     // MFMAs of one stage; each step's A registers are refilled with the same
     // step of stage `next` as soon as its MFMAs are issued (one A buffer)
-    auto compute_stage = [&](v4i (&a)[2][SSTEPS], int slot, int next) {
+    // MFMAs of one stage from LDS slot `slot`; each step's A registers are
+    // refilled with the same step of stage `next` as soon as its MFMAs are
+    // issued (one A buffer), the next step's weight operands are read from LDS
+    // before the current step's MFMAs, and the dequantisation of `raw` (stage
+    // dq_stage) into slot dq_slot is spread over the steps so the wavefront has
+    // VALU work between its MFMAs.
+    auto compute_stage = [&](v4i (&a)[2][SSTEPS], int slot, int next, const Raw (&raw)[IPT], int dq_stage,
+                             int dq_slot) {
         const uint4* base = gA + size_t(next) * (SSTEPS * 64);
+        DqPrep prep[IPT];
+#pragma unroll
+        for (int j = 0; j < IPT; ++j) prep[j] = dequant_prep<T>(raw[j], dq_stage * SSTEPS + it_step[j]);
+        v4i bh = __builtin_bit_cast(v4i, s_b[lds_at(slot, 0, 0, half, wr * 32 + l32)]);
+        v4i bl = __builtin_bit_cast(v4i, s_b[lds_at(slot, 1, 0, half, wr * 32 + l32)]);
 #pragma unroll
         for (int s = 0; s < SSTEPS; ++s) {
-            const v4i bh = __builtin_bit_cast(v4i, s_b[lds_at(slot, 0, s, half, wr * 32 + l32)]);
-            const v4i bl = __builtin_bit_cast(v4i, s_b[lds_at(slot, 1, s, half, wr * 32 + l32)]);
+            v4i nbh = bh, nbl = bl;
+            if (s + 1 < SSTEPS) {
+                nbh = __builtin_bit_cast(v4i, s_b[lds_at(slot, 0, s + 1, half, wr * 32 + l32)]);
+                nbl = __builtin_bit_cast(v4i, s_b[lds_at(slot, 1, s + 1, half, wr * 32 + l32)]);
+            }
 #pragma unroll
             for (int b = 0; b < 2; ++b) {
                 accH[b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[b][s], bh, accH[b], 0, 0, 0);
                 accL[b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[b][s], bl, accL[b], 0, 0, 0);
                 a[b][s] = __builtin_bit_cast(v4i, base[a_off[b] + s * 64]);
             }
+#pragma unroll
+            for (int j = 0; j < IPT; ++j) {
+                if constexpr (ITEMS % (64 * NW) != 0) {
+                    if (!it_on[j]) continue;
+                }
+                dequant_part<T>(raw[j], prep[j], s, [&](int plane, int h, uint4 v) {
+                    s_b[lds_at(dq_slot, plane, it_step[j], h, it_row[j])] = v;
+                });
+            }
+            bh = nbh;
+            bl = nbl;
         }
     };
 
@@ -318,21 +399,13 @@ __global__ __launch_bounds__(64 * WT * WR) __attribute__((amdgpu_waves_per_eu(2)
         __syncthreads();
         load_epi(i >> 1);
         load_stage(raw1, min(i + 3, stages - 1));
-        compute_stage(a0, slot, i + 1);
-        {
-            const int ns = slot + 2 >= RING ? slot + 2 - RING : slot + 2;
-            store_stage(raw0, i + 2, ns);
-        }
+        compute_stage(a0, slot, i + 1, raw0, i + 2, slot + 2 >= RING ? slot + 2 - RING : slot + 2);
         store_epi();
         slot = slot + 1 == RING ? 0 : slot + 1;
         // odd stage i + 1: raw1 holds stage i + 3
         __syncthreads();
         load_stage(raw0, min(i + 4, stages - 1));
-        compute_stage(a0, slot, min(i + 2, stages - 1));
-        {
-            const int ns = slot + 2 >= RING ? slot + 2 - RING : slot + 2;
-            store_stage(raw1, i + 3, ns);
-        }
+        compute_stage(a0, slot, min(i + 2, stages - 1), raw1, i + 3, slot + 2 >= RING ? slot + 2 - RING : slot + 2);
         slot = slot + 1 == RING ? 0 : slot + 1;
         epilogue();
     }

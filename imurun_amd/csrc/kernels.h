@@ -8,12 +8,31 @@
 
 namespace fishhip {
 
-// f32 x[n_tok][ldx] -> device activation buffer `act` (act_layout(n_tok, n_in)).
-// aos32 / aos256 (nullable) receive FISH's Q8Act / Q8ActK bytes as well.
-// With u != nullptr the quantized values are silu(x) * u (FFN gate and up,
-// ops.cpp:25-30 and model.cpp:1504-1508), optionally also written to h_out.
+// Planes of an activation buffer a quantization writes (common.h layout):
+// each matmul kernel reads its own, so a batch writes only what its
+// consumers read.
+enum : unsigned {
+    kPlanesGemv = 1,      // q32 d32 s32 q256 d256 s16: GEMV (<= 4 tokens), per-block integers
+    kPlanesBatch32 = 2,   // m32 d32: 16x16 MFMA batch kernel, Q8_0 / Q4_0
+    kPlanesBatch256 = 4,  // m256 d256 bsm: 16x16 MFMA batch kernel, K-quants
+    kPlanesGemm = 8,      // gA gX gJ: the K-quant GEMM
+    kPlanesAll = 15,
+};
+// The planes a matmul of n_tok tokens reads (the dispatch of capi.cpp; rows
+// that are not whole 256-value units only ever go to the GEMV).
+inline unsigned planes_for_tokens(int n_tok, int n_in) {
+    if (n_tok <= 4 || n_in % 256) return kPlanesGemv;
+    if (n_tok <= 64) return kPlanesBatch32 | kPlanesBatch256;
+    return kPlanesBatch32 | kPlanesGemm;
+}
+
+// f32 x[n_tok][ldx] -> device activation buffer `act` (act_layout(n_tok, n_in)),
+// the planes in `planes` only. aos32 / aos256 (nullable) receive FISH's
+// Q8Act / Q8ActK bytes as well. With u != nullptr the quantized values are
+// silu(x) * u (FFN gate and up, ops.cpp:25-30 and model.cpp:1504-1508),
+// optionally also written to h_out.
 hipError_t launch_quantize(const float* x, int n_tok, int n_in, int ldx, void* act, void* aos32, void* aos256,
-                           hipStream_t stream, const float* u = nullptr, float* h_out = nullptr);
+                           hipStream_t stream, unsigned planes, const float* u = nullptr, float* h_out = nullptr);
 
 // Expert routing from router logits (model.cpp:1528-1547) and grouping of
 // the chosen (token, expert) pairs by expert, tokens ascending

@@ -509,7 +509,7 @@ hipError_t launch_moe1(const float* x, const float* logits, int n_embd, int n_ff
     hipError_t e = moe1_type<false>(tg, n_embd, x, A, logits, n_embd, n_ff, n_expert, k, norm, Wg, Wu, r, g, u, h, s);
     // large hidden rows: quantized once here rather than by every down workgroup
     if (e == hipSuccess && k * n_ff > kMoe1LdsHidden)
-        e = launch_quantize(h, k, n_ff, n_ff, act_h, nullptr, nullptr, s);
+        e = launch_quantize(h, k, n_ff, n_ff, act_h, nullptr, nullptr, s, kPlanesGemv);
     if (e == hipSuccess)
         e = moe1_type<true>(td, n_ff, h, A, logits, n_embd, n_ff, n_expert, k, norm, Wd, Wd, r, dn, out, nullptr, s);
     return e;

@@ -74,13 +74,13 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float* __restrict__
         const int sum = wave_sum8(q0 + q1 + q2 + q3);
         if (active) {
             const uint32_t packed = pack4(q0, q1, q2, q3);
-            *reinterpret_cast<uint32_t*>(o.q32 + size_t(t) * n_in + k0) = packed;
+            if (o.q32) *reinterpret_cast<uint32_t*>(o.q32 + size_t(t) * n_in + k0) = packed;
             if (o.m32)
                 *reinterpret_cast<uint32_t*>(o.m32 + size_t(t) * n_in + size_t(c) * 256 + mfma_offset(lane)) = packed;
             const size_t blk = size_t(t) * (n_in / 32) + k0 / 32;
             if ((lane & 7) == 0) {
-                o.d32[blk] = d;
-                o.s32[blk] = sum;
+                if (o.d32) o.d32[blk] = d;
+                if (o.s32) o.s32[blk] = sum;
             }
             if (o.aos32) {
                 uint8_t* b = o.aos32 + blk * 40;
@@ -94,7 +94,7 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float* __restrict__
     }
 
     // ---- 256-value blocks (only when every row is a whole number of them)
-    if (o.q256 && (n_in % 256) == 0) {
+    if ((o.d256 || o.gA || o.aos256) && (n_in % 256) == 0) {
         float amax = a;
         for (int off = 1; off < 64; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
         const float d = amax / 127.0f;
@@ -106,7 +106,7 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float* __restrict__
         g16 += __shfl_xor(g16, 2);
         const int g32 = g16 + __shfl_xor(g16, 4);
         const uint32_t packed = pack4(q0, q1, q2, q3);
-        {
+        if (o.gA) {
             // 32x32x32 MFMA planes: token block tb, step k0 / 32, half h, 4-byte slot of the lane
             const int n_sb = n_in / 256, tb = t >> 5, tt = t & 31;
             const size_t step = size_t(k0 >> 5), h = size_t((lane & 7) >> 2);
@@ -121,12 +121,13 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float* __restrict__
             }
         }
         if (!real) return;
-        *reinterpret_cast<uint32_t*>(o.q256 + size_t(t) * n_in + k0) = packed;
-        *reinterpret_cast<uint32_t*>(o.m256 + size_t(t) * n_in + size_t(c) * 256 + mfma_offset(lane)) = packed;
+        if (o.q256) *reinterpret_cast<uint32_t*>(o.q256 + size_t(t) * n_in + k0) = packed;
+        if (o.m256)
+            *reinterpret_cast<uint32_t*>(o.m256 + size_t(t) * n_in + size_t(c) * 256 + mfma_offset(lane)) = packed;
         const size_t sb = size_t(t) * (n_in / 256) + c;
-        if (lane == 0) o.d256[sb] = d;
-        if ((lane & 3) == 0) o.s16[size_t(t) * (n_in / 16) + k0 / 16] = int16_t(g16);
-        if ((lane & 7) == 0) {
+        if (lane == 0 && o.d256) o.d256[sb] = d;
+        if ((lane & 3) == 0 && o.s16) o.s16[size_t(t) * (n_in / 16) + k0 / 16] = int16_t(g16);
+        if ((lane & 7) == 0 && o.bsm) {
             const int g = lane >> 3;
             o.bsm[sb * 16 + g] = int8_t(g32 >> 6);      // arithmetic shift: floor(bsum / 64)
             o.bsm[sb * 16 + 8 + g] = int8_t(g32 & 63);
@@ -143,26 +144,28 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float* __restrict__
 }  // namespace
 
 hipError_t launch_quantize(const float* x, int n_tok, int n_in, int ldx, void* act, void* aos32, void* aos256,
-                           hipStream_t stream, const float* u, float* h_out) {
+                           hipStream_t stream, unsigned planes, const float* u, float* h_out) {
     const ActLayout L = act_layout(n_tok, n_in);
     if (!L.total) return hipErrorInvalidValue;
     uint8_t* b = static_cast<uint8_t*>(act);
+    const bool gemv = planes & kPlanesGemv, b32 = planes & kPlanesBatch32;
+    const bool b256 = L.has256 && (planes & kPlanesBatch256), gemm = L.has256 && (planes & kPlanesGemm);
     QuantOut o;
-    o.q32 = reinterpret_cast<int8_t*>(b + L.q32);
-    o.d32 = reinterpret_cast<float*>(b + L.d32);
-    o.s32 = reinterpret_cast<int32_t*>(b + L.s32);
-    o.q256 = L.has256 ? reinterpret_cast<int8_t*>(b + L.q256) : nullptr;
-    o.d256 = L.has256 ? reinterpret_cast<float*>(b + L.d256) : nullptr;
-    o.s16 = L.has256 ? reinterpret_cast<int16_t*>(b + L.s16) : nullptr;
-    o.bsm = L.has256 ? reinterpret_cast<int8_t*>(b + L.bsm) : nullptr;
-    o.m32 = L.has256 ? reinterpret_cast<int8_t*>(b + L.m32) : nullptr;
-    o.m256 = L.has256 ? reinterpret_cast<int8_t*>(b + L.m256) : nullptr;
-    o.gA = L.has256 ? reinterpret_cast<int8_t*>(b + L.gA) : nullptr;
-    o.gX = L.has256 ? reinterpret_cast<float*>(b + L.gX) : nullptr;
-    o.gJ = L.has256 ? reinterpret_cast<uint16_t*>(b + L.gJ) : nullptr;
+    o.q32 = gemv ? reinterpret_cast<int8_t*>(b + L.q32) : nullptr;
+    o.d32 = (gemv || b32) ? reinterpret_cast<float*>(b + L.d32) : nullptr;
+    o.s32 = gemv ? reinterpret_cast<int32_t*>(b + L.s32) : nullptr;
+    o.q256 = (gemv && L.has256) ? reinterpret_cast<int8_t*>(b + L.q256) : nullptr;
+    o.d256 = ((gemv && L.has256) || b256) ? reinterpret_cast<float*>(b + L.d256) : nullptr;
+    o.s16 = (gemv && L.has256) ? reinterpret_cast<int16_t*>(b + L.s16) : nullptr;
+    o.bsm = b256 ? reinterpret_cast<int8_t*>(b + L.bsm) : nullptr;
+    o.m32 = (b32 && L.has256) ? reinterpret_cast<int8_t*>(b + L.m32) : nullptr;
+    o.m256 = b256 ? reinterpret_cast<int8_t*>(b + L.m256) : nullptr;
+    o.gA = gemm ? reinterpret_cast<int8_t*>(b + L.gA) : nullptr;
+    o.gX = gemm ? reinterpret_cast<float*>(b + L.gX) : nullptr;
+    o.gJ = gemm ? reinterpret_cast<uint16_t*>(b + L.gJ) : nullptr;
     o.aos32 = static_cast<uint8_t*>(aos32);
     o.aos256 = L.has256 ? static_cast<uint8_t*>(aos256) : nullptr;
-    const long waves = long(L.has256 ? L.n_tb * 32 : n_tok) * ((n_in + 255) / 256);
+    const long waves = long(gemm ? L.n_tb * 32 : n_tok) * ((n_in + 255) / 256);
     const unsigned blocks = unsigned((waves + 3) / 4);
     hipLaunchKernelGGL(quantize_kernel, dim3(blocks), dim3(256), 0, stream, x, n_tok, n_in, ldx, o, u, h_out);
     return hipGetLastError();

@@ -70,7 +70,9 @@ FISH_HIP_API int fish_hip_quantize_rows(uint32_t type, const float* x, void* dst
 /* ---------------------------------------------------------------- operators (device pointers) */
 
 /* ActBatch::quantize (ops.cpp:158-175) on the device: x f32 [n_tok][n_in] ->
- * act (fish_hip_act_bytes). q32_fish / q256_fish (nullable) also receive
+ * act (fish_hip_act_bytes), written with the planes a matmul of n_tok tokens
+ * reads (fish_hip_matmul / _group with the same n_tok, and
+ * fish_hip_block_ints for n_tok <= 4). q32_fish / q256_fish (nullable) also receive
  * FISH's byte layouts Q8Act[n_tok][n_in/32] / Q8ActK[n_tok][n_in/256]
  * (quant.h:58-70), bit-identical to quantize_acts / quantize_acts_k. */
 FISH_HIP_API int fish_hip_quantize(const float* x, int n_tok, int n_in, void* act, void* q32_fish, void* q256_fish,
