@@ -29,12 +29,18 @@ FLAGS = [
 ]
 
 
+# Per-file additions. batch.hip: MFMA results in VGPRs, read directly by the
+# integer scaling that follows each MFMA (no accumulator-register copies).
+EXTRA = {"batch.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
     lang = ["-x", "hip"] if src.endswith(".hip") else []
     flags = [f for f in FLAGS if not (src in NO_CONTRACT and f.startswith("-ffp-contract"))]
     if src in NO_CONTRACT:
         flags.append("-ffp-contract=off")
+    flags += EXTRA.get(src, [])
     cmd = [HIPCC, *flags, *lang, "-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:

@@ -464,6 +464,7 @@ int fish_hip_moe_ffn(const float* x, const float* logits, int n_tok, int n_embd,
     if (!w.total || !x || !logits || !w_gate || !w_up || !w_down || !workspace || !out)
         return fail(FISH_HIP_ERR_ARG, "moe_ffn: bad arguments");
     if (workspace_bytes < w.total) return fail(FISH_HIP_ERR_ARG, "moe_ffn: workspace too small");
+    if (reinterpret_cast<uintptr_t>(workspace) % 256) return fail(FISH_HIP_ERR_ARG, "moe_ffn: workspace not 256-byte aligned");
     if (!type_ok(t_gate) || !type_ok(t_up) || !type_ok(t_down) ||
         ((is_kquant(t_gate) || is_kquant(t_up)) && n_embd % 256) || (is_kquant(t_down) && n_ff % 256))
         return fail(FISH_HIP_ERR_ARG, "moe_ffn: unsupported weight type/shape");

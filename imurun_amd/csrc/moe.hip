@@ -91,12 +91,33 @@ __global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ log
         }
 }
 
+// Exclusive prefix sum of v over the 256 threads of the workgroup (LDS
+// Hillis-Steele); every thread gets its own prefix and the total.
+__device__ __forceinline__ int block_exclusive_scan(int v, int* s, int tid, int& total) {
+    s[tid] = v;
+    __syncthreads();
+    for (int off = 1; off < 256; off <<= 1) {
+        const int a = (tid >= off) ? s[tid - off] : 0;
+        __syncthreads();
+        s[tid] += a;
+        __syncthreads();
+    }
+    const int incl = s[tid];
+    total = s[255];
+    __syncthreads();
+    return incl - v;
+}
+
 // One workgroup: group the (token, choice) pairs by expert, tokens ascending,
 // through an expert x token bitmap (rank = set bits before the token), and
-// write the work list of items of at most item_tokens slots.
+// write the work list of items of at most item_tokens slots (experts
+// ascending, then slot ranges ascending). One thread per expert forms its
+// count, offsets and items from two workgroup prefix sums.
 __global__ __launch_bounds__(256) void group_kernel(int n_tok, int n_expert, int k, int item_tokens, MoeRouting r) {
+    static_assert(kMaxExperts <= 256, "one thread per expert");
     __shared__ uint32_t s_bits[kMaxExperts * (kMaxTok / 32)];
     __shared__ int s_off[kMaxExperts + 1];
+    __shared__ int s_scan[256];
     const int tid = threadIdx.x;
     const int words = (n_tok + 31) / 32;
     for (int i = tid; i < n_expert * words; i += blockDim.x) s_bits[i] = 0;
@@ -106,29 +127,27 @@ __global__ __launch_bounds__(256) void group_kernel(int n_tok, int n_expert, int
         atomicOr(&s_bits[e * words + t / 32], 1u << (t % 32));
     }
     __syncthreads();
-    for (int e = tid; e < n_expert; e += blockDim.x) {
-        int c = 0;
-        for (int q = 0; q < words; ++q) c += __popc(s_bits[e * words + q]);
-        r.counts[e] = c;
-    }
-    __syncthreads();
-    if (tid == 0) {
-        int off = 0, n_items = 0;
-        for (int e = 0; e < n_expert; ++e) {
-            const int c = r.counts[e];
-            s_off[e] = off;
-            r.offsets[e] = off;
-            for (int b = 0; b < c; b += item_tokens) {
-                r.items[3 * n_items] = e;
-                r.items[3 * n_items + 1] = off + b;
-                r.items[3 * n_items + 2] = min(item_tokens, c - b);
-                ++n_items;
-            }
-            off += c;
+    int c = 0;
+    if (tid < n_expert)
+        for (int q = 0; q < words; ++q) c += __popc(s_bits[tid * words + q]);
+    const int n_it = (c + item_tokens - 1) / item_tokens;
+    int total_slots = 0, total_items = 0;
+    const int off = block_exclusive_scan(c, s_scan, tid, total_slots);
+    const int ioff = block_exclusive_scan(n_it, s_scan, tid, total_items);
+    if (tid < n_expert) {
+        s_off[tid] = off;
+        r.counts[tid] = c;
+        r.offsets[tid] = off;
+        for (int b = 0; b < n_it; ++b) {
+            r.items[3 * (ioff + b)] = tid;
+            r.items[3 * (ioff + b) + 1] = off + b * item_tokens;
+            r.items[3 * (ioff + b) + 2] = min(item_tokens, c - b * item_tokens);
         }
-        s_off[n_expert] = off;
-        r.offsets[n_expert] = off;
-        *r.n_items = n_items;
+    }
+    if (tid == 0) {
+        s_off[n_expert] = total_slots;
+        r.offsets[n_expert] = total_slots;
+        *r.n_items = total_items;
     }
     __syncthreads();
     for (int i = tid; i < n_tok * k; i += blockDim.x) {
@@ -142,34 +161,50 @@ __global__ __launch_bounds__(256) void group_kernel(int n_tok, int n_expert, int
     }
 }
 
-// One thread per (token, column).
+// Workgroup (token t, 1024-column chunk): the token's k choices ranked in
+// ascending expert order (thread j counts the choices before its own; the
+// experts of one token are distinct), then four columns per thread add the
+// experts' weighted down rows (workspace rows, 16-byte aligned) in that order.
 __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ down, MoeRouting r, int n_tok, int k,
                                                       int n_embd, float* __restrict__ out) {
-    const long gid = long(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (gid >= long(n_tok) * n_embd) return;
-    const int t = int(gid / n_embd), i = int(gid % n_embd);
-    // the token's choices in ascending expert order (k is small)
-    int order[kMaxK];
-    for (int j = 0; j < k; ++j) order[j] = j;
-    for (int a = 1; a < k; ++a) {
-        const int v = order[a];
-        int b = a - 1;
-        while (b >= 0 && r.sel[t * k + order[b]] > r.sel[t * k + v]) {
-            order[b + 1] = order[b];
-            --b;
-        }
-        order[b + 1] = v;
+    __shared__ int s_sel[kMaxK];
+    __shared__ int s_slot[kMaxK];
+    __shared__ float s_w[kMaxK];
+    const int t = int(blockIdx.x), tid = threadIdx.x;
+    int sel = 0, slot = 0;
+    float w = 0.0f;
+    if (tid < k) {
+        sel = r.sel[t * k + tid];
+        slot = r.tok_slot[t * k + tid];
+        w = r.wsel[t * k + tid];
+        s_sel[tid] = sel;
     }
-    float acc = 0.0f;
+    __syncthreads();
+    if (tid < k) {
+        int rank = 0;
+        for (int j = 0; j < k; ++j) rank += (s_sel[j] < sel) ? 1 : 0;
+        s_slot[rank] = slot;
+        s_w[rank] = w;
+    }
+    __syncthreads();
+    const int i = (int(blockIdx.y) * 256 + tid) * 4;
+    if (i >= n_embd) return;
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     for (int q = 0; q < k; ++q) {
         // w * down is rounded before the add: this file is built without
         // multiply-add contraction
-        const int j = order[q];
-        const int slot = r.tok_slot[t * k + j];
-        const float p = r.wsel[t * k + j] * down[size_t(slot) * n_embd + i];
-        acc = acc + p;
+        const float wq = s_w[q];
+        const float4 d = *reinterpret_cast<const float4*>(down + size_t(s_slot[q]) * n_embd + i);
+        acc.x = acc.x + wq * d.x;
+        acc.y = acc.y + wq * d.y;
+        acc.z = acc.z + wq * d.z;
+        acc.w = acc.w + wq * d.w;
     }
-    out[gid] = acc;
+    float* o = out + size_t(t) * n_embd + i;  // the caller's buffer: 4-byte alignment only
+    o[0] = acc.x;
+    o[1] = acc.y;
+    o[2] = acc.z;
+    o[3] = acc.w;
 }
 
 // ---------------------------------------------------------------- one token
@@ -403,9 +438,9 @@ hipError_t launch_moe_route(const float* logits, int n_tok, int n_expert, int k,
 
 hipError_t launch_moe_combine(const float* down, const MoeRouting& r, int n_tok, int k, int n_embd, float* out,
                               hipStream_t stream) {
-    const long n = long(n_tok) * n_embd;
-    hipLaunchKernelGGL(combine_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0, stream, down, r, n_tok, k,
-                       n_embd, out);
+    if (n_tok <= 0 || k <= 0 || k > kMaxK || n_embd % 4) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(combine_kernel, dim3(unsigned(n_tok), unsigned((n_embd + 1023) / 1024)), dim3(256), 0, stream,
+                       down, r, n_tok, k, n_embd, out);
     return hipGetLastError();
 }
 

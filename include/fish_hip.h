@@ -127,8 +127,9 @@ FISH_HIP_API uint64_t fish_hip_moe_workspace_bytes(int n_tok, int n_embd, int n_
  * x f32 [n_tok][n_embd], logits f32 [n_tok][n_expert], out f32 [n_tok][n_embd];
  * w_gate / w_up: repacked n_expert * n_ff rows of n_embd (fish_hip_repack of
  * the 3-D tensor, experts contiguous as expert_ptr, model.cpp:66-69);
- * w_down: n_expert * n_embd rows of n_ff. This is a new device hook: FISH's
- * own backends never receive expert matmuls (model.cpp:1466-1470). */
+ * w_down: n_expert * n_embd rows of n_ff; workspace 256-byte aligned. This
+ * is a new device hook: FISH's own backends never receive expert matmuls
+ * (model.cpp:1466-1470). */
 FISH_HIP_API int fish_hip_moe_ffn(const float* x, const float* logits, int n_tok, int n_embd, int n_ff, int n_expert,
                                   int k, int norm, uint32_t t_gate, const void* w_gate, uint32_t t_up,
                                   const void* w_up, uint32_t t_down, const void* w_down, void* workspace,
