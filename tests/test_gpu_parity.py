@@ -224,6 +224,25 @@ def test_matmul_tensors_one_token_fused(torch_dev, oracle, t, n_in):
         check_close(got, oracle.matmul_f32(t, r, x, n), f"{fh.TYPE_NAMES[t]} fused K={n_in}")
 
 
+@pytest.mark.parametrize("t", [fh.Q4_0, fh.Q8_0, fh.Q4_K, fh.Q6_K])
+@pytest.mark.parametrize("n_in", [2048, 4096])
+def test_matmul_tensors_one_token_many_rows(torch_dev, oracle, t, n_in):
+    """Gate/up-sized row counts (more workgroups than fit on the device at
+    once), split unevenly between two tensors: bit-identical to quantize +
+    matmul, close to the oracle."""
+    n_outs = [12000, 9000]
+    rows = [packed_weights(oracle, t, n, n_in, 1450 + i) for i, n in enumerate(n_outs)]
+    x = normal(1550 + n_in, (1, n_in))
+    xd = dev_f32(torch_dev, x)
+    ws = [fh.repack(t, dev_u8(torch_dev, r), n_in, n) for r, n in zip(rows, n_outs)]
+    ys = fh.matmul_tensors(t, ws, xd, n_outs)
+    act = fh.quantize(xd)
+    for w, r, n, y in zip(ws, rows, n_outs, ys):
+        got = y.cpu().numpy()
+        assert np.array_equal(got, fh.matmul(t, w, act, 1, n_in, n).cpu().numpy())
+        check_close(got, oracle.matmul_f32(t, r, x, n), f"{fh.TYPE_NAMES[t]} many rows K={n_in}")
+
+
 @pytest.mark.parametrize("t", [fh.Q4_0, fh.Q4_K])
 @pytest.mark.parametrize("n_tok", [3, 130])
 def test_matmul_tensors_batches(torch_dev, oracle, t, n_tok):
