@@ -243,7 +243,10 @@ __global__ __launch_bounds__(64 * kGemvXWaves) void gemv_x_kernel(GemvXGroup G, 
 #pragma unroll
     for (int i = 0; i < XV; ++i) {
         const int k0 = 4 * (tid + 64 * kGemvXWaves * i);
-        xv[i] = k0 < n_in ? *reinterpret_cast<const float4*>(x + k0) : make_float4(0.f, 0.f, 0.f, 0.f);
+        // unconditional load from a clamped address: chunks past the end lie in whole
+        // 32/256-value blocks the quantizer discards, and a load inside a branch would
+        // make the compiler wait for every outstanding load at the join
+        xv[i] = *reinterpret_cast<const float4*>(x + min(k0, n_in - 4));
     }
     // then every weight load of the wavefront (clamped, unconditional)
     int cg[MAXC];
@@ -262,6 +265,8 @@ __global__ __launch_bounds__(64 * kGemvXWaves) void gemv_x_kernel(GemvXGroup G, 
         for (int k = 0; k < MAXC; ++k) f[rb][k] = load_group_wave<T>(W, row, cg[k], n_in, lane);
     }
 
+    // every load is issued before the quantization's first use of x
+    __builtin_amdgcn_sched_barrier(0);
     const LdsAct L{s_codes, s_d, s_s, kGemvXMaxGroups};
     quantize_to_lds<kq, XV, 64 * kGemvXWaves>(xv, n_in, tid, L);
     __syncthreads();

@@ -236,7 +236,10 @@ __global__ __launch_bounds__(64 * kMoe1UpWaves) void moe1_gate_up_kernel(
 #pragma unroll
     for (int i = 0; i < XV; ++i) {
         const int k0 = 4 * (tid + TH * i);
-        xv[i] = k0 < n_embd ? *reinterpret_cast<const float4*>(x + k0) : make_float4(0.f, 0.f, 0.f, 0.f);
+        // unconditional load from a clamped address: chunks past the end lie in whole
+        // 32/256-value blocks the quantizer discards, and a load inside a branch would
+        // make the compiler wait for every outstanding load at the join
+        xv[i] = *reinterpret_cast<const float4*>(x + min(k0, n_embd - 4));
     }
     if (tid < 64) {
         int chosen[kMaxK];
@@ -284,6 +287,8 @@ __global__ __launch_bounds__(64 * kMoe1UpWaves) void moe1_gate_up_kernel(
             fu[rb][q] = load_group_wave<T>(Wu, row, cg[q], n_embd, lane);
         }
     }
+    // every load is issued before the quantization's first use of x
+    __builtin_amdgcn_sched_barrier(0);
     const LdsAct L{s_codes, s_d, s_s, kGemvXMaxGroups};
     quantize_to_lds<kq, XV, TH>(xv, n_embd, tid, L);
     __syncthreads();
@@ -375,6 +380,7 @@ __global__ __launch_bounds__(64 * kMoe1Waves) void moe1_down_kernel(const float*
 #pragma unroll
         for (int q = 0; q < MAXC; ++q) f[s][q] = load_group_wave<T>(Wd, e * n_embd + rowc, cg[q], n_ff, lane);
     }
+    __builtin_amdgcn_sched_barrier(0);
     const LdsAct L{s_codes, s_d, s_s, MG};
     if constexpr (XV > 0) {
         quantize_to_lds<kq, XV, TH>(xv, n_h, tid, L);
