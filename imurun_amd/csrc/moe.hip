@@ -23,7 +23,7 @@ constexpr int kMaxExperts = 256;
 constexpr int kMaxK = 16;
 constexpr int kMaxTok = 2048;  // grouping bitmap: kMaxExperts x kMaxTok bits in LDS
 constexpr int kMoe1UpWaves = 16;      // wavefronts per workgroup: one-token gate+up
-constexpr int kMoe1Waves = 8;         // and down (its k * groups fragments need the registers)
+constexpr int kMoe1DownWaves = 16;    // and down: KMAX expert slots x 16 / KMAX row groups
 constexpr int kMoe1MaxGroups = 1024;  // k * n_ff <= 32768 hidden values in LDS
 
 // One token's routing by one wavefront (model.cpp:1528-1547): softmax over
@@ -326,44 +326,53 @@ __global__ __launch_bounds__(64 * kMoe1UpWaves) void moe1_gate_up_kernel(
 
 // Launch 2, down and combine: every workgroup quantizes the k hidden rows
 // (each row on its own, as ActBatch::quantize does per expert batch) into
-// LDS, and for rows i computes down_e[i] for the k experts in ascending
-// order, writing them and out[i] = sum of w_e * down_e[i] with FISH's
-// separate multiply and add, in that order (model.cpp:1574-1579).
-// XV > 0: the workgroup quantizes the k * n_ff <= 4 * 64 * kMoe1Waves * XV
+// LDS; its 16 wavefronts are KMAX slots x (16 / KMAX) row groups, so each
+// wavefront reads one expert's rows. down_e[i] is written per slot, and
+// out[i] = sum of w_e * down_e[i] is formed from LDS in ascending slot
+// (= expert) order with FISH's separate multiply and add
+// (model.cpp:1574-1579).
+// XV > 0: the workgroup quantizes the k * n_ff <= 4 * 64 * kMoe1DownWaves * XV
 // hidden values itself (small experts); XV == 0: they were quantized by the
 // quantize kernel into `act` (one row per slot) and the workgroup copies
 // them into the same LDS layout.
 template <uint32_t T, int LPR, int MAXC, int KMAX, int XV>
-__global__ __launch_bounds__(64 * kMoe1Waves) void moe1_down_kernel(const float* __restrict__ h, ActPtrs act,
-                                                                    int n_embd, int n_ff, int k, WeightPtrs Wd,
-                                                                    MoeRouting r, float* __restrict__ dn,
-                                                                    float* __restrict__ out) {
+__global__ __launch_bounds__(64 * kMoe1DownWaves) void moe1_down_kernel(const float* __restrict__ h, ActPtrs act,
+                                                                        int n_embd, int n_ff, int k, WeightPtrs Wd,
+                                                                        MoeRouting r, float* __restrict__ dn,
+                                                                        float* __restrict__ out) {
     constexpr bool kq = (T == kQ4_K || T == kQ6_K);
-    constexpr int RPP = 64 / LPR, TH = 64 * kMoe1Waves;
+    constexpr int RPP = 64 / LPR, TH = 64 * kMoe1DownWaves;
+    constexpr int R = kMoe1DownWaves / KMAX, ROWS = R * RPP;         // row groups, rows per workgroup
     constexpr int MG = XV > 0 ? XV * TH * 4 / 32 : kMoe1MaxGroups;  // LDS groups
     __shared__ uint4 s_codes[2 * MG];
     __shared__ float s_d[MG];
     __shared__ int s_s[MG];
     __shared__ int s_exp[kMaxK];
     __shared__ float s_w[kMaxK];
+    __shared__ float s_dn[KMAX][ROWS];
 
-    const int tid = threadIdx.x, lane = tid & 63, sub = lane % LPR;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, sub = lane % LPR;
+    const int slot = wave / R, rw = wave % R;
     const int n_h = k * n_ff;
     float4 xv[XV > 0 ? XV : 1];
 #pragma unroll
     for (int i = 0; i < XV; ++i) {
+        // unconditional load from a clamped address (chunks past the end lie in blocks the
+        // quantizer discards): no load in a branch, so no wait for all outstanding loads
         const int k0 = 4 * (tid + TH * i);
-        xv[i] = k0 < n_h ? *reinterpret_cast<const float4*>(h + k0) : make_float4(0.f, 0.f, 0.f, 0.f);
+        xv[i] = *reinterpret_cast<const float4*>(h + min(k0, n_h - 4));
     }
     if (tid < k) {
-        const int s = r.tok_slot[tid];
-        s_exp[s] = r.sel[tid];
-        s_w[s] = r.wsel[tid];
+        const int sl = r.tok_slot[tid];
+        s_exp[sl] = r.sel[tid];
+        s_w[sl] = r.wsel[tid];
     }
     __syncthreads();
-    const int wave_id = int(blockIdx.x) * kMoe1Waves + (tid >> 6);
-    const int row = wave_id * RPP + lane / LPR;
+    const int lrow = rw * RPP + lane / LPR;  // row within the workgroup
+    const int row = int(blockIdx.x) * ROWS + lrow;
     const int rowc = min(row, n_embd - 1);
+    const int sc = min(slot, k - 1);  // wavefronts of slots past k read the last slot's rows, unused
+    const int e = s_exp[sc];
     const int groups = n_ff / 32;
     int cg[MAXC];
     bool cv[MAXC];
@@ -373,13 +382,9 @@ __global__ __launch_bounds__(64 * kMoe1Waves) void moe1_down_kernel(const float*
         cv[q] = c < groups;
         cg[q] = cv[q] ? c : groups - 1;
     }
-    Frag f[KMAX][MAXC];
+    Frag f[MAXC];
 #pragma unroll
-    for (int s = 0; s < KMAX; ++s) {
-        const int e = s_exp[min(s, k - 1)];
-#pragma unroll
-        for (int q = 0; q < MAXC; ++q) f[s][q] = load_group_wave<T>(Wd, e * n_embd + rowc, cg[q], n_ff, lane);
-    }
+    for (int q = 0; q < MAXC; ++q) f[q] = load_group_wave<T>(Wd, e * n_embd + rowc, cg[q], n_ff, lane);
     __builtin_amdgcn_sched_barrier(0);
     const LdsAct L{s_codes, s_d, s_s, MG};
     if constexpr (XV > 0) {
@@ -404,27 +409,29 @@ __global__ __launch_bounds__(64 * kMoe1Waves) void moe1_down_kernel(const float*
         }
     }
     __syncthreads();
-    if (wave_id * RPP >= n_embd) return;  // uniform over the wavefront
-    float acc = 0.0f;
+    float d = 0.0f;
 #pragma unroll
-    for (int s = 0; s < KMAX; ++s) {
-        float d = 0.0f;
-        const int sc = min(s, k - 1);  // slots past k compute on the last slot's rows and are discarded
-#pragma unroll
-        for (int q = 0; q < MAXC; ++q) {
-            const float v = group_dot<T>(f[s][q], lds_act<T>(L, sc * groups + cg[q]));
-            d += cv[q] ? v : 0.0f;
-        }
-#pragma unroll
-        for (int off = LPR / 2; off > 0; off >>= 1) d += __shfl_xor(d, off);
-        if (s < k) {
-            // w * down rounded, then added: this file is built without contraction
-            const float p = s_w[s] * d;
-            acc = acc + p;
-            if (sub == 0 && row < n_embd) dn[size_t(s) * n_embd + row] = d;
-        }
+    for (int q = 0; q < MAXC; ++q) {
+        const float v = group_dot<T>(f[q], lds_act<T>(L, sc * groups + cg[q]));
+        d += cv[q] ? v : 0.0f;
     }
-    if (sub == 0 && row < n_embd) out[row] = acc;
+#pragma unroll
+    for (int off = LPR / 2; off > 0; off >>= 1) d += __shfl_xor(d, off);
+    if (sub == 0) {
+        s_dn[slot][lrow] = d;
+        if (slot < k && row < n_embd) dn[size_t(slot) * n_embd + row] = d;
+    }
+    __syncthreads();
+    if (tid < ROWS) {
+        const int orow = int(blockIdx.x) * ROWS + tid;
+        float acc = 0.0f;
+        for (int j = 0; j < k; ++j) {
+            // w * down rounded, then added: this file is built without contraction
+            const float p = s_w[j] * s_dn[j][tid];
+            acc = acc + p;
+        }
+        if (orow < n_embd) out[orow] = acc;
+    }
 }
 
 }  // namespace
@@ -460,7 +467,9 @@ template <uint32_t T, int LPR, int MAXC>
 hipError_t moe1_gate_up_launch(const float* x, const float* logits, int n_embd, int n_ff, int n_expert, int k,
                                int norm, const WeightPtrs& Wg, const WeightPtrs& Wu, const MoeRouting& r, float* g,
                                float* u, float* h, hipStream_t s) {
-    constexpr int RB = gemv_rb<T, MAXC>();
+    // one row (of gate and of up) per wavefront: the fewest registers and the most workgroups
+    // (two rows per wavefront left one 16-wavefront workgroup per CU)
+    constexpr int RB = 1;
     constexpr int RPW = (64 / LPR) * RB;
     constexpr int TH = 64 * kMoe1UpWaves;
     constexpr int XV = LPR == 64 ? (64 * 32 * MAXC / 4 + TH - 1) / TH : 1;
@@ -470,23 +479,30 @@ hipError_t moe1_gate_up_launch(const float* x, const float* logits, int n_embd, 
     return hipGetLastError();
 }
 
-// hidden values a workgroup quantizes itself: up to 4 chunks per thread
-constexpr int kMoe1LdsHidden = 4 * 64 * kMoe1Waves * 4;
+// hidden values a workgroup quantizes itself: up to 2 chunks per thread
+constexpr int kMoe1LdsXV = 2;
+constexpr int kMoe1LdsHidden = 4 * 64 * kMoe1DownWaves * kMoe1LdsXV;
+
+template <uint32_t T, int LPR, int MAXC, int KMAX>
+hipError_t moe1_down_launch_k(const float* h, const ActPtrs& act, int n_embd, int n_ff, int k, const WeightPtrs& Wd,
+                              const MoeRouting& r, float* dn, float* out, hipStream_t s) {
+    constexpr int ROWS = (kMoe1DownWaves / KMAX) * (64 / LPR);
+    const dim3 grid(unsigned((n_embd + ROWS - 1) / ROWS)), block(64 * kMoe1DownWaves);
+    if (k * n_ff <= kMoe1LdsHidden)
+        hipLaunchKernelGGL((moe1_down_kernel<T, LPR, MAXC, KMAX, kMoe1LdsXV>), grid, block, 0, s, h, act, n_embd, n_ff,
+                           k, Wd, r, dn, out);
+    else
+        hipLaunchKernelGGL((moe1_down_kernel<T, LPR, MAXC, KMAX, 0>), grid, block, 0, s, h, act, n_embd, n_ff, k, Wd,
+                           r, dn, out);
+    return hipGetLastError();
+}
 
 template <uint32_t T, int LPR, int MAXC>
 hipError_t moe1_down_launch(const float* h, const ActPtrs& act, int n_embd, int n_ff, int k, const WeightPtrs& Wd,
                             const MoeRouting& r, float* dn, float* out, hipStream_t s) {
-    const int waves = (n_embd + 64 / LPR - 1) / (64 / LPR);
-    const dim3 grid(unsigned((waves + kMoe1Waves - 1) / kMoe1Waves)), block(64 * kMoe1Waves);
-    const bool lds = k * n_ff <= kMoe1LdsHidden;
-    if (k <= 2) {
-        if (lds) hipLaunchKernelGGL((moe1_down_kernel<T, LPR, MAXC, 2, 4>), grid, block, 0, s, h, act, n_embd, n_ff, k, Wd, r, dn, out);
-        else hipLaunchKernelGGL((moe1_down_kernel<T, LPR, MAXC, 2, 0>), grid, block, 0, s, h, act, n_embd, n_ff, k, Wd, r, dn, out);
-    } else {
-        if (lds) hipLaunchKernelGGL((moe1_down_kernel<T, LPR, MAXC, 8, 4>), grid, block, 0, s, h, act, n_embd, n_ff, k, Wd, r, dn, out);
-        else hipLaunchKernelGGL((moe1_down_kernel<T, LPR, MAXC, 8, 0>), grid, block, 0, s, h, act, n_embd, n_ff, k, Wd, r, dn, out);
-    }
-    return hipGetLastError();
+    if (k <= 2) return moe1_down_launch_k<T, LPR, MAXC, 2>(h, act, n_embd, n_ff, k, Wd, r, dn, out, s);
+    if (k <= 4) return moe1_down_launch_k<T, LPR, MAXC, 4>(h, act, n_embd, n_ff, k, Wd, r, dn, out, s);
+    return moe1_down_launch_k<T, LPR, MAXC, 8>(h, act, n_embd, n_ff, k, Wd, r, dn, out, s);
 }
 
 // (LPR, groups per lane) as the GEMV picks them
