@@ -143,7 +143,9 @@ def run_prefill(args, torch, fh, dev):
     }
     reps = max(10, args.steps // 4)
     layer_us = graph_time(torch, [lambda: [f() for f in parts.values()]], reps)
-    per = {name: graph_time(torch, [f], reps) for name, f in parts.items()}
+    # each part as eight back-to-back calls in one graph: a one-launch graph per replay would
+    # time the host's graph launches for the short parts, not the kernels
+    per = {name: graph_time_seq(torch, [f] * 8, reps) for name, f in parts.items()}
     return ops, layer_us, per
 
 

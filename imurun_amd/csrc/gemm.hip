@@ -457,7 +457,9 @@ hipError_t launch_gemm_group(int n, const void* const* ws, const WeightLayout* W
     const ActPtrs A = act_ptrs(act, AL);
     switch (type) {
         case kQ4_K: return gemm_launch<kQ4_K, 2, 2>(G, n_outs, A, n_in, n_tok, s);
-        case kQ6_K: return gemm_launch<kQ6_K, 2, 2>(G, n_outs, A, n_in, n_tok, s);
+        // Q6_K (no mins MFMA, heavier dequantization): four token wavefronts share each
+        // dequantized stage (measured 8-11 % faster on the 4096 x 14336 down projection)
+        case kQ6_K: return gemm_launch<kQ6_K, 4, 1>(G, n_outs, A, n_in, n_tok, s);
         default: return hipErrorInvalidValue;
     }
 }
