@@ -60,6 +60,18 @@ def test_bad_arguments_return_errors_without_device_work():
     assert "bad arguments" in fh.last_error()
     assert L.fish_hip_matmul(fh.Q4_K, None, None, 1, 4000, 16, None, None) == -1
     assert L.fish_hip_supports(fh.Q4_K) == 1 and L.fish_hip_supports(3) == 0
+    # moe_ffn: a workspace that is not 256-byte aligned is refused before any device work
+    # (the pointers are never dereferenced on this path)
+    n_tok, E, F, NE, K = 4, 256, 256, 8, 2
+    nb = fh.moe_workspace_bytes(n_tok, E, F, NE, K)
+    assert nb > 0
+    fake = 1 << 20
+    assert L.fish_hip_moe_ffn(fake, fake, n_tok, E, F, NE, K, 1, fh.Q4_K, fake, fh.Q4_K, fake, fh.Q4_K, fake,
+                              fake + 16, nb, fake, None) == -1
+    assert "aligned" in fh.last_error()
+    assert L.fish_hip_moe_ffn(fake, fake, n_tok, E, F, NE, K, 1, fh.Q4_K, fake, fh.Q4_K, fake, fh.Q4_K, fake,
+                              fake, nb - 1, fake, None) == -1
+    assert "too small" in fh.last_error()
 
 
 @pytest.mark.parametrize("t", [fh.Q8_0, fh.Q4_0, fh.Q4_K, fh.Q6_K])
