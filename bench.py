@@ -312,6 +312,26 @@ def run_kernel_only(args, torch, fh, dev):
     return 0
 
 
+def run_kernel_only_gemm(args, torch, fh, dev):
+    """For rocprofv3 counter passes: one M = 512 prefill GEMM (Q4_K gate 14336x4096 or Q6_K down
+    4096x14336, the prefill layer's weights: 1024 distinct packed rows, repeated) on activations
+    quantized once, `--steps` times back to back."""
+    from imurun_amd.synth import normal
+    M = 512
+    t, n_out, n_in, seed = {"gemm_gate": (fh.Q4_K, F, E, 204), "gemm_down": (fh.Q6_K, E, F, 206)}[args.kernel_only]
+    base = fh.quantize_rows(t, normal(seed, (1024, n_in), 0.02))
+    w = fh.repack(t, torch.from_numpy(base).to(dev).repeat(n_out // 1024), n_in, n_out)
+    x = torch.from_numpy(normal(210, (M, n_in))).to(dev)
+    act = fh.quantize(x)
+    y = torch.empty((M, n_out), dtype=torch.float32, device=dev)
+    for _ in range(args.steps):
+        fh.matmul_group(t, [w], act, M, n_in, [n_out], ys=[y])
+    torch.cuda.synchronize()
+    print(json.dumps({"kernel_only": f"gemm_kq_kernel {fh.TYPE_NAMES[t]} {n_out}x{n_in}, M={M}",
+                      "launches": args.steps}))
+    return 0
+
+
 def measured_traffic():
     """HBM bytes per launch of the dominant kernel from the committed counter passes, or None."""
     try:
@@ -330,8 +350,10 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
-    ap.add_argument("--kernel-only", action="store_true",
-                    help="run only the dominant launch and a calibration copy (for rocprofv3 --pmc)")
+    ap.add_argument("--kernel-only", nargs="?", const="gemv_gate_up", default=None,
+                    choices=["gemv_gate_up", "gemm_gate", "gemm_down"],
+                    help="run only one launch --steps times (for rocprofv3 --pmc): the dominant GEMV "
+                         "(then a calibration copy), or the M=512 Q4_K gate / Q6_K down GEMM")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the path shards by rows/experts "
@@ -343,8 +365,10 @@ def main() -> int:
     assert torch.cuda.is_available(), "bench needs a ROCm GPU"
     dev = torch.device("cuda:0")
     fh.load()
-    if args.kernel_only:
+    if args.kernel_only == "gemv_gate_up":
         return run_kernel_only(args, torch, fh, dev)
+    if args.kernel_only:
+        return run_kernel_only_gemm(args, torch, fh, dev)
 
     step_bytes, gate_bytes = gemv_step_bytes()
     elapsed, copies, gate_us = run_gemv(args, torch, fh, dev)
