@@ -24,8 +24,6 @@
 // the A-operand registers (the quantizer writes them in operand order), one
 // stage ahead; two wavefronts per SIMD hide each other's latencies. The lane that owns an output owns its weight row, so row
 // scales are lane scalars; token scales come in output-register order.
-#include <type_traits>
-
 #include "common.h"
 #include "kernels.h"
 
@@ -424,308 +422,7 @@ __global__ __launch_bounds__(64 * WT * WR) __attribute__((amdgpu_waves_per_eu(2)
     }
 }
 
-// Software-pipelined form of the kernel above: two accumulator sets
-// alternate by super-block, and the epilogue of super-block s - 1 (its mins
-// MFMA first, then a quarter of its outputs after each step's MFMAs) runs
-// inside super-block s's first stage, so its VALU work issues while MFMAs
-// that do not depend on it execute. The first MFMA of every super-block
-// starts from zero (no reset pass). Epilogue data in LDS is double-buffered
-// by super-block parity. One wavefront per SIMD: the two sets, the mins
-// results and the operand buffers need more than half the register file.
 template <uint32_t T, int WT, int WR>
-__global__ __launch_bounds__(64 * WT * WR) __attribute__((amdgpu_waves_per_eu(1))) void gemm_kq_pipe_kernel(
-    GemmGroup G, ActPtrs A, int n_in, int n_tok, int tok_tiles) {
-    constexpr int NW = WT * WR;
-    constexpr int RWG = 32 * WR;
-    constexpr int ITEMS = RWG * SSTEPS;
-    constexpr int IPT = (ITEMS + 64 * NW - 1) / (64 * NW);
-    constexpr int SHIFT = (T == kQ4_K) ? 3 : 6;
-    constexpr int EJ = (T == kQ4_K) ? 2 * WT * 64 : 1;  // mins-operand pieces
-    constexpr int EX = 2 * WT * 2 * 4;                  // token-scale pieces
-    __shared__ uint4 s_b[RING * 2 * SSTEPS * 2 * RWG];
-    __shared__ uint4 s_meta[2][RWG];
-    __shared__ float4 s_xd[2][EX];
-    __shared__ uint4 s_j[2][EJ];
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int l32 = lane & 31, half = lane >> 5;
-    const int wt = wave % WT, wr = wave / WT;
-
-    const int n_wg = G.tiles_end[G.n - 1] * tok_tiles;
-    int lin = int(blockIdx.x);
-    if ((n_wg & 7) == 0) lin = (lin & 7) * (n_wg >> 3) + (lin >> 3);
-    int row_tile = lin / tok_tiles;
-    const int tok_tile = lin % tok_tiles;
-    int gm = 0;
-#pragma unroll
-    for (int j = 1; j < kGemmGroupMax; ++j)
-        if (j < G.n && row_tile >= G.tiles_end[j - 1]) gm = j;
-    if (gm > 0) row_tile -= G.tiles_end[gm - 1];
-    const WeightPtrs W = G.w[gm];
-    const int n_out = G.n_out[gm], ldy = G.ldy[gm];
-    float* __restrict__ y = G.y[gm];
-    const int row0 = row_tile * RWG;
-
-    const int steps = n_in / 32, stages = steps / SSTEPS, n_sb = n_in / 256;
-    const int tb0 = tok_tile * (2 * WT) + wt * 2;
-    int tb[2];
-    tb[0] = min(tb0, A.n_tb - 1);
-    tb[1] = min(tb0 + 1, A.n_tb - 1);
-    const int my_row = row0 + wr * 32 + l32;
-
-    int it_row[IPT], it_step[IPT];
-    bool it_on[IPT];
-#pragma unroll
-    for (int j = 0; j < IPT; ++j) {
-        const int item = tid + 64 * NW * j;
-        it_on[j] = item < ITEMS;
-        const int it = it_on[j] ? item : 0;
-        it_row[j] = it >> 2;
-        it_step[j] = it & 3;
-    }
-    auto lds_at = [&](int st, int plane, int s, int h, int r) {
-        return (((st * 2 + plane) * SSTEPS + s) * 2 + h) * RWG + (r ^ (s << 2));
-    };
-    auto load_stage = [&](Raw (&raw)[IPT], int stage) {
-#pragma unroll
-        for (int j = 0; j < IPT; ++j)
-            load_raw<T>(raw[j], W, min(row0 + it_row[j], n_out - 1), stage * SSTEPS + it_step[j], n_in);
-    };
-    auto store_stage = [&](const Raw (&raw)[IPT], int stage, int slot) {
-#pragma unroll
-        for (int j = 0; j < IPT; ++j) {
-            if constexpr (ITEMS % (64 * NW) != 0) {
-                if (!it_on[j]) continue;
-            }
-            uint4 o[2][2];
-            dequant<T>(raw[j], stage * SSTEPS + it_step[j], o);
-#pragma unroll
-            for (int p = 0; p < 2; ++p)
-#pragma unroll
-                for (int h = 0; h < 2; ++h) s_b[lds_at(slot, p, it_step[j], h, it_row[j])] = o[p][h];
-        }
-    };
-    const uint4* gA = reinterpret_cast<const uint4*>(A.gA);
-    int a_off[2];
-#pragma unroll
-    for (int b = 0; b < 2; ++b) a_off[b] = tb[b] * steps * 64 + lane;
-    auto load_a = [&](v4i (&a)[2][SSTEPS], int stage) {
-        const uint4* base = gA + size_t(stage) * (SSTEPS * 64);
-#pragma unroll
-        for (int b = 0; b < 2; ++b)
-#pragma unroll
-            for (int s = 0; s < SSTEPS; ++s) a[b][s] = __builtin_bit_cast(v4i, base[a_off[b] + s * 64]);
-    };
-
-    v16i accH[2][2], accL[2][2];  // [set][block]
-    v16f accY[2];
-#pragma unroll
-    for (int b = 0; b < 2; ++b) accY[b] = v16f{};
-    const v16i zero16 = v16i{};
-
-    // one stage's MFMAs into accumulator set S (FIRST: a new super-block, step 0 starts from
-    // zero), the A refill of stage `next`, the dequantisation of `raw` into dq_slot, and after
-    // each step's MFMAs the callback epi(step) (the previous super-block's epilogue quarter)
-    auto compute_stage = [&](auto set_c, auto first_c, v4i (&a)[2][SSTEPS], int slot, int next,
-                             const Raw (&raw)[IPT], int dq_stage, int dq_slot, auto&& epi) {
-        constexpr int S = decltype(set_c)::value;
-        constexpr bool FIRST = decltype(first_c)::value;
-        const uint4* base = gA + size_t(next) * (SSTEPS * 64);
-        DqPrep prep[IPT];
-#pragma unroll
-        for (int j = 0; j < IPT; ++j) prep[j] = dequant_prep<T>(raw[j], dq_stage * SSTEPS + it_step[j]);
-        v4i bh = __builtin_bit_cast(v4i, s_b[lds_at(slot, 0, 0, half, wr * 32 + l32)]);
-        v4i bl = __builtin_bit_cast(v4i, s_b[lds_at(slot, 1, 0, half, wr * 32 + l32)]);
-#pragma unroll
-        for (int s = 0; s < SSTEPS; ++s) {
-            v4i nbh = bh, nbl = bl;
-            if (s + 1 < SSTEPS) {
-                nbh = __builtin_bit_cast(v4i, s_b[lds_at(slot, 0, s + 1, half, wr * 32 + l32)]);
-                nbl = __builtin_bit_cast(v4i, s_b[lds_at(slot, 1, s + 1, half, wr * 32 + l32)]);
-            }
-#pragma unroll
-            for (int b = 0; b < 2; ++b) {
-                const bool z = FIRST && s == 0;
-                accH[S][b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[b][s], bh, z ? zero16 : accH[S][b], 0, 0, 0);
-                accL[S][b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[b][s], bl, z ? zero16 : accL[S][b], 0, 0, 0);
-                a[b][s] = __builtin_bit_cast(v4i, base[a_off[b] + s * 64]);
-            }
-            epi(s);
-#pragma unroll
-            for (int j = 0; j < IPT; ++j) {
-                if constexpr (ITEMS % (64 * NW) != 0) {
-                    if (!it_on[j]) continue;
-                }
-                dequant_part<T>(raw[j], prep[j], s, [&](int plane, int h, uint4 v) {
-                    s_b[lds_at(dq_slot, plane, it_step[j], h, it_row[j])] = v;
-                });
-            }
-            bh = nbh;
-            bl = nbl;
-        }
-    };
-    auto no_epi = [](int) {};
-
-    uint4 e_meta = make_uint4(0, 0, 0, 0), e_j = make_uint4(0, 0, 0, 0);
-    float4 e_x = make_float4(0.f, 0.f, 0.f, 0.f);
-    const int e_tb = min(tok_tile * (2 * WT) + (tid >> 6) % (2 * WT), A.n_tb - 1);
-    auto load_epi = [&](int sb) {
-        const size_t r = size_t(min(row0 + tid % RWG, n_out - 1));
-        if constexpr (T == kQ4_K) e_meta = *reinterpret_cast<const uint4*>(W.aux + (r * n_sb + sb) * 16);
-        else e_meta.x = W.d[r * n_sb + sb];
-        if constexpr (T == kQ4_K)
-            e_j = *reinterpret_cast<const uint4*>(A.gJ + ((size_t(e_tb) * n_sb + sb) * 64 + lane) * 8);
-        const int xi = tid % EX, b = xi >> 3, q = xi & 7;
-        const int tbb = min(tok_tile * (2 * WT) + b, A.n_tb - 1);
-        e_x = reinterpret_cast<const float4*>(A.gX + (size_t(tbb) * n_sb + sb) * 32)[q];
-    };
-    auto store_epi = [&](int par) {
-        s_meta[par][tid % RWG] = e_meta;
-        if constexpr (T == kQ4_K) s_j[par][tid % EJ] = e_j;
-        s_xd[par][tid % EX] = e_x;
-    };
-
-    // epilogue of a super-block whose data is in parity par: row scales and mins MFMA first,
-    // then four quarters y += xd * (d * I - dmin * J)   (Q6_K: y += xd * (d * I))
-    struct Epi {
-        float d, dmin;
-        v16f J[2];
-    };
-    auto epi_begin = [&](int par) {
-        Epi p;
-        p.dmin = 0.0f;
-        const uint4 m = s_meta[par][wr * 32 + l32];
-        if constexpr (T == kQ4_K) {
-            p.d = f16_bits_to_f32(uint16_t(m.x & 0xFFFF));
-            p.dmin = f16_bits_to_f32(uint16_t(m.x >> 16));
-            const _Float16 f = half ? _Float16(1.0f) : _Float16(64.0f);
-            v8h bj;
-#pragma unroll
-            for (int g = 0; g < 8; ++g) {
-                int scv, mn;
-                k4_scale_min(m.y, m.z, m.w, g, scv, mn);
-                bj[g] = _Float16(float(mn)) * f;
-            }
-#pragma unroll
-            for (int b = 0; b < 2; ++b) {
-                const v8h aj = __builtin_bit_cast(v8h, s_j[par][(wt * 2 + b) * 64 + lane]);
-                p.J[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(aj, bj, v16f{}, 0, 0, 0);
-            }
-        } else {
-            p.d = f16_bits_to_f32(uint16_t(m.x));
-        }
-        return p;
-    };
-    auto epi_chunk = [&](auto set_c, const Epi& p, int par, int c) {
-        constexpr int S = decltype(set_c)::value;
-#pragma unroll
-        for (int b = 0; b < 2; ++b) {
-            const float4 xv = s_xd[par][(wt * 2 + b) * 8 + half * 4 + c];
-            const float xd[4] = {xv.x, xv.y, xv.z, xv.w};
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int i = 4 * c + r;
-                const float fi = float((accH[S][b][i] << SHIFT) + accL[S][b][i]);
-                float t = p.d * fi;
-                if constexpr (T == kQ4_K) t = fmaf(-p.dmin, p.J[b][i], t);
-                accY[b][i] = fmaf(xd[r], t, accY[b][i]);
-            }
-        }
-    };
-    using I0 = std::integral_constant<int, 0>;
-    using I1 = std::integral_constant<int, 1>;
-    using TRUE_ = std::integral_constant<bool, true>;
-    using FALSE_ = std::integral_constant<bool, false>;
-
-    // ---- prologue: stages 0 and 1 into the ring, stage 2 raw in registers
-    Raw raw0[IPT], raw1[IPT];
-    load_stage(raw0, 0);
-    load_stage(raw1, min(1, stages - 1));
-    store_stage(raw0, 0, 0);
-    store_stage(raw1, 1, 1);
-    load_stage(raw0, min(2, stages - 1));
-    v4i a0[2][SSTEPS];
-    load_a(a0, 0);
-
-    // stage j computes from slot j % 3, refills A with stage j + 1, dequantises raw (stage j + 2,
-    // loaded one stage earlier) into slot (j + 2) % 3 and loads raw for stage j + 3
-    int slot = 0;
-    auto next_slot = [](int sl, int k) { return (sl + k) % RING; };
-    const int pairs = n_sb / 2;
-    for (int p = 0; p < pairs; ++p) {
-        const int i0 = 4 * p;
-        // super-block 2p (set 0), first stage: the epilogue of super-block 2p - 1 (set 1) under it
-        __syncthreads();
-        load_epi(2 * p);
-        load_stage(raw1, min(i0 + 3, stages - 1));
-        if (p > 0) {
-            const Epi ep = epi_begin(1);
-            compute_stage(I0{}, TRUE_{}, a0, slot, i0 + 1, raw0, i0 + 2, next_slot(slot, 2),
-                          [&](int c) { epi_chunk(I1{}, ep, 1, c); });
-        } else {
-            compute_stage(I0{}, TRUE_{}, a0, slot, i0 + 1, raw0, i0 + 2, next_slot(slot, 2), no_epi);
-        }
-        store_epi(0);
-        slot = next_slot(slot, 1);
-        __syncthreads();
-        load_stage(raw0, min(i0 + 4, stages - 1));
-        compute_stage(I0{}, FALSE_{}, a0, slot, min(i0 + 2, stages - 1), raw1, i0 + 3, next_slot(slot, 2), no_epi);
-        slot = next_slot(slot, 1);
-        // super-block 2p + 1 (set 1), first stage: the epilogue of super-block 2p (set 0) under it
-        __syncthreads();
-        load_epi(2 * p + 1);
-        load_stage(raw1, min(i0 + 5, stages - 1));
-        {
-            const Epi ep = epi_begin(0);
-            compute_stage(I1{}, TRUE_{}, a0, slot, min(i0 + 3, stages - 1), raw0, i0 + 4, next_slot(slot, 2),
-                          [&](int c) { epi_chunk(I0{}, ep, 0, c); });
-        }
-        store_epi(1);
-        slot = next_slot(slot, 1);
-        __syncthreads();
-        load_stage(raw0, min(i0 + 6, stages - 1));
-        compute_stage(I1{}, FALSE_{}, a0, slot, min(i0 + 4, stages - 1), raw1, i0 + 5, next_slot(slot, 2), no_epi);
-        slot = next_slot(slot, 1);
-    }
-    if (n_sb & 1) {
-        // a last, odd super-block (set 0)
-        const int i0 = 4 * pairs;
-        __syncthreads();
-        load_epi(n_sb - 1);
-        load_stage(raw1, min(i0 + 3, stages - 1));
-        if (pairs > 0) {
-            const Epi ep = epi_begin(1);
-            compute_stage(I0{}, TRUE_{}, a0, slot, min(i0 + 1, stages - 1), raw0, i0 + 2, next_slot(slot, 2),
-                          [&](int c) { epi_chunk(I1{}, ep, 1, c); });
-        } else {
-            compute_stage(I0{}, TRUE_{}, a0, slot, min(i0 + 1, stages - 1), raw0, i0 + 2, next_slot(slot, 2), no_epi);
-        }
-        store_epi(0);
-        slot = next_slot(slot, 1);
-        __syncthreads();
-        load_stage(raw0, min(i0 + 4, stages - 1));
-        compute_stage(I0{}, FALSE_{}, a0, slot, min(i0 + 2, stages - 1), raw1, i0 + 3, next_slot(slot, 2), no_epi);
-        const Epi ep = epi_begin(0);
-#pragma unroll
-        for (int c = 0; c < 4; ++c) epi_chunk(I0{}, ep, 0, c);
-    } else {
-        const Epi ep = epi_begin(1);
-#pragma unroll
-        for (int c = 0; c < 4; ++c) epi_chunk(I1{}, ep, 1, c);
-    }
-
-    if (my_row < n_out) {
-#pragma unroll
-        for (int b = 0; b < 2; ++b)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int t = (tb0 + b) * 32 + 8 * (i >> 2) + 4 * half + (i & 3);
-                if (t < n_tok) y[size_t(t) * ldy + my_row] = accY[b][i];
-            }
-    }
-}
-
-template <uint32_t T, int WT, int WR, bool PIPE = false>
 hipError_t gemm_launch(GemmGroup G, const int* n_outs, const ActPtrs& A, int n_in, int n_tok, hipStream_t s) {
     int tiles = 0;
     for (int j = 0; j < G.n; ++j) {
@@ -733,12 +430,8 @@ hipError_t gemm_launch(GemmGroup G, const int* n_outs, const ActPtrs& A, int n_i
         G.tiles_end[j] = tiles;
     }
     const int tok_tiles = (n_tok + 64 * WT - 1) / (64 * WT);
-    if constexpr (PIPE)
-        hipLaunchKernelGGL((gemm_kq_pipe_kernel<T, WT, WR>), dim3(unsigned(tiles * tok_tiles)), dim3(64 * WT * WR), 0,
-                           s, G, A, n_in, n_tok, tok_tiles);
-    else
-        hipLaunchKernelGGL((gemm_kq_kernel<T, WT, WR>), dim3(unsigned(tiles * tok_tiles)), dim3(64 * WT * WR), 0, s, G,
-                           A, n_in, n_tok, tok_tiles);
+    hipLaunchKernelGGL((gemm_kq_kernel<T, WT, WR>), dim3(unsigned(tiles * tok_tiles)), dim3(64 * WT * WR), 0, s, G, A,
+                       n_in, n_tok, tok_tiles);
     return hipGetLastError();
 }
 
@@ -763,10 +456,10 @@ hipError_t launch_gemm_group(int n, const void* const* ws, const WeightLayout* W
     }
     const ActPtrs A = act_ptrs(act, AL);
     switch (type) {
-        case kQ4_K: return gemm_launch<kQ4_K, 2, 2, true>(G, n_outs, A, n_in, n_tok, s);
+        case kQ4_K: return gemm_launch<kQ4_K, 2, 2>(G, n_outs, A, n_in, n_tok, s);
         // Q6_K (no mins MFMA, heavier dequantization): four token wavefronts share each
         // dequantized stage (measured 8-11 % faster on the 4096 x 14336 down projection)
-        case kQ6_K: return gemm_launch<kQ6_K, 4, 1, true>(G, n_outs, A, n_in, n_tok, s);
+        case kQ6_K: return gemm_launch<kQ6_K, 4, 1>(G, n_outs, A, n_in, n_tok, s);
         default: return hipErrorInvalidValue;
     }
 }
