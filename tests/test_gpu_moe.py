@@ -128,7 +128,7 @@ def check_stages(torch_dev, oracle, x, logits, parts, out, n_ff, k, types, packe
     assert np.array_equal(out, want)
 
 
-def run_case(torch_dev, oracle, n_tok, n_embd, n_ff, n_expert, k, types, seed, distinct=None):
+def run_case(torch_dev, oracle, n_tok, n_embd, n_ff, n_expert, k, types, seed, distinct=None, favour=None):
     torch, d = torch_dev
     tg, tu, td = types
     pg, wg = repacked_experts(torch_dev, oracle, tg, n_expert, n_ff, n_embd, seed, distinct)
@@ -136,6 +136,8 @@ def run_case(torch_dev, oracle, n_tok, n_embd, n_ff, n_expert, k, types, seed, d
     pd, wd = repacked_experts(torch_dev, oracle, td, n_expert, n_embd, n_ff, seed + 200, distinct)
     x = normal(seed + 300, (n_tok, n_embd))
     logits = normal(seed + 301, (n_tok, n_expert))
+    if favour is not None:
+        logits[:, favour] += np.float32(8.0)  # every token picks this expert (skewed counts)
     ws = torch.empty(fh.moe_workspace_bytes(n_tok, n_embd, n_ff, n_expert, k), dtype=torch.uint8, device=d)
     out = fh.moe_ffn(dev(torch_dev, x), dev(torch_dev, logits), n_ff, n_expert, k, True, tg, wg, tu, wu, td, wd,
                      workspace=ws).cpu().numpy()
@@ -175,6 +177,14 @@ def test_moe_decode_hidden_sizes(torch_dev, oracle, n_embd, n_ff, k, types):
     """One token: hidden rows quantized by the down workgroups themselves
     (k * n_ff <= 8192) or once by the quantize kernel (larger)."""
     run_case(torch_dev, oracle, 1, n_embd, n_ff, 8, k, types, 6000 + n_ff + k)
+
+
+@pytest.mark.parametrize("n_tok,n_expert,k,favour", [(100, 8, 2, 0), (96, 32, 8, 5), (40, 8, 2, 7)])
+def test_moe_skewed_routing(torch_dev, oracle, n_tok, n_expert, k, favour):
+    """One expert chosen by every token: its slots span several work-list items
+    (more than one 32-token item), the other experts get few or none."""
+    run_case(torch_dev, oracle, n_tok, 512, 512, n_expert, k, (fh.Q4_K, fh.Q4_K, fh.Q6_K), 7000 + n_tok,
+             favour=favour)
 
 
 def test_moe_mixed_types(torch_dev, oracle):
