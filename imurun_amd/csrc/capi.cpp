@@ -75,7 +75,8 @@ MoeWork moe_work(int n_tok, int n_embd, int n_ff, int n_expert, int k) {
     w.slots = n_tok * k;
     // Work-list items: one token per item at decode sizes (every expert
     // streams its rows once anyway), else 16- or 32-token MFMA items sized to
-    // the mean tokens per expert.
+    // the mean tokens per expert (each extra item of an expert re-reads its
+    // weights: at 16 tokens per expert 32-token items measure faster).
     const int avg = (w.slots + n_expert - 1) / n_expert;
     w.mfma = avg > 1 && n_embd % 256 == 0 && n_ff % 256 == 0;
     if (w.mfma) w.item_tokens = avg <= 12 ? 16 : kBatchItemTokens;

@@ -98,7 +98,7 @@ bool gemv_x_supported(const WeightLayout& L);
 hipError_t launch_gemv_x(int n, const void* const* ws, const WeightLayout* WLs, const float* x, float* const* ys,
                          hipStream_t stream);
 
-// Few-token matmul on int8 MFMA (16x16x32 tiles), same token mapping as
+// Few-token matmul on int8 MFMA (16x16 tiles), same token mapping as
 // launch_gemv; work-list items of up to kBatchItemTokens tokens. Needs
 // n_in % 256 == 0.
 constexpr int kBatchItemTokens = 32;
