@@ -210,6 +210,7 @@ def run_moe(args, torch, fh, dev, name, NE, K, E, F_, types, cases):
     wu = fh.repack(tu, torch.from_numpy(pu).to(dev).repeat(NE), E, NE * F_)
     wd = fh.repack(td, torch.from_numpy(pd).to(dev).repeat(NE), F_, NE * E)
     per_expert = pg.size + pu.size + pd.size
+    wr = torch.from_numpy(normal(136, (NE, E), 0.05)).to(dev)
     out = {"workload": f"{name} expert layer: {NE} experts, top-{K}, hidden {E}, expert FFN {F_}",
            "weights_per_expert_bytes": per_expert}
     for M in cases:
@@ -234,8 +235,13 @@ def run_moe(args, torch, fh, dev, name, NE, K, E, F_, types, cases):
         us = graph_time_seq(torch, fns, max(20, 80 // len(fns)))
         b = active * per_expert + M * E * 8
         ops = 2 * M * K * 3 * E * F_
+        # the router matmul before it (model.cpp:1529), f32 router rows [NE][E], timed on its own
+        lg_out = torch.empty((M, NE), dtype=torch.float32, device=dev)
+        # (16 calls per graph: one short kernel per replay would time the replay, not the kernel)
+        router_us = graph_time_seq(torch, [lambda: fh.router_logits(x, wr, out=lg_out)] * 16, 20)
         out[f"M{M}"] = {"us": round(us, 2), "active_experts": active, "bytes": b, "gbs": round(b / us / 1e3, 1),
-                        "pct_hbm": round(100 * b / us / 1e3 / HBM_PEAK_GBS, 2), "tops": round(ops / us / 1e6, 2)}
+                        "pct_hbm": round(100 * b / us / 1e3 / HBM_PEAK_GBS, 2), "tops": round(ops / us / 1e6, 2),
+                        "router_f32_us": round(router_us, 2)}
     return out
 
 

@@ -69,6 +69,8 @@ def load() -> ctypes.CDLL:
                               ctypes.c_uint64, _P, _P], ctypes.c_int),
         "fish_hip_moe_route": ([_P, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, _P, ctypes.c_uint64, _P,
                                 _P, _P], ctypes.c_int),
+        "fish_hip_router_logits": ([_P, ctypes.c_int, ctypes.c_int, ctypes.c_uint32, _P, ctypes.c_int, _P, _P],
+                                   ctypes.c_int),
         "fish_hip_silu_mul_quantize": ([_P, _P, ctypes.c_int, ctypes.c_int, _P, _P, _P, _P], ctypes.c_int),
         "fish_hip_backend_available": ([], ctypes.c_int),
         "fish_hip_device_name": ([], ctypes.c_char_p),
@@ -296,6 +298,25 @@ def moe_route(logits, k: int, norm: bool = True, stream=None):
     _check(load().fish_hip_moe_route(logits.data_ptr(), n_tok, n_expert, k, int(norm), ws.data_ptr(), ws.numel(),
                                      sel.data_ptr(), wsel.data_ptr(), _stream(stream)), "moe_route")
     return sel, wsel
+
+
+def router_logits(x, w, out=None, stream=None):
+    """logits [n_tok][n_expert] = x @ w.T in f32 for f32 or f16 router rows w
+    [n_expert][n_embd] (model.cpp:1529); written into `out` when given."""
+    import torch
+    if w.dtype not in (torch.float32, torch.float16):
+        raise ValueError("router_logits: weights must be float32 or float16")
+    n_tok, n_embd = x.shape
+    n_expert = w.shape[0]
+    if w.shape[1] != n_embd or x.dtype != torch.float32 or not x.is_contiguous() or not w.is_contiguous():
+        raise ValueError("router_logits: x f32 [n_tok][n_embd], w [n_expert][n_embd], both contiguous")
+    logits = torch.empty((n_tok, n_expert), dtype=torch.float32, device=x.device) if out is None else out
+    if logits.shape != (n_tok, n_expert) or logits.dtype != torch.float32 or not logits.is_contiguous():
+        raise ValueError("router_logits: out must be contiguous f32 [n_tok][n_expert]")
+    t = 0 if w.dtype == torch.float32 else 1
+    _check(load().fish_hip_router_logits(x.data_ptr(), n_tok, n_embd, t, w.data_ptr(), n_expert, logits.data_ptr(),
+                                         _stream(stream)), "router_logits")
+    return logits
 
 
 def silu_mul_quantize(g, u, stream=None):

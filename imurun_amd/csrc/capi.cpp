@@ -494,6 +494,22 @@ int fish_hip_moe_route(const float* logits, int n_tok, int n_expert, int k, int 
     return e == hipSuccess ? 0 : hip_fail(e, "moe_route");
 }
 
+int fish_hip_router_logits(const float* x, int n_tok, int n_embd, uint32_t t_router, const void* w_router,
+                           int n_expert, float* logits, void* stream) {
+    if (!x || !w_router || !logits || n_tok <= 0 || n_embd <= 0 || n_expert <= 0)
+        return fail(FISH_HIP_ERR_ARG, "router_logits: bad arguments");
+    if (t_router != kF32 && t_router != kF16) return fail(FISH_HIP_ERR_ARG, "router_logits: weights not f32 or f16");
+    if (n_embd % 4) return fail(FISH_HIP_ERR_ARG, "router_logits: n_embd not a multiple of 4");
+    if (n_embd > (1 << 30) || int64_t(n_tok) * n_expert > (int64_t(1) << 30))
+        return fail(FISH_HIP_ERR_ARG, "router_logits: too large");
+    const uintptr_t walign = t_router == kF32 ? 16 : 8;
+    if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(w_router) % walign ||
+        reinterpret_cast<uintptr_t>(logits) % 4)
+        return fail(FISH_HIP_ERR_ARG, "router_logits: misaligned pointer");
+    const hipError_t e = launch_router(x, n_tok, n_embd, t_router, w_router, n_expert, logits, as_stream(stream));
+    return e == hipSuccess ? 0 : hip_fail(e, "router_logits");
+}
+
 int fish_hip_silu_mul_quantize(const float* g, const float* u, int n_rows, int n_ff, void* act, void* q256_fish,
                                float* h, void* stream) {
     if (!g || !u || !act || n_rows <= 0 || n_ff <= 0 || n_ff % 32)

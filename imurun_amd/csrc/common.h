@@ -42,7 +42,7 @@
 
 namespace fishhip {
 
-enum : uint32_t { kQ4_0 = 2, kQ8_0 = 8, kQ4_K = 12, kQ6_K = 14 };
+enum : uint32_t { kF32 = 0, kF16 = 1, kQ4_0 = 2, kQ8_0 = 8, kQ4_K = 12, kQ6_K = 14 };
 
 inline size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 

@@ -50,6 +50,12 @@ struct MoeRouting {
 hipError_t launch_moe_route(const float* logits, int n_tok, int n_expert, int k, int norm, int item_tokens,
                             const MoeRouting& r, hipStream_t stream);
 
+// logits[t][e] = dot(x[t], w[e]) in f32 over f32 (type 0) or f16 (type 1)
+// router rows (model.cpp:1529); n_embd % 4 == 0, x 16-byte and w 16-byte
+// (f32) or 8-byte (f16) aligned.
+hipError_t launch_router(const float* x, int n_tok, int n_embd, uint32_t type, const void* w, int n_expert,
+                         float* logits, hipStream_t stream);
+
 // The expert FFN of one token: gate+up (routing and x quantization
 // in-kernel; writes the routing, gate, up and h = silu(gate)*up rows), then
 // down+combine (h quantized in-kernel for small experts, else by one quantize

@@ -434,6 +434,110 @@ __global__ __launch_bounds__(64 * kMoe1DownWaves) void moe1_down_kernel(const fl
     }
 }
 
+// Router logits (model.cpp:1529: matmul_batch over the f32 or f16 gate_inp
+// tensor, n_expert rows of n_embd): logits[t][e] = sum_k x[t][k] * w[e][k] in
+// f32. One wavefront covers TT tokens x TE experts; lane l owns k = 4l + 256j,
+// fuses its products in k order into one f32 accumulator per (token, expert),
+// then the 64 lanes are added by a xor butterfly. Every (t, e) therefore sums
+// in the same order whatever the tile shape, so a token's logits do not
+// depend on how many tokens share the launch. FISH's AVX2 f32 dot keeps 8 lane
+// partials: the two agree to f32 rounding, not bit for bit.
+template <bool F16>
+__device__ __forceinline__ float4 router_w4(const void* w, size_t off) {
+    if constexpr (F16) {
+        const uint2 h = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(w) + off);
+        return make_float4(f16_bits_to_f32(uint16_t(h.x & 0xFFFF)), f16_bits_to_f32(uint16_t(h.x >> 16)),
+                           f16_bits_to_f32(uint16_t(h.y & 0xFFFF)), f16_bits_to_f32(uint16_t(h.y >> 16)));
+    } else {
+        return *reinterpret_cast<const float4*>(static_cast<const float*>(w) + off);
+    }
+}
+
+template <bool F16, int TT, int TE, int U>
+__device__ __forceinline__ void router_steps(const float* __restrict__ x, const void* __restrict__ w,
+                                             const size_t (&xo)[TT], const size_t (&wo)[TE], int k,
+                                             float (&acc)[TT][TE]) {
+    float4 xv[U][TT], wv[U][TE];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+#pragma unroll
+        for (int i = 0; i < TT; ++i) xv[u][i] = *reinterpret_cast<const float4*>(x + xo[i] + k + 256 * u);
+#pragma unroll
+        for (int j = 0; j < TE; ++j) wv[u][j] = router_w4<F16>(w, wo[j] + k + 256 * u);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int i = 0; i < TT; ++i)
+#pragma unroll
+            for (int j = 0; j < TE; ++j) {
+                float a = acc[i][j];
+                a = fmaf(xv[u][i].x, wv[u][j].x, a);
+                a = fmaf(xv[u][i].y, wv[u][j].y, a);
+                a = fmaf(xv[u][i].z, wv[u][j].z, a);
+                acc[i][j] = fmaf(xv[u][i].w, wv[u][j].w, a);
+            }
+}
+
+template <bool F16, int TT, int TE>
+__global__ __launch_bounds__(256) void router_kernel(const float* __restrict__ x, const void* __restrict__ w,
+                                                     int n_tok, int n_embd, int n_expert, float* __restrict__ logits) {
+    // loads of U steps are issued together before their products (same sums, more loads in flight)
+    constexpr int U = TT * TE == 1 ? 4 : 2;
+    const int tiles_e = (n_expert + TE - 1) / TE;
+    const int wave = __builtin_amdgcn_readfirstlane(int(blockIdx.x) * 4 + int(threadIdx.x >> 6));
+    const int lane = threadIdx.x & 63;
+    if (wave >= (n_tok + TT - 1) / TT * tiles_e) return;  // uniform over the wavefront
+    const int t0 = wave / tiles_e * TT, e0 = wave % tiles_e * TE;
+    // rows past the end repeat the last one (loaded, never stored)
+    size_t xo[TT], wo[TE];
+#pragma unroll
+    for (int i = 0; i < TT; ++i) xo[i] = size_t(min(t0 + i, n_tok - 1)) * n_embd;
+#pragma unroll
+    for (int j = 0; j < TE; ++j) wo[j] = size_t(min(e0 + j, n_expert - 1)) * n_embd;
+    float acc[TT][TE];
+#pragma unroll
+    for (int i = 0; i < TT; ++i)
+#pragma unroll
+        for (int j = 0; j < TE; ++j) acc[i][j] = 0.0f;
+    int k = 4 * lane;
+    if constexpr (U > 1)
+        for (; k + 256 * (U - 1) < n_embd; k += 256 * U) router_steps<F16, TT, TE, U>(x, w, xo, wo, k, acc);
+    for (; k < n_embd; k += 256) router_steps<F16, TT, TE, 1>(x, w, xo, wo, k, acc);
+    float mine = 0.0f;
+#pragma unroll
+    for (int i = 0; i < TT; ++i)
+#pragma unroll
+        for (int j = 0; j < TE; ++j) {
+            float a = acc[i][j];
+            for (int off = 32; off > 0; off >>= 1) a += __shfl_xor(a, off);
+            if (lane == i * TE + j) mine = a;
+        }
+    const int i = lane / TE, j = lane % TE;
+    if (lane < TT * TE && t0 + i < n_tok && e0 + j < n_expert) logits[size_t(t0 + i) * n_expert + e0 + j] = mine;
+}
+
+template <bool F16, int TT, int TE>
+void router_launch(const float* x, const void* w, int n_tok, int n_embd, int n_expert, float* logits,
+                   hipStream_t stream) {
+    const int waves = (n_tok + TT - 1) / TT * ((n_expert + TE - 1) / TE);
+    hipLaunchKernelGGL((router_kernel<F16, TT, TE>), dim3(unsigned((waves + 3) / 4)), dim3(256), 0, stream, x, w,
+                       n_tok, n_embd, n_expert, logits);
+}
+
+// The largest tile that still gives at least one wavefront per SIMD (1024);
+// few-token calls keep one (token, expert) per wavefront. Measured with f32
+// rows: 256 tokens x 128 experts x 2048 take 9.4 us as 2x4 tiles, 10.0 as
+// 4x8 and 17.5 as 1x1; 1024 tokens take 20.4 us as 8x8, 30.1 as 2x4.
+template <bool F16>
+void router_pick(const float* x, const void* w, int n_tok, int n_embd, int n_expert, float* logits,
+                 hipStream_t stream) {
+    auto waves = [&](int tt, int te) { return long((n_tok + tt - 1) / tt) * ((n_expert + te - 1) / te); };
+    if (waves(8, 8) >= 1024) router_launch<F16, 8, 8>(x, w, n_tok, n_embd, n_expert, logits, stream);
+    else if (waves(2, 4) >= 1024) router_launch<F16, 2, 4>(x, w, n_tok, n_embd, n_expert, logits, stream);
+    else router_launch<F16, 1, 1>(x, w, n_tok, n_embd, n_expert, logits, stream);
+}
+
 }  // namespace
 
 hipError_t launch_moe_route(const float* logits, int n_tok, int n_expert, int k, int norm, int item_tokens,
@@ -446,6 +550,17 @@ hipError_t launch_moe_route(const float* logits, int n_tok, int n_expert, int k,
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(group_kernel, dim3(1), dim3(256), 0, stream, n_tok, n_expert, k, item_tokens, r);
+    return hipGetLastError();
+}
+
+hipError_t launch_router(const float* x, int n_tok, int n_embd, uint32_t type, const void* w, int n_expert,
+                         float* logits, hipStream_t stream) {
+    // sizes that keep k + 1024 and the wavefront count inside an int
+    if (n_tok <= 0 || n_embd <= 0 || n_embd % 4 || n_embd > (1 << 30) || n_expert <= 0 ||
+        long(n_tok) * n_expert > (1L << 30) || (type != kF32 && type != kF16))
+        return hipErrorInvalidValue;
+    if (type == kF16) router_pick<true>(x, w, n_tok, n_embd, n_expert, logits, stream);
+    else router_pick<false>(x, w, n_tok, n_embd, n_expert, logits, stream);
     return hipGetLastError();
 }
 

@@ -155,6 +155,17 @@ FISH_HIP_API int fish_hip_moe_workspace_layout(int n_tok, int n_embd, int n_ff, 
 FISH_HIP_API int fish_hip_moe_route(const float* logits, int n_tok, int n_expert, int k, int norm, void* workspace,
                                     uint64_t workspace_bytes, int* sel, float* wsel, void* stream);
 
+/* Router logits for unquantized router weights: logits[t][e] = sum_k
+ * x[t][k] * w[e][k] in f32, with w n_expert rows of n_embd f32 (t_router 0)
+ * or f16 (t_router 1). Replaces matmul_batch(L.gate_inp->type, ...)
+ * (model.cpp:1529) on its f32 dot path (ops.cpp:220-250: dequant_row +
+ * dot_f32_fast); a quantized gate_inp goes through fish_hip_matmul instead.
+ * Sums are in a different order than FISH's 8-lane AVX2 dot, so results agree
+ * to f32 rounding. n_embd % 4 == 0; x 16-byte aligned, w 16-byte (f32) or
+ * 8-byte (f16) aligned. Returns 0 or FISH_HIP_ERR_ARG. */
+FISH_HIP_API int fish_hip_router_logits(const float* x, int n_tok, int n_embd, uint32_t t_router,
+                                        const void* w_router, int n_expert, float* logits, void* stream);
+
 /* silu(g) * u (silu_inplace, ops.cpp:25-30; model.cpp:1504-1508) quantized
  * like ActBatch::quantize into act (fish_hip_act_bytes(n_rows, n_ff));
  * q256_fish and h (f32 [n_rows][n_ff]) are optional copies of FISH's Q8ActK

@@ -20,6 +20,9 @@
  *   or_vec_dot_q8 / or_matmul_batch  golden per-row dots and matmul outputs.
  *   or_moe_ffn            golden output of a tiny MoE layer composed from the
  *       reference's own primitives in the order of model.cpp:1523-1580.
+ *   or_router_logits      golden matmul_batch outputs on f32 / f16 router
+ *       rows (to f32 rounding: the reference's installed dot sums in another
+ *       order) and a float64 dot of the same operands.
  * Nothing here is "parity unpinned".
  */
 #define _GNU_SOURCE
@@ -407,6 +410,60 @@ int or_matmul_batch(uint32_t type, const void* w, const void* acts32, const void
     for (int k = 1; k < n_threads; ++k) pthread_create(&th[k], NULL, mm_worker, &jobs[k]);
     mm_worker(&jobs[0]);
     for (int k = 1; k < n_threads; ++k) pthread_join(th[k], NULL);
+    return 1;
+}
+
+/* ------------------------------------------------------------------ router (f32 / f16 weights)
+ * matmul_batch on a weight type without an int8 kernel (ops.cpp:219-250),
+ * as the router of model.cpp:1529 runs it for f32 / f16 gate_inp tensors:
+ *   n_tok == 1: vec_dot (quant.cpp:530-546): f32 rows dot the whole row; f16
+ *       rows are widened 64 values at a time and each chunk's dot is added
+ *       to a running f32 sum;
+ *   n_tok > 1: the row is widened once and dotted with every token.
+ * Every dot is FISH's scalar dot_f32 (quant.cpp:67-78): four interleaved f32
+ * partial sums, a scalar tail into the first, then (s0 + s1) + (s2 + s3). The
+ * reference installs an AVX2 dot in its place on x86, which sums in another
+ * order, so this agrees with it to f32 rounding only. */
+#define OR_F32 0u
+#define OR_F16 1u
+
+static float dot_f32_scalar(const float* a, const float* b, int n) {
+    float s0 = 0, s1 = 0, s2 = 0, s3 = 0;
+    int i = 0;
+    for (; i + 4 <= n; i += 4) {
+        s0 += a[i] * b[i];
+        s1 += a[i + 1] * b[i + 1];
+        s2 += a[i + 2] * b[i + 2];
+        s3 += a[i + 3] * b[i + 3];
+    }
+    for (; i < n; ++i) s0 += a[i] * b[i];
+    return (s0 + s1) + (s2 + s3);
+}
+
+/* logits [n_tok][n_expert]; w holds n_expert rows of n_embd f32 or f16 bits. */
+int or_router_logits(uint32_t type, const void* w, const float* x, int n_tok, int n_embd, int n_expert,
+                     float* logits) {
+    if ((type != OR_F32 && type != OR_F16) || n_tok < 1 || n_embd < 1 || n_expert < 1) return 0;
+    float* row = (float*)malloc(sizeof(float) * (size_t)n_embd);
+    if (!row) return 0;
+    for (int e = 0; e < n_expert; ++e) {
+        const size_t off = (size_t)e * n_embd;
+        if (type == OR_F32) memcpy(row, (const float*)w + off, sizeof(float) * (size_t)n_embd);
+        else
+            for (int k = 0; k < n_embd; ++k) row[k] = or_fp16_to_fp32(((const uint16_t*)w)[off + k]);
+        for (int t = 0; t < n_tok; ++t) {
+            const float* xt = x + (size_t)t * n_embd;
+            float v;
+            if (n_tok == 1 && type == OR_F16) {
+                v = 0.0f;
+                for (int i = 0; i < n_embd; i += 64) v += dot_f32_scalar(row + i, xt + i, n_embd - i < 64 ? n_embd - i : 64);
+            } else {
+                v = dot_f32_scalar(row, xt, n_embd);
+            }
+            logits[(size_t)t * n_expert + e] = v;
+        }
+    }
+    free(row);
     return 1;
 }
 

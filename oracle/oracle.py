@@ -76,6 +76,7 @@ class Oracle:
         L.or_moe_ffn.argtypes = [_P, _P, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                  ctypes.c_int, ctypes.c_uint32, _P, ctypes.c_uint32, _P, ctypes.c_uint32, _P, _P,
                                  ctypes.c_int]
+        L.or_router_logits.argtypes = [ctypes.c_uint32, _P, _P, ctypes.c_int, ctypes.c_int, ctypes.c_int, _P]
         self.threads = min(16, os.cpu_count() or 1)
 
     # activations -----------------------------------------------------------
@@ -148,6 +149,17 @@ class Oracle:
         wsel = np.zeros((n_tok, k), np.float32)
         self.L.or_route(_ptr(logits), n_tok, ne, k, int(norm), _ptr(sel), _ptr(wsel))
         return sel, wsel
+
+    def router_logits(self, t: int, w: np.ndarray, x: np.ndarray) -> np.ndarray:
+        """matmul_batch on f32 (t=0) or f16 (t=1, w as uint16 bits) router rows
+        w [n_expert][n_embd] (ops.cpp:219-250)."""
+        x = np.ascontiguousarray(x, np.float32)
+        w = np.ascontiguousarray(w, np.float32 if t == 0 else np.uint16)
+        n_tok, n_embd = x.shape
+        out = np.zeros((n_tok, w.shape[0]), np.float32)
+        if not self.L.or_router_logits(t, _ptr(w), _ptr(x), n_tok, n_embd, w.shape[0], _ptr(out)):
+            raise ValueError("bad router arguments")
+        return out
 
     def silu(self, v: float) -> float:
         return self.L.or_silu(v)

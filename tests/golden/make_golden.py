@@ -16,6 +16,8 @@ Fixtures (numpy .npz, no pickles):
               (test/test_kernels.cpp:89-107).
   matmul.npz  ActBatch::quantize + matmul_batch outputs, N=32,
               K in {512, 768}, M in {1, 3, 17}.
+  router.npz  matmul_batch on f32 / f16 router rows (NE=8, K in {256, 992},
+              M in {1, 5}).
   moe.npz     a tiny expert layer (NE=4, top-2, E=256, F=256, M=6,
               gate/up Q4_K, down Q6_K) composed in model.cpp's order.
 """
@@ -141,6 +143,20 @@ def main() -> None:
     out, sel, wsel = ref.moe_ffn(x, logits, E, F, NE, K, True, Q4_K, pg, Q4_K, pu, Q6_K, pd)
     np.savez_compressed(os.path.join(HERE, "moe.npz"), E=E, F=F, NE=NE, K=K, x=x, logits=logits, gate=pg, up=pu,
                         down=pd, out=out, sel=sel, wsel=wsel)
+    # router logits on unquantized gate_inp rows (model.cpp:1529): f32 (type 0)
+    # and f16 (type 1, stored as uint16 bits), one token (vec_dot) and five
+    # (dequant_row + dot_f32_fast); 992 leaves a 32-value f16 tail chunk.
+    d = {}
+    for n in (256, 992):
+        w = normal(9100 + n, (8, n), 0.05)
+        d[f"w0_{n}"] = w
+        d[f"w1_{n}"] = w.astype(np.float16).view(np.uint16)
+        for m in (1, 5):
+            x = normal(9200 + n + m, (m, n), 1.0)
+            d[f"x_{n}_{m}"] = x
+            for t in (0, 1):
+                d[f"y{t}_{n}_{m}"] = ref.matmul_f32(t, d[f"w{t}_{n}"], x, 8)
+    np.savez_compressed(os.path.join(HERE, "router.npz"), **d)
     for f in sorted(os.listdir(HERE)):
         if f.endswith(".npz"):
             print(f, os.path.getsize(os.path.join(HERE, f)))

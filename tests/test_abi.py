@@ -72,6 +72,17 @@ def test_bad_arguments_return_errors_without_device_work():
     assert L.fish_hip_moe_ffn(fake, fake, n_tok, E, F, NE, K, 1, fh.Q4_K, fake, fh.Q4_K, fake, fh.Q4_K, fake,
                               fake, nb - 1, fake, None) == -1
     assert "too small" in fh.last_error()
+    # router_logits: weight type, row length and alignment are checked before any device work
+    assert L.fish_hip_router_logits(fake, 4, 4096, fh.Q8_0, fake, 8, fake, None) == -1
+    assert "f32 or f16" in fh.last_error()
+    assert L.fish_hip_router_logits(fake, 4, 4094, 0, fake, 8, fake, None) == -1
+    assert "multiple of 4" in fh.last_error()
+    assert L.fish_hip_router_logits(fake + 8, 4, 4096, 0, fake, 8, fake, None) == -1
+    assert "misaligned" in fh.last_error()
+    assert L.fish_hip_router_logits(fake, 4, 4096, 0, fake + 8, 8, fake, None) == -1
+    assert "misaligned" in fh.last_error()
+    assert L.fish_hip_router_logits(fake, 0, 4096, 1, fake, 8, fake, None) == -1
+    assert "bad arguments" in fh.last_error()
 
 
 @pytest.mark.parametrize("t", [fh.Q8_0, fh.Q4_0, fh.Q4_K, fh.Q6_K])

@@ -57,6 +57,57 @@ def test_routing_matches_oracle(torch_dev, oracle, n_tok, n_expert, k):
     assert np.allclose(wsel2.cpu().numpy(), want_w2, rtol=0, atol=1e-6)
 
 
+def _router_check(torch_dev, oracle, t, w, x):
+    """GPU router logits against the oracle, per element within 1e-6 * sum|x w|
+    (both sum in f32, in different orders), then the same top-k selection."""
+    torch, _ = torch_dev
+    wt = dev(torch_dev, w) if t == 0 else dev(torch_dev, w).view(torch.float16)
+    got = fh.router_logits(dev(torch_dev, x), wt).cpu().numpy()
+    want = oracle.router_logits(t, w, x)
+    wf = w if t == 0 else w.view(np.float16)
+    bound = np.abs(x.astype(np.float64)) @ np.abs(wf.astype(np.float64)).T
+    err = np.abs(got.astype(np.float64) - want)
+    assert np.all(err <= 1e-6 * bound), f"max err / bound {float(np.max(err / bound)):.3e}"
+    return got, want
+
+
+# tile shapes: one (token, expert) per wavefront below 1024 wavefronts' worth, then 2x4, then 8x8
+# (100x128, 257x60 and 256x128 take 2x4; 1030x61 and 1100x67 take 8x8, ragged on both axes)
+@pytest.mark.parametrize("t", [0, 1])
+@pytest.mark.parametrize("n_tok,n_embd,n_expert", [(1, 4096, 8), (64, 4096, 8), (1, 2048, 128), (256, 2048, 128),
+                                                   (5, 992, 8), (3, 260, 60), (33, 4, 3), (100, 1024, 128),
+                                                   (257, 264, 60), (1030, 256, 61), (1100, 96, 67)])
+def test_router_logits_match_oracle(torch_dev, oracle, t, n_tok, n_embd, n_expert):
+    x = normal(50 + n_tok + n_embd, (n_tok, n_embd), 1.0)
+    w = normal(60 + n_expert + n_embd, (n_expert, n_embd), 0.05)
+    if t == 1:
+        w = w.astype(np.float16).view(np.uint16)
+    got, _ = _router_check(torch_dev, oracle, t, w, x)
+    # every tile shape sums each (token, expert) in the same order: a token's logits are the
+    # same bits whether it is routed alone or with the others
+    torch, _ = torch_dev
+    wt = dev(torch_dev, w) if t == 0 else dev(torch_dev, w).view(torch.float16)
+    for r in sorted({0, n_tok // 2, n_tok - 1}):
+        alone = fh.router_logits(dev(torch_dev, x[r:r + 1]), wt).cpu().numpy()
+        assert np.array_equal(alone[0], got[r]), f"token {r}"
+    # the device logits drive the device routing exactly as the oracle's routing
+    k = min(2 if n_expert <= 8 else 8, n_expert)
+    sel, _ = fh.moe_route(dev(torch_dev, got), k, True)
+    assert np.array_equal(sel.cpu().numpy(), oracle.route(got, k, True)[0])
+
+
+def test_router_logits_golden(torch_dev, oracle, golden):
+    g = golden("router")
+    for n in (256, 992):
+        for t in (0, 1):
+            for m in (1, 5):
+                x = g[f"x_{n}_{m}"]
+                got, _ = _router_check(torch_dev, oracle, t, g[f"w{t}_{n}"], x)
+                wf = g[f"w{t}_{n}"] if t == 0 else g[f"w{t}_{n}"].view(np.float16)
+                bound = np.abs(x.astype(np.float64)) @ np.abs(wf.astype(np.float64)).T
+                assert np.all(np.abs(got - g[f"y{t}_{n}_{m}"]) <= 1e-6 * bound)
+
+
 @pytest.mark.parametrize("n_rows,n_ff", [(20, 768), (3, 14336), (64, 256)])
 def test_silu_mul_quantize_bit_exact_on_own_values(torch_dev, oracle, n_rows, n_ff):
     g = normal(51 + n_ff, (n_rows, n_ff)) * np.float32(2.0)

@@ -147,3 +147,43 @@ def test_moe_golden(oracle, golden):
     out = oracle.moe_ffn(g["x"], g["logits"], E, F_, NE, K, True, Q4_K, g["gate"], Q4_K, g["up"], Q6_K, g["down"])
     want = g["out"]
     assert np.max(np.abs(out - want)) <= 1e-5 * np.max(np.abs(want))
+
+
+def _abs_bound(x, w):
+    """sum_k |x_k w_k| per (token, row): the scale of f32 rounding in a dot."""
+    return np.abs(x.astype(np.float64)) @ np.abs(w.astype(np.float64)).T
+
+
+@pytest.mark.parametrize("n", [256, 992])
+def test_router_golden_and_float64(oracle, golden, n):
+    g = golden("router")
+    for t in (0, 1):
+        w = g[f"w{t}_{n}"]
+        wf = w if t == 0 else w.view(np.float16)
+        for m in (1, 5):
+            x = g[f"x_{n}_{m}"]
+            want = g[f"y{t}_{n}_{m}"]
+            got = oracle.router_logits(t, w, x)
+            bound = _abs_bound(x, wf)
+            if t == 1 and m == 1:
+                # vec_dot's f16 branch uses the scalar four-sum dot on 64-value chunks
+                # (quant.cpp:537-546), the same order as the oracle: bit-identical.
+                assert np.array_equal(got, want)
+            assert np.all(np.abs(got - want) <= 1e-6 * bound)
+            exact = x.astype(np.float64) @ wf.astype(np.float64).T
+            assert np.all(np.abs(got - exact) <= 1e-6 * bound)
+
+
+def test_router_catches_a_dropped_term(oracle):
+    # a dot that misses one product, or uses the transposed operand, is far outside the tolerance above
+    n = 992
+    x = normal(31, (3, n), 1.0)
+    w = normal(32, (8, n), 0.05)
+    got = oracle.router_logits(0, w, x)
+    bound = _abs_bound(x, w)
+    x2 = x.copy()
+    x2[:, 17] = 0.0
+    dropped = x2.astype(np.float64) @ w.astype(np.float64).T
+    assert np.any(np.abs(got - dropped) > 1e-6 * bound)
+    shifted = x.astype(np.float64) @ np.roll(w, 1, axis=0).astype(np.float64).T
+    assert np.all(np.abs(got - shifted) > 1e-6 * bound)
