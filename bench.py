@@ -200,6 +200,35 @@ def run_q8_gemv(args, torch, fh, dev):
             "gbs": round(b / us / 1e3, 1), "pct_hbm": round(100 * b / us / 1e3 / HBM_PEAK_GBS, 2)}
 
 
+def run_kquant_gemv(args, torch, fh, dev, t, name):
+    """Llama-3-8B FFN decode (M = 1) on K-quant weights: the fused gate+up GEMV
+    (2 x 14336x4096) and the down GEMV (4096x14336), x / h quantized in-kernel,
+    rotating copies past the MALL; each kernel graph-timed on its own."""
+    from imurun_amd.synth import normal
+    wg = fh.quantize_rows(t, normal(141, (F, E), 0.02))
+    wu = fh.quantize_rows(t, normal(142, (F, E), 0.02))
+    wd = fh.quantize_rows(t, normal(143, (E, F), 0.02))
+    copies = max(2, int(2 * MALL_BYTES // (wg.size + wu.size + wd.size)) + 2)
+    sets = [tuple(fh.repack(t, torch.from_numpy(a).to(dev), n_in, n_out)
+                  for a, n_in, n_out in ((wg, E, F), (wu, E, F), (wd, F, E))) for _ in range(copies)]
+    x = torch.from_numpy(normal(144, (1, E))).to(dev)
+    h = torch.from_numpy(normal(145, (1, F))).to(dev)
+    yg, yu = (torch.empty((1, F), dtype=torch.float32, device=dev) for _ in range(2))
+    yd = torch.empty((1, E), dtype=torch.float32, device=dev)
+    gu = [lambda s_=s_: fh.matmul_tensors(t, [s_[0], s_[1]], x, [F, F], ys=[yg, yu]) for s_ in sets]
+    dn = [lambda s_=s_: fh.matmul_tensors(t, [s_[2]], h, [E], ys=[yd]) for s_ in sets]
+    gu_us = graph_time_seq(torch, gu, max(20, args.steps // 4))
+    dn_us = graph_time_seq(torch, dn, max(20, args.steps // 4))
+    b_gu = wg.size + wu.size + E * 4 + 2 * F * 4
+    b_dn = wd.size + F * 4 + E * 4
+    return {"workload": f"Llama-3-8B FFN decode, {name}, M=1: gate+up 2x14336x4096 fused, down 4096x14336; "
+                        "f32 x / h quantized in-kernel",
+            "gate_up_us": round(gu_us, 3), "gate_up_gbs": round(b_gu / gu_us / 1e3, 1),
+            "gate_up_pct_hbm": round(100 * b_gu / gu_us / 1e3 / HBM_PEAK_GBS, 2),
+            "down_us": round(dn_us, 3), "down_gbs": round(b_dn / dn_us / 1e3, 1),
+            "down_pct_hbm": round(100 * b_dn / dn_us / 1e3 / HBM_PEAK_GBS, 2)}
+
+
 def run_moe(args, torch, fh, dev, name, NE, K, E, F_, types, cases):
     """Expert FFN layer at the given token counts; one distinct expert replicated (same traffic)."""
     from imurun_amd.synth import normal
@@ -407,6 +436,8 @@ def main() -> int:
     }
     if not args.no_extras:
         out["q8_0_gemv"] = run_q8_gemv(args, torch, fh, dev)
+        out["q4_k_gemv"] = run_kquant_gemv(args, torch, fh, dev, fh.Q4_K, "Q4_K")
+        out["q6_k_gemv"] = run_kquant_gemv(args, torch, fh, dev, fh.Q6_K, "Q6_K")
         out["moe_mixtral"] = run_moe(args, torch, fh, dev, "Mixtral-8x7B", 8, 2, 4096, 14336,
                                      (fh.Q4_K, fh.Q4_K, fh.Q4_K), (1, 64))
         out["moe_qwen3"] = run_moe(args, torch, fh, dev, "Qwen3-30B-A3B", 128, 8, 2048, 768,

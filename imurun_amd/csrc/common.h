@@ -208,13 +208,10 @@ __device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
 __device__ __forceinline__ void k4_scale_min(uint32_t s03, uint32_t s47, uint32_t s811, int g, int& sc, int& mn) {
     const int h = (g & 3) * 8;
     const uint32_t a = (s03 >> h) & 0xFF, b = (s47 >> h) & 0xFF, c = (s811 >> h) & 0xFF;
-    if (g < 4) {
-        sc = int(a & 63);
-        mn = int(b & 63);
-    } else {
-        sc = int((c & 15) | ((a >> 6) << 4));
-        mn = int((c >> 4) | ((b >> 6) << 4));
-    }
+    // selects, not branches: lanes of one wavefront hold different g
+    const bool lo = g < 4;
+    sc = int(lo ? (a & 63) : ((c & 15) | ((a >> 6) << 4)));
+    mn = int(lo ? (b & 63) : ((c >> 4) | ((b >> 6) << 4)));
 }
 
 }  // namespace fishhip

@@ -72,8 +72,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(WeightPtrs W, ActPtrs A, int 
     for (int rb = 0; rb < RB; ++rb) {
         const int row = wrow0 + min(row_base + rb * RPP, n_out - 1);
 #pragma unroll
-        for (int k = 0; k < MAXC; ++k) f[rb][k] = load_group_wave<T>(W, row, cg[k], n_in, lane);
+        for (int k = 0; k < MAXC; ++k) f[rb][k] = load_group_raw<T, true>(W, row, cg[k], n_in, lane);
     }
+    __builtin_amdgcn_sched_barrier(0);
 
     float acc[RB][NT];
 #pragma unroll
@@ -85,6 +86,14 @@ __global__ __launch_bounds__(256) void gemv_kernel(WeightPtrs W, ActPtrs A, int 
         ActFrag ac[MAXC];
 #pragma unroll
         for (int k = 0; k < MAXC; ++k) ac[k] = load_act<T>(A, arow[t], cg[k], n_in);
+        if (t == 0) {
+            // the first token's activation loads are in flight: decode the weight scales
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+                for (int k = 0; k < MAXC; ++k) finish_group<T, true>(f[rb][k], cg[k], lane);
+        }
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
@@ -262,7 +271,7 @@ __global__ __launch_bounds__(64 * kGemvXWaves) void gemv_x_kernel(GemvXGroup G, 
     for (int rb = 0; rb < RB; ++rb) {
         const int row = min(row_base + rb * RPP, n_out - 1);
 #pragma unroll
-        for (int k = 0; k < MAXC; ++k) f[rb][k] = load_group_wave<T>(W, row, cg[k], n_in, lane);
+        for (int k = 0; k < MAXC; ++k) f[rb][k] = load_group_raw<T, true>(W, row, cg[k], n_in, lane);
     }
 
     // every load is issued before the quantization's first use of x
@@ -271,6 +280,10 @@ __global__ __launch_bounds__(64 * kGemvXWaves) void gemv_x_kernel(GemvXGroup G, 
     quantize_to_lds<kq, XV, 64 * kGemvXWaves>(xv, n_in, tid, L);
     __syncthreads();
     if (wave_id * (RPP * RB) >= n_out) return;  // uniform over the wavefront
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int k = 0; k < MAXC; ++k) finish_group<T, true>(f[rb][k], cg[k], lane);
 
     float acc[RB];
 #pragma unroll

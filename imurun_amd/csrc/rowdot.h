@@ -15,63 +15,75 @@ struct Frag {
     uint4 w0, w1;   // codes (Q8_0 uses both)
     uint4 meta;     // Q4_K: d, dmin, scales[12]
     uint2 qh;       // Q6_K high bits
+    uint32_t raw;   // as loaded: f16 d (Q8_0, Q4_0, Q6_K); one Q4_K meta dword (wavefront form)
+    uint32_t raw2;  // as loaded: Q6_K's two int8 16-group scales
     float d, dmin;  // f32 weight scales
     int sca, scb;   // integer group scales (Q4_K: sc, min; Q6_K: two 16-group scales)
 };
 
-
-template <uint32_t T>
-__device__ __forceinline__ Frag load_group(const WeightPtrs& W, int row, int c, int n_in) {
+// Loads of one group, with no arithmetic on what they return, so that a
+// caller can issue every load of a wavefront before the first wait (the
+// memory counter is waited on in order: decoding one group right after its
+// load would serialise the loads behind it). finish_group decodes.
+// WAVE (Q4_K only): for wavefront-synchronous callers whose lanes 8j..8j+7
+// hold the eight groups of one super-block (lane sub takes groups sub,
+// sub + LPR, ... with LPR a multiple of 8): the meta is loaded as one dword
+// per lane and assembled with four shuffles in finish_group, so a wavefront
+// moves 4 instead of 16 meta bytes per lane.
+template <uint32_t T, bool WAVE>
+__device__ __forceinline__ Frag load_group_raw(const WeightPtrs& W, int row, int c, int n_in, int lane) {
     Frag f{};
-    const int groups = n_in / 32;
-    const size_t gi = size_t(row) * groups + c;
+    const size_t gi = size_t(row) * (n_in / 32) + c;
     if constexpr (T == kQ8_0) {
         const uint4* p = reinterpret_cast<const uint4*>(W.codes + size_t(row) * n_in + size_t(c) * 32);
         f.w0 = p[0];
         f.w1 = p[1];
-        f.d = f16_bits_to_f32(W.d[gi]);
+        f.raw = W.d[gi];
     } else if constexpr (T == kQ4_0) {
         f.w0 = *reinterpret_cast<const uint4*>(W.codes + gi * 16);
-        f.d = f16_bits_to_f32(W.d[gi]);
+        f.raw = W.d[gi];
     } else if constexpr (T == kQ4_K) {
         f.w0 = *reinterpret_cast<const uint4*>(W.codes + gi * 16);
-        f.meta = *reinterpret_cast<const uint4*>(W.aux + (size_t(row) * (n_in / 256) + (c >> 3)) * 16);
-        f.d = f16_bits_to_f32(uint16_t(f.meta.x & 0xFFFF));
-        f.dmin = f16_bits_to_f32(uint16_t(f.meta.x >> 16));
-        k4_scale_min(f.meta.y, f.meta.z, f.meta.w, c & 7, f.sca, f.scb);
+        const uint8_t* m = W.aux + (size_t(row) * (n_in / 256) + (c >> 3)) * 16;
+        if constexpr (WAVE) f.raw = reinterpret_cast<const uint32_t*>(m)[lane & 3];
+        else f.meta = *reinterpret_cast<const uint4*>(m);
     } else {
         f.w0 = *reinterpret_cast<const uint4*>(W.codes + gi * 16);
         f.qh = *reinterpret_cast<const uint2*>(W.aux + gi * 8);
-        const uint16_t s2 = *reinterpret_cast<const uint16_t*>(W.sc + size_t(row) * (n_in / 16) + 2 * c);
-        f.sca = int(int8_t(s2 & 0xFF));
-        f.scb = int(int8_t(s2 >> 8));
-        f.d = f16_bits_to_f32(W.d[size_t(row) * (n_in / 256) + (c >> 3)]);
+        f.raw2 = *reinterpret_cast<const uint16_t*>(W.sc + size_t(row) * (n_in / 16) + 2 * c);
+        f.raw = W.d[size_t(row) * (n_in / 256) + (c >> 3)];
     }
     return f;
 }
 
-// load_group for wavefront-synchronous callers whose lanes 8j..8j+7 hold the
-// eight groups of one super-block (lane sub takes groups sub, sub + LPR, ...
-// with LPR a multiple of 8): the Q4_K meta is loaded as one dword per lane
-// and assembled with four shuffles, so a wavefront moves 4 instead of 16
-// meta bytes per lane. Other types load as load_group.
-template <uint32_t T>
-__device__ __forceinline__ Frag load_group_wave(const WeightPtrs& W, int row, int c, int n_in, int lane) {
-    if constexpr (T != kQ4_K) {
-        return load_group<T>(W, row, c, n_in);
-    } else {
-        Frag f{};
-        const size_t gi = size_t(row) * (n_in / 32) + c;
-        f.w0 = *reinterpret_cast<const uint4*>(W.codes + gi * 16);
-        const uint32_t part = reinterpret_cast<const uint32_t*>(W.aux + (size_t(row) * (n_in / 256) + (c >> 3)) * 16)
-            [lane & 3];
-        const int base = lane & ~7;
-        f.meta = make_uint4(__shfl(part, base), __shfl(part, base + 1), __shfl(part, base + 2), __shfl(part, base + 3));
+// Decodes the scales of a group loaded by load_group_raw<T, WAVE> (group
+// index c; every lane of the wavefront calls it in the WAVE form).
+template <uint32_t T, bool WAVE>
+__device__ __forceinline__ void finish_group(Frag& f, int c, int lane) {
+    if constexpr (T == kQ8_0 || T == kQ4_0) {
+        f.d = f16_bits_to_f32(uint16_t(f.raw));
+    } else if constexpr (T == kQ4_K) {
+        if constexpr (WAVE) {
+            const int base = lane & ~7;
+            f.meta = make_uint4(__shfl(f.raw, base), __shfl(f.raw, base + 1), __shfl(f.raw, base + 2),
+                                __shfl(f.raw, base + 3));
+        }
         f.d = f16_bits_to_f32(uint16_t(f.meta.x & 0xFFFF));
         f.dmin = f16_bits_to_f32(uint16_t(f.meta.x >> 16));
         k4_scale_min(f.meta.y, f.meta.z, f.meta.w, c & 7, f.sca, f.scb);
-        return f;
+    } else {
+        f.sca = int(int8_t(f.raw2 & 0xFF));
+        f.scb = int(int8_t(f.raw2 >> 8));
+        f.d = f16_bits_to_f32(uint16_t(f.raw));
     }
+}
+
+// One group, loaded and decoded (callers that handle one group at a time).
+template <uint32_t T>
+__device__ __forceinline__ Frag load_group(const WeightPtrs& W, int row, int c, int n_in) {
+    Frag f = load_group_raw<T, false>(W, row, c, n_in, 0);
+    finish_group<T, false>(f, c, 0);
+    return f;
 }
 
 // Activation side of one 32-element group for one token.
