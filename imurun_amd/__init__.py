@@ -81,6 +81,7 @@ def load() -> ctypes.CDLL:
         "fish_hip_resident": ([_P], ctypes.c_int),
         "fish_hip_release": ([_P], None),
         "fish_hip_bytes_resident": ([], ctypes.c_uint64),
+        "fish_hip_backend_served": ([], ctypes.c_uint64),
         "fish_hip_backend_matmul": ([_P, _P, ctypes.c_int, ctypes.c_int, ctypes.c_int, _P], ctypes.c_int),
         "fish_hip_backend_matmul_group": ([_P, ctypes.c_int, _P, ctypes.c_int, ctypes.c_int, _P, _P], ctypes.c_int),
     }

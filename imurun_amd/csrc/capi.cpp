@@ -316,7 +316,13 @@ public:
             }
             off += cnt;
         }
+        ++served_;
         return true;
+    }
+
+    uint64_t served() {
+        std::lock_guard<std::mutex> lk(mu_);
+        return served_;
     }
 
 private:
@@ -356,6 +362,7 @@ private:
 
     std::mutex mu_;
     bool init_done_ = false, ok_ = false, broken_ = false;
+    uint64_t served_ = 0;  // matmul groups computed on the device
     std::string name_ = "";
     hipStream_t stream_ = nullptr;
     std::unordered_map<const void*, Resident> map_;
@@ -531,6 +538,7 @@ int fish_hip_upload(const void* key, uint32_t type, const void* data, int n_in, 
 int fish_hip_resident(const void* key) { return HipBackend::instance().resident(key) ? 1 : 0; }
 void fish_hip_release(const void* key) { HipBackend::instance().release(key); }
 uint64_t fish_hip_bytes_resident(void) { return HipBackend::instance().bytes_resident(); }
+uint64_t fish_hip_backend_served(void) { return HipBackend::instance().served(); }
 
 int fish_hip_backend_matmul(const void* key, const float* x, int n_tok, int n_in, int n_out, float* y) {
     const void* keys[1] = {key};

@@ -1,0 +1,61 @@
+// FISH's compute-backend hook implemented over libfish_hip.so: the file FISH
+// would add as model/fish/src/gpu/hip_backend.cpp. It is compiled against
+// FISH's own headers (fish/backend.h, backend.h:26-163), registers itself at
+// load the way the Vulkan backend does (vulkan_backend.cpp:2168-2177), and
+// forwards every call to the C ABI of include/fish_hip.h. FISH's routing
+// (matmul_tensor / matmul_tensors, ops.cpp:283-299) then sends every matmul on
+// a resident tensor to the GPU and keeps everything else on the CPU.
+//
+// Contracts kept (backend.h:11-17): upload() happens at load and fails
+// without side effects when a type or shape is not supported; matmul() is
+// synchronous; a false return makes FISH recompute on the CPU; one call at a
+// time (the C ABI serialises); after a HIP error every call returns false.
+#include <fish/backend.h>
+
+#include <cstdlib>
+
+#include "fish_hip.h"
+
+namespace fish {
+namespace {
+
+class HipComputeBackend final : public ComputeBackend {
+public:
+    const char* name() const override { return "hip"; }
+    const char* device_name() const override { return fish_hip_device_name(); }
+    uint64_t memory_total() const override { return fish_hip_memory_total(); }
+    uint64_t memory_free() const override { return fish_hip_memory_free(); }
+    bool supports(GgmlType t) const override { return fish_hip_supports(uint32_t(t)) != 0; }
+
+    bool upload(const TensorInfo* t) override {
+        if (!t || !t->data || t->ne.size() < 2 || !supports(t->type)) return false;
+        // [ne1][ne0] rows of ne0 inputs; a 3-D expert tensor passes ne[2] experts
+        const int n_expert = t->ne.size() > 2 ? int(t->ne[2]) : 1;
+        return fish_hip_upload(t, uint32_t(t->type), t->data, int(t->ne[0]), int(t->ne[1]), n_expert) != 0;
+    }
+    bool resident(const TensorInfo* t) const override { return fish_hip_resident(t) != 0; }
+    void release(const TensorInfo* t) override { fish_hip_release(t); }
+    uint64_t bytes_resident() const override { return fish_hip_bytes_resident(); }
+
+    // `acts` is not used: the device quantizer writes the same int8 bytes as ActBatch
+    bool matmul(const TensorInfo* t, const float* x, const ActBatch*, int n_tok, int n_in, int n_out,
+                float* y) override {
+        return fish_hip_backend_matmul(t, x, n_tok, n_in, n_out, y) != 0;
+    }
+    bool matmul_group(const TensorInfo* const* ts, int n, const float* x, const ActBatch*, int n_tok, int n_in,
+                      const int* n_outs, float* const* ys) override {
+        return fish_hip_backend_matmul_group(reinterpret_cast<const void* const*>(ts), n, x, n_tok, n_in, n_outs,
+                                             ys) != 0;
+    }
+};
+
+struct Registrar {
+    Registrar() {
+        const char* e = std::getenv("FISH_HIP");  // FISH_HIP=0 keeps FISH on the CPU
+        if (e && *e == '0') return;
+        if (fish_hip_backend_available()) set_gpu_backend(new HipComputeBackend());  // lives until exit
+    }
+} g_hip_registrar;
+
+}  // namespace
+}  // namespace fish

@@ -192,6 +192,12 @@ FISH_HIP_API int fish_hip_upload(const void* key, uint32_t type, const void* dat
 FISH_HIP_API int fish_hip_resident(const void* key);
 FISH_HIP_API void fish_hip_release(const void* key);
 FISH_HIP_API uint64_t fish_hip_bytes_resident(void);
+/* How many fish_hip_backend_matmul / _matmul_group calls this process has
+ * computed on the device (each one that returned 1), so a host can confirm
+ * that its matmuls ran on the GPU rather than falling back to its CPU path.
+ * No counterpart in FISH's ComputeBackend; a diagnostic like the stats FISH
+ * reports (c_api.h fish_stats). */
+FISH_HIP_API uint64_t fish_hip_backend_served(void);
 /* ComputeBackend::matmul (backend.h:73-76): y valid on return; 1 ok, 0 failed
  * (y untouched; the caller recomputes on the CPU, ops.cpp:283-291). */
 FISH_HIP_API int fish_hip_backend_matmul(const void* key, const float* x, int n_tok, int n_in, int n_out, float* y);

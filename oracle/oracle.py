@@ -256,3 +256,80 @@ class Ref:
         self.L.ref_moe_ffn(_ptr(x), _ptr(logits), n_tok, E, F, NE, K, int(norm), tg, _ptr(wg), tu, _ptr(wu), td,
                            _ptr(wd), _ptr(out), _ptr(sel), _ptr(wsel))
         return out, sel, wsel
+
+
+DROPIN_SO = os.path.join(HERE, "_ref", "libfishref_hip.so")
+
+
+class DropIn:
+    """FISH's own routing (ops.cpp:283-299) with the HIP backend binding
+    registered, from _ref/libfishref_hip.so. Weight bytes stay owned by the
+    caller (numpy arrays kept alive in self._keep)."""
+
+    @staticmethod
+    def available() -> bool:
+        return os.path.exists(DROPIN_SO)
+
+    def __init__(self, path: str = DROPIN_SO):
+        L = ctypes.CDLL(path)
+        self.L = L
+        L.drop_backend_name.restype = ctypes.c_char_p
+        L.drop_tensor_new.restype = _P
+        L.drop_tensor_new.argtypes = [ctypes.c_uint32, _P, ctypes.c_int, ctypes.c_int]
+        for f in ("drop_tensor_free", "drop_upload", "drop_resident", "drop_release"):
+            getattr(L, f).argtypes = [_P]
+        L.drop_bytes_resident.restype = ctypes.c_uint64
+        mm = [_P, _P, ctypes.c_int, ctypes.c_int, ctypes.c_int, _P]
+        L.drop_matmul_tensor.argtypes = mm
+        L.drop_matmul_cpu.argtypes = mm
+        L.drop_matmul_tensors.argtypes = [_P, ctypes.c_int, _P, ctypes.c_int, ctypes.c_int, _P, _P]
+        self._keep = {}
+
+    def backend_name(self) -> str:
+        return self.L.drop_backend_name().decode()
+
+    def tensor(self, t: int, packed: np.ndarray, n_in: int, n_out: int):
+        packed = np.ascontiguousarray(packed)
+        h = self.L.drop_tensor_new(t, _ptr(packed), n_in, n_out)
+        self._keep[h] = (packed, n_in, n_out)
+        return h
+
+    def free(self, h) -> None:
+        self.L.drop_tensor_free(h)
+        self._keep.pop(h, None)
+
+    def upload(self, h) -> bool:
+        return bool(self.L.drop_upload(h))
+
+    def resident(self, h) -> bool:
+        return bool(self.L.drop_resident(h))
+
+    def release(self, h) -> None:
+        self.L.drop_release(h)
+
+    def bytes_resident(self) -> int:
+        return int(self.L.drop_bytes_resident())
+
+    def _mm(self, fn, h, x):
+        _, n_in, n_out = self._keep[h]
+        x = np.ascontiguousarray(x, np.float32)
+        y = np.zeros((x.shape[0], n_out), np.float32)
+        fn(h, _ptr(x), x.shape[0], n_in, n_out, _ptr(y))
+        return y
+
+    def matmul_tensor(self, h, x):
+        return self._mm(self.L.drop_matmul_tensor, h, x)
+
+    def matmul_cpu(self, h, x):
+        return self._mm(self.L.drop_matmul_cpu, h, x)
+
+    def matmul_tensors(self, hs, x):
+        x = np.ascontiguousarray(x, np.float32)
+        n_in = self._keep[hs[0]][1]
+        ys = [np.zeros((x.shape[0], self._keep[h][2]), np.float32) for h in hs]
+        arr = (_P * len(hs))(*hs)
+        outs = (ctypes.c_int * len(hs))(*[self._keep[h][2] for h in hs])
+        yp = (_P * len(hs))(*[y.ctypes.data for y in ys])
+        self.L.drop_matmul_tensors(arr, len(hs), _ptr(x), x.shape[0], n_in, outs, yp)
+        return ys
+

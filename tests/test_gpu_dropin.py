@@ -1,0 +1,103 @@
+"""FISH's own host code driving the HIP path: the drop-in test.
+
+oracle/_ref/libfishref_hip.so holds the reference's ops/quant/gguf sources
+(compiled where they lie) and the FISH-side backend binding
+(imurun_amd/fish_side/hip_backend.cpp), which registers itself with FISH at
+load like the Vulkan backend (vulkan_backend.cpp:2168-2177). The tests do
+what FISH's loader and forward pass do -- supports() and upload() per weight
+tensor, then matmul_tensor / matmul_tensors (ops.cpp:283-299) -- and compare
+with FISH's CPU matmul_batch on the same bytes (max error <= 1e-4 of the
+output's L-inf norm). The library exists only where the reference sources
+were present at build time; without it these tests skip.
+"""
+import numpy as np
+import pytest
+
+import imurun_amd as fh
+from imurun_amd.synth import normal
+from oracle.oracle import DropIn
+
+pytestmark = [pytest.mark.gpu,
+              pytest.mark.skipif(not DropIn.available(), reason="oracle/_ref/libfishref_hip.so not built")]
+
+TOL = 1e-4
+Q5_K = 13  # a type FISH has and this backend does not take
+
+
+@pytest.fixture(scope="module")
+def drop():
+    import torch
+    assert torch.cuda.is_available(), "GPU tests need a ROCm device"
+    d = DropIn()
+    assert d.backend_name() == "hip", "the HIP binding did not register with FISH"
+    return d
+
+
+def served() -> int:
+    """Device matmuls computed so far (the backend's own count, same library instance)."""
+    return int(fh.load().fish_hip_backend_served())
+
+
+def check(got, want, what):
+    err = float(np.max(np.abs(got - want)))
+    scale = float(np.max(np.abs(want)))
+    assert err <= TOL * scale, f"{what}: max err {err:.3e} vs {TOL} * {scale:.3e}"
+
+
+@pytest.mark.parametrize("t", [fh.Q8_0, fh.Q4_0, fh.Q4_K, fh.Q6_K])
+@pytest.mark.parametrize("n_in,n_out", [(1024, 384), (4096, 512)])
+def test_matmul_tensor_through_fish_routing(drop, t, n_in, n_out):
+    packed = fh.quantize_rows(t, normal(300 + t + n_in, (n_out, n_in), 0.02))
+    h = drop.tensor(t, packed, n_in, n_out)
+    try:
+        before = drop.bytes_resident()
+        assert drop.upload(h) and drop.resident(h)
+        assert drop.bytes_resident() > before
+        for m in (1, 4, 17, 64, 130):
+            x = normal(310 + m + t, (m, n_in), 1.0)
+            n0 = served()
+            y = drop.matmul_tensor(h, x)
+            assert served() == n0 + 1, "FISH did not get this matmul from the device"
+            check(y, drop.matmul_cpu(h, x), f"type {t} {n_out}x{n_in} M={m}")
+        drop.release(h)
+        assert not drop.resident(h)
+    finally:
+        drop.free(h)
+
+
+@pytest.mark.parametrize("t", [fh.Q4_0, fh.Q4_K])
+@pytest.mark.parametrize("m", [1, 5, 96])
+def test_matmul_tensors_gate_up_group(drop, t, m):
+    # gate and up on the same x: matmul_tensors -> ComputeBackend::matmul_group
+    n_in, n_out = 2048, 1536
+    hs = [drop.tensor(t, fh.quantize_rows(t, normal(320 + i + t, (n_out, n_in), 0.02)), n_in, n_out)
+          for i in range(2)]
+    try:
+        for h in hs:
+            assert drop.upload(h)
+        x = normal(330 + m, (m, n_in), 1.0)
+        n0 = served()
+        ys = drop.matmul_tensors(hs, x)
+        assert served() == n0 + 1, "the group was not one device call"
+        for i, h in enumerate(hs):
+            check(ys[i], drop.matmul_cpu(h, x), f"group member {i}, M={m}")
+    finally:
+        for h in hs:
+            drop.release(h)
+            drop.free(h)
+
+
+def test_unsupported_type_stays_on_the_cpu(drop):
+    # supports() is false, upload() is never attempted, matmul_tensor takes FISH's CPU path
+    from oracle.oracle import Oracle
+    n_in, n_out = 512, 64
+    packed = Oracle().quantize_rows(Q5_K, normal(340, (n_out, n_in), 0.02))
+    h = drop.tensor(Q5_K, packed, n_in, n_out)
+    try:
+        assert not drop.upload(h) and not drop.resident(h)
+        x = normal(341, (3, n_in), 1.0)
+        n0 = served()
+        assert np.array_equal(drop.matmul_tensor(h, x), drop.matmul_cpu(h, x))
+        assert served() == n0
+    finally:
+        drop.free(h)
