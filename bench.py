@@ -229,6 +229,23 @@ def run_kquant_gemv(args, torch, fh, dev, t, name):
             "down_pct_hbm": round(100 * b_dn / dn_us / 1e3 / HBM_PEAK_GBS, 2)}
 
 
+def run_q5k_prefill(args, torch, fh, dev):
+    """Q5_K gate+up (2 x 14336x4096, a Q5_K_M layer's FFN input side) at M = 512 as one
+    grouped GEMM launch on activations quantized once; 1024 distinct packed rows repeated."""
+    from imurun_amd.synth import normal
+    M, t = 512, fh.Q5_K
+    ws = []
+    for seed in (221, 222):
+        base = fh.quantize_rows(t, normal(seed, (1024, E), 0.02))
+        ws.append(fh.repack(t, torch.from_numpy(base).to(dev).repeat(F // 1024), E, F))
+    act = fh.quantize(torch.from_numpy(normal(223, (M, E))).to(dev))
+    ys = [torch.empty((M, F), dtype=torch.float32, device=dev) for _ in range(2)]
+    us = graph_time_seq(torch, [lambda: fh.matmul_group(t, ws, act, M, E, [F, F], ys=ys)] * 4, 10)
+    ops = 2 * 2 * M * F * E
+    return {"workload": "Q5_K gate+up GEMM 2 x 14336x4096, M=512, one grouped launch", "us": round(us, 2),
+            "tops": round(ops / us / 1e6, 1), "pct_int8_peak": round(100 * ops / us / 1e6 / INT8_PEAK_TOPS, 2)}
+
+
 def run_moe(args, torch, fh, dev, name, NE, K, E, F_, types, cases):
     """Expert FFN layer at the given token counts; one distinct expert replicated (same traffic)."""
     from imurun_amd.synth import normal
@@ -437,12 +454,15 @@ def main() -> int:
     if not args.no_extras:
         out["q8_0_gemv"] = run_q8_gemv(args, torch, fh, dev)
         out["q4_k_gemv"] = run_kquant_gemv(args, torch, fh, dev, fh.Q4_K, "Q4_K")
+        out["q5_k_gemv"] = run_kquant_gemv(args, torch, fh, dev, fh.Q5_K, "Q5_K")
         out["q6_k_gemv"] = run_kquant_gemv(args, torch, fh, dev, fh.Q6_K, "Q6_K")
         out["moe_mixtral"] = run_moe(args, torch, fh, dev, "Mixtral-8x7B", 8, 2, 4096, 14336,
                                      (fh.Q4_K, fh.Q4_K, fh.Q4_K), (1, 64))
         out["moe_qwen3"] = run_moe(args, torch, fh, dev, "Qwen3-30B-A3B", 128, 8, 2048, 768,
                                    (fh.Q4_K, fh.Q4_K, fh.Q6_K), (1, 256))
     if not args.no_prefill:
+        if not args.no_extras:
+            out["q5_k_prefill"] = run_q5k_prefill(args, torch, fh, dev)
         ops, layer_us, per = run_prefill(args, torch, fh, dev)
         tops = ops / layer_us / 1e6
         proj_ops = {"qkv": 2 * 512 * 6144 * E, "o": 2 * 512 * E * E, "gate_up": 2 * 512 * 2 * F * E,

@@ -22,10 +22,10 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libfish_hip.so")
 
-Q4_0, Q8_0, Q4_K, Q6_K = 2, 8, 12, 14
-TYPE_NAMES = {Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q6_K: "Q6_K"}
-BLOCK_ELEMS = {Q4_0: 32, Q8_0: 32, Q4_K: 256, Q6_K: 256}
-BLOCK_BYTES = {Q4_0: 18, Q8_0: 34, Q4_K: 144, Q6_K: 210}
+Q4_0, Q8_0, Q4_K, Q5_K, Q6_K = 2, 8, 12, 13, 14
+TYPE_NAMES = {Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K"}
+BLOCK_ELEMS = {Q4_0: 32, Q8_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256}
+BLOCK_BYTES = {Q4_0: 18, Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210}
 
 _P = ctypes.c_void_p
 _lib = None
@@ -238,7 +238,7 @@ def matmul_batch(t: int, w, x, n_out: int, stream=None):
 def block_ints(t: int, w, act, n_in: int, n_out: int, stream=None):
     """Per-block integer dots of every row with token 0 (int32 cuda tensor)."""
     import torch
-    per_row = (2 * (n_in // 256)) if t == Q4_K else ((n_in // 256) if t == Q6_K else n_in // 32)
+    per_row = (2 * (n_in // 256)) if t in (Q4_K, Q5_K) else ((n_in // 256) if t == Q6_K else n_in // 32)
     out = torch.empty(n_out * per_row, dtype=torch.int32, device=w.device)
     _check(load().fish_hip_block_ints(t, w.data_ptr(), act.data_ptr(), n_in, n_out, out.data_ptr(),
                                       _stream(stream)), "block_ints")

@@ -111,7 +111,8 @@ __device__ __forceinline__ uint4 transpose4(uint4 v) {
 // Raw weight data of one 256-element unit for one 16-row block (the lane's row).
 struct WUnit {
     uint4 v[4];     // codes: Q4 layouts chunks 2q, 2q+1 (v[0..1]); Q8_0 groups 2q, 2q+1 (v[0..3])
-    uint4 m;        // Q8_0/Q4_0: 8 f16 group scales; Q4_K: d, dmin, scales; Q6_K: 16 int8 scales
+    uint4 m;        // Q8_0/Q4_0: 8 f16 group scales; Q4_K / Q5_K: d, dmin, scales; Q6_K: 16 int8 scales
+    uint4 hb[2];    // Q5_K: fifth bits of the 8 groups (one dword each)
     uint4 qh[4];    // Q6_K: high bits of the 8 groups (8 bytes each)
     uint32_t d6;    // Q6_K: f16 d
 };
@@ -133,8 +134,13 @@ __device__ __forceinline__ void load_w(WUnit& o, const WeightPtrs& W, uint32_t r
         o.v[1] = p[1];
         if constexpr (T == kQ4_0) {
             o.m = *reinterpret_cast<const uint4*>(W.d + (row * groups + c0));
-        } else if constexpr (T == kQ4_K) {
+        } else if constexpr (has_mins(T)) {
             o.m = *reinterpret_cast<const uint4*>(W.aux + (row * units + u) * 16);
+            if constexpr (T == kQ5_K) {
+                const uint4* h = reinterpret_cast<const uint4*>(W.hb + (row * groups + c0));
+                o.hb[0] = h[0];
+                o.hb[1] = h[1];
+            }
         } else {
             const uint4* h = reinterpret_cast<const uint4*>(W.aux + (row * groups + c0) * 8);
 #pragma unroll
@@ -152,10 +158,10 @@ __device__ __forceinline__ void load_w(WUnit& o, const WeightPtrs& W, uint32_t r
 // t as two float4) and, for Q4_K, the 16 split bsum bytes of token t.
 template <uint32_t T, int NB>
 struct ALds {
-    static constexpr bool kq = (T == kQ4_K || T == kQ6_K);
+    static constexpr bool kq = kquant_type(T);
     uint4 code[2][NB * 256];
     float dk[2][kq ? NB * 16 : 1];
-    uint4 bs[2][T == kQ4_K ? NB * 16 : 1];
+    uint4 bs[2][has_mins(T) ? NB * 16 : 1];
     float4 da[2][kq ? 1 : NB * 32];
 };
 
@@ -174,7 +180,7 @@ struct AMap {
 
 template <uint32_t T, int NB>
 __device__ __forceinline__ AReg<NB> load_act(const ActPtrs& A, const AMap& m, int u, int tid) {
-    constexpr bool kq = (T == kQ4_K || T == kQ6_K);
+    constexpr bool kq = kquant_type(T);
     const int8_t* codes = kq ? A.m256 : A.m32;
     const uint32_t c = uint32_t(u) * 256 + (tid & 15) * 16;
     AReg<NB> r;
@@ -185,7 +191,7 @@ __device__ __forceinline__ AReg<NB> load_act(const ActPtrs& A, const AMap& m, in
     r.dk = 0.0f;
     if constexpr (kq) {
         r.dk = A.d256[m.meta_off + u];
-        if constexpr (T == kQ4_K) r.meta = *reinterpret_cast<const uint4*>(A.bsm + (m.meta_off + u) * 16);
+        if constexpr (has_mins(T)) r.meta = *reinterpret_cast<const uint4*>(A.bsm + (m.meta_off + u) * 16);
     } else {
         r.meta = *reinterpret_cast<const uint4*>(A.d32 + (m.meta_off + 8 * u + 4 * (tid & 1)));
     }
@@ -198,9 +204,9 @@ __device__ __forceinline__ void store_act(ALds<T, NB>& L, int slot, const AReg<N
     L.code[slot][t0 * 16 + (c ^ t0)] = r.c0;
     if constexpr (NB > 1)
         if (nbu > 1) L.code[slot][(t0 + 16) * 16 + (c ^ t0)] = r.c1;
-    if constexpr (T == kQ4_K || T == kQ6_K) {
+    if constexpr (kquant_type(T)) {
         if (tid < NB * 16) L.dk[slot][tid] = r.dk;
-        if constexpr (T == kQ4_K)
+        if constexpr (has_mins(T))
             if (tid >= 128 && tid < 128 + NB * 16) L.bs[slot][tid - 128] = r.meta;
     } else {
         if (tid < NB * 32) L.da[slot][tid] = __builtin_bit_cast(float4, r.meta);
@@ -268,7 +274,7 @@ __device__ __forceinline__ void unit_dot(const WUnit& w, const ALds<T, NB>& L, i
                 for (int r = 0; r < 4; ++r) acc[nb][r] += float(c[r]) * (dw[g] * da[r][g]);
             }
         }
-    } else if constexpr (T == kQ4_K) {
+    } else if constexpr (has_mins(T)) {
         const float d = f16_bits_to_f32(uint16_t(w.m.x & 0xFFFF));
         const float dmin = f16_bits_to_f32(uint16_t(w.m.x >> 16));
         const uint32_t sc_lo = w.m.y & 0x3F3F3F3Fu;
@@ -280,10 +286,12 @@ __device__ __forceinline__ void unit_dot(const WUnit& w, const ALds<T, NB>& L, i
         const uint32_t fb[2] = {sc_lo & 0x07070707u, sc_hi & 0x07070707u};
         const long m8 = pack2(mn_lo, mn_hi);
         const long mh = (q == 0) ? m8 : 0L, ml = (q == 1) ? m8 : 0L;
-        // each pair of planes is formed once and consumed by every staged token block at once
-        v4i H[NB], Lo[NB];
+        // Q5_K: a third plane sc * (fifth bit) (<= 63), I = 8 H + L + 16 C
+        const uint32_t sc2[2] = {sc_lo, sc_hi};
+        // each set of planes is formed once and consumed by every staged token block at once
+        v4i H[NB], Lo[NB], C[NB];
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb) H[nb] = Lo[nb] = zero;
+        for (int nb = 0; nb < NB; ++nb) H[nb] = Lo[nb] = C[nb] = zero;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int g0 = 2 * i, g1 = 2 * i + 1;
@@ -291,14 +299,24 @@ __device__ __forceinline__ void unit_dot(const WUnit& w, const ALds<T, NB>& L, i
             const uint32_t b0 = bcast2(fb[g0 >> 2], g0 & 3), b1 = bcast2(fb[g1 >> 2], g1 & 3);
             const v4i pa = {int(mul4(lo[g0], a0)), int(mul4(hi[g0], a0)), int(mul4(lo[g1], a1)), int(mul4(hi[g1], a1))};
             const v4i pb = {int(mul4(lo[g0], b0)), int(mul4(hi[g0], b0)), int(mul4(lo[g1], b1)), int(mul4(hi[g1], b1))};
+            v4i pc = zero;
+            if constexpr (T == kQ5_K) {
+                // the lane's fifth bits: bit 8b + q (elements 4q + b), bit 8b + 4 + q (16 + 4q + b)
+                const uint32_t h0 = dword_at(w.hb[g0 >> 2], g0 & 3), h1 = dword_at(w.hb[g1 >> 2], g1 & 3);
+                const uint32_t s0 = bcast2(sc2[g0 >> 2], g0 & 3), s1 = bcast2(sc2[g1 >> 2], g1 & 3);
+                pc = v4i{int(mul4((h0 >> q) & 0x01010101u, s0)), int(mul4((h0 >> (4 + q)) & 0x01010101u, s0)),
+                         int(mul4((h1 >> q) & 0x01010101u, s1)), int(mul4((h1 >> (4 + q)) & 0x01010101u, s1))};
+            }
             const v4i a_0 = __builtin_bit_cast(v4i, L.code[slot][aidx[i]]);
             H[0] = mfma64(a_0, pa, H[0]);
             Lo[0] = mfma64(a_0, pb, Lo[0]);
+            if constexpr (T == kQ5_K) C[0] = mfma64(a_0, pc, C[0]);
             if constexpr (NB > 1) {
                 if (nbu > 1) {
                     const v4i a_1 = __builtin_bit_cast(v4i, L.code[slot][256 + aidx[i]]);
                     H[1] = mfma64(a_1, pa, H[1]);
                     Lo[1] = mfma64(a_1, pb, Lo[1]);
+                    if constexpr (T == kQ5_K) C[1] = mfma64(a_1, pc, C[1]);
                 }
             }
         }
@@ -313,7 +331,7 @@ __device__ __forceinline__ void unit_dot(const WUnit& w, const ALds<T, NB>& L, i
             const float dkr[4] = {dk.x, dk.y, dk.z, dk.w};
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int isum = (H[nb][r] << 3) + Lo[nb][r];
+                const int isum = (H[nb][r] << 3) + Lo[nb][r] + (C[nb][r] << 4);
                 const int mins = (ch[r] << 6) + cl[r];
                 acc[nb][r] += dkr[r] * (d * float(isum) - dmin * float(mins));
             }
@@ -378,7 +396,7 @@ __global__ __launch_bounds__(64 * kWaves) void batch_mfma_kernel(WeightPtrs W, A
                                                                  int n_tok, TokenMap map, float* __restrict__ y,
                                                                  int ldy) {
     constexpr int TOK = 16 * NB;
-    constexpr bool kq = (T == kQ4_K || T == kQ6_K);
+    constexpr bool kq = kquant_type(T);
     __shared__ ALds<T, NB> L;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int j = lane & 15, q = lane >> 4;
@@ -398,7 +416,8 @@ __global__ __launch_bounds__(64 * kWaves) void batch_mfma_kernel(WeightPtrs W, A
             W.codes += erow * size_t(groups) * 16;
         }
         if constexpr (T == kQ8_0 || T == kQ4_0) W.d += erow * size_t(groups);
-        if constexpr (T == kQ4_K) W.aux += erow * size_t(units) * 16;
+        if constexpr (has_mins(T)) W.aux += erow * size_t(units) * 16;
+        if constexpr (T == kQ5_K) W.hb += erow * size_t(groups);
         if constexpr (T == kQ6_K) {
             W.aux += erow * size_t(groups) * 8;
             W.sc += erow * size_t(n_in / 16);
@@ -549,6 +568,7 @@ hipError_t launch_batch_mfma(const void* w, const WeightLayout& WL, const void* 
         case kQ8_0: return batch_pick<kQ8_0>(tok, W, A, WL.n_in, n_out, n_tok, map, yb, y, ldy, s);
         case kQ4_0: return batch_pick<kQ4_0>(tok, W, A, WL.n_in, n_out, n_tok, map, yb, y, ldy, s);
         case kQ4_K: return batch_pick<kQ4_K>(tok, W, A, WL.n_in, n_out, n_tok, map, yb, y, ldy, s);
+        case kQ5_K: return batch_pick<kQ5_K>(tok, W, A, WL.n_in, n_out, n_tok, map, yb, y, ldy, s);
         case kQ6_K: return batch_pick<kQ6_K>(tok, W, A, WL.n_in, n_out, n_tok, map, yb, y, ldy, s);
         default: return hipErrorInvalidValue;
     }

@@ -39,7 +39,9 @@ int hip_fail(hipError_t e, const char* what) {
 
 hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
 
-bool type_ok(uint32_t type) { return type == kQ8_0 || type == kQ4_0 || type == kQ4_K || type == kQ6_K; }
+bool type_ok(uint32_t type) {
+    return type == kQ8_0 || type == kQ4_0 || type == kQ4_K || type == kQ5_K || type == kQ6_K;
+}
 
 // Matmul dispatch on an already quantized activation buffer: up to
 // kGemvMaxTok tokens -> the bandwidth-bound GEMV; up to kBatchMaxTok tokens

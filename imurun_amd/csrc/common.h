@@ -42,14 +42,19 @@
 
 namespace fishhip {
 
-enum : uint32_t { kF32 = 0, kF16 = 1, kQ4_0 = 2, kQ8_0 = 8, kQ4_K = 12, kQ6_K = 14 };
+enum : uint32_t { kF32 = 0, kF16 = 1, kQ4_0 = 2, kQ8_0 = 8, kQ4_K = 12, kQ5_K = 13, kQ6_K = 14 };
+
+// K-quants: 256-value super-blocks, multiplied with the Q8ActK activations.
+constexpr bool kquant_type(uint32_t t) { return t == kQ4_K || t == kQ5_K || t == kQ6_K; }
+// K-quants with a per-group min (w = d sc q - dmin m): the Q8ActK block sums enter.
+constexpr bool has_mins(uint32_t t) { return t == kQ4_K || t == kQ5_K; }
 
 inline size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 
 struct WeightLayout {
     uint32_t type = 0;
     int n_in = 0, n_out = 0;
-    size_t codes = 0, aux = 0, sc = 0, d = 0, total = 0;  // plane byte offsets
+    size_t codes = 0, aux = 0, sc = 0, d = 0, hb = 0, total = 0;  // plane byte offsets
 };
 
 // Plane offsets of a repacked tensor; total == 0 when the type/shape is refused.
@@ -77,6 +82,15 @@ inline WeightLayout weight_layout(uint32_t type, int n_in, int n_out) {
             L.codes = off; off = align256(off + N * (K / 32) * 16);
             L.aux = off;   off = align256(off + N * (K / 256) * 16);
             break;
+        case kQ5_K:
+            // Q4_K's planes plus the fifth bits: one dword per group, bit 8b + k
+            // = element 4k + b, bit 8b + 4 + k = element 16 + 4k + b (k, b < 4),
+            // so a shift and a mask put dword k's four bits at bit 4 of its bytes
+            if (K % 256) return L;
+            L.codes = off; off = align256(off + N * (K / 32) * 16);
+            L.aux = off;   off = align256(off + N * (K / 256) * 16);
+            L.hb = off;    off = align256(off + N * (K / 32) * 4);
+            break;
         case kQ6_K:
             if (K % 256) return L;
             L.codes = off; off = align256(off + N * (K / 32) * 16);
@@ -97,12 +111,13 @@ inline size_t gguf_row_bytes(uint32_t type, int n_in) {
         case kQ8_0: return size_t(n_in / 32) * 34;
         case kQ4_0: return size_t(n_in / 32) * 18;
         case kQ4_K: return size_t(n_in / 256) * 144;
+        case kQ5_K: return size_t(n_in / 256) * 176;
         case kQ6_K: return size_t(n_in / 256) * 210;
         default: return 0;
     }
 }
 
-inline bool is_kquant(uint32_t type) { return type == kQ4_K || type == kQ6_K; }
+inline bool is_kquant(uint32_t type) { return kquant_type(type); }
 
 struct ActLayout {
     int n_tok = 0, n_in = 0;
@@ -181,6 +196,7 @@ struct WeightPtrs {
     const uint8_t* aux;
     const int8_t* sc;
     const uint16_t* d;
+    const uint32_t* hb;  // Q5_K fifth bits
 };
 
 inline WeightPtrs weight_ptrs(const void* base, const WeightLayout& L) {
@@ -190,6 +206,7 @@ inline WeightPtrs weight_ptrs(const void* base, const WeightLayout& L) {
     p.aux = b + L.aux;
     p.sc = reinterpret_cast<const int8_t*>(b + L.sc);
     p.d = reinterpret_cast<const uint16_t*>(b + L.d);
+    p.hb = reinterpret_cast<const uint32_t*>(b + L.hb);
     return p;
 }
 

@@ -8,6 +8,7 @@
 //   Q8_0  sum_k w_k x_k                          (w int8)
 //   Q4_0  sum_k (nib_k - 8) x_k                  (nib 0..15)
 //   Q4_K  dot_g = sum_l q_l x_l; the caller forms sc_g*dot_g and m_g*bsum_g
+//   Q5_K  the same with 5-bit codes (quant_x86.cpp:384-427)
 //   Q6_K  sc_a*sum_{16}(q-32)x + sc_b*sum_{16}(q-32)x  (two 16-groups)
 #pragma once
 
@@ -50,6 +51,22 @@ __device__ __forceinline__ int isum_q4_0(uint4 w, uint4 alo, uint4 ahi, int asum
 
 __device__ __forceinline__ int dot_q4_k(uint4 w, uint4 alo, uint4 ahi) {
     return dot16(hi_nibbles(w), ahi, dot16(lo_nibbles(w), alo, 0));
+}
+
+// Q5_K codes: nibbles plus the fifth bits of the group (the repacked dword
+// whose bit 8b + k is element 4k + b and bit 8b + 4 + k element 16 + 4k + b):
+// a shift and a mask move dword k's bits to bit 4 of its bytes.
+__device__ __forceinline__ uint4 q5_codes_lo(uint4 lo, uint32_t h) {
+    return make_uint4(lo.x | ((h << 4) & 0x10101010u), lo.y | ((h << 3) & 0x10101010u),
+                      lo.z | ((h << 2) & 0x10101010u), lo.w | ((h << 1) & 0x10101010u));
+}
+__device__ __forceinline__ uint4 q5_codes_hi(uint4 hi, uint32_t h) {
+    return make_uint4(hi.x | (h & 0x10101010u), hi.y | ((h >> 1) & 0x10101010u), hi.z | ((h >> 2) & 0x10101010u),
+                      hi.w | ((h >> 3) & 0x10101010u));
+}
+
+__device__ __forceinline__ int dot_q5_k(uint4 w, uint32_t h, uint4 alo, uint4 ahi) {
+    return dot16(q5_codes_hi(hi_nibbles(w), h), ahi, dot16(q5_codes_lo(lo_nibbles(w), h), alo, 0));
 }
 
 __device__ __forceinline__ int isum_q6_k(uint4 w, uint2 qh, uint4 alo, uint4 ahi, int s16a, int s16b, int sca,

@@ -5,14 +5,16 @@
 // quant_x86.cpp:346-382, :445-495), per output (token t, row r) and
 // super-block of 256 values:
 //   Q4_K  I = sum_g sc_g sum_l q x       J = sum_g m_g bsum_g
-//         y += xd * (d * I - dmin * J)
+//         y += xd * (d * I - dmin * J)       (Q5_K the same with 5-bit q,
+//         quant_x86.cpp:384-427)
 //   Q6_K  I = sum_j sc_j sum_{16} (q - 32) x            y += xd * (d * I)
 // A scaled code (sc * q up to 945, sc * (q - 32) up to 4096 in magnitude) does
 // not fit an int8 MFMA operand, so every weight is split into two int8 planes
 // that one MFMA each multiplies with the same activation operand:
 //   Q4_K  sc = 8 a + b (a, b in 0..7): planes a*q and b*q (<= 105), I = 8 H + L
 //         -- one packed 16-bit multiply makes four bytes of a plane;
-//   Q6_K  w' = sc * (q - 32) = 64 hi + lo (0 <= lo < 64): I = 64 H + L.
+//   Q6_K  w' = sc * (q - 32) = 64 hi + lo (0 <= lo < 64): I = 64 H + L;
+//   Q5_K  w' = sc * q (<= 1953) = 64 hi + lo the same way.
 // J is exact on one f16 MFMA per super-block: A = (bsum >> 6, bsum & 63) per
 // token (written by the quantizer), B = (64 m_g, m_g) per row, all small
 // integers, so every product and sum is exact in f32.
@@ -25,6 +27,7 @@
 // stage ahead; two wavefronts per SIMD hide each other's latencies. The lane that owns an output owns its weight row, so row
 // scales are lane scalars; token scales come in output-register order.
 #include "common.h"
+#include "dots.h"
 #include "kernels.h"
 
 namespace fishhip {
@@ -45,9 +48,10 @@ constexpr int RING = 3;    // LDS stages in flight
 // and its dequantisation.
 struct Raw {
     uint4 codes;   // 16 bytes: Q4 nibble chunk (Q6_K: the low nibbles)
-    uint4 meta;    // Q4_K: d, dmin, scales[12] of the super-block
+    uint4 meta;    // Q4_K / Q5_K: d, dmin, scales[12] of the super-block
     uint2 qh;      // Q6_K: high bits
     uint32_t sc2;  // Q6_K: the two 16-value scales of the step (bytes 0, 1)
+    uint32_t hb;   // Q5_K: fifth bits of the step's 32 values
 };
 
 template <uint32_t T>
@@ -55,8 +59,9 @@ __device__ __forceinline__ void load_raw(Raw& r, const WeightPtrs& W, int row, i
     const int groups = n_in / 32;
     const size_t gi = size_t(row) * groups + step;
     r.codes = *reinterpret_cast<const uint4*>(W.codes + gi * 16);
-    if constexpr (T == kQ4_K) {
+    if constexpr (has_mins(T)) {
         r.meta = *reinterpret_cast<const uint4*>(W.aux + (size_t(row) * (n_in / 256) + (step >> 3)) * 16);
+        if constexpr (T == kQ5_K) r.hb = W.hb[gi];
     } else {
         r.qh = *reinterpret_cast<const uint2*>(W.aux + gi * 8);
         r.sc2 = *reinterpret_cast<const uint16_t*>(W.sc + size_t(row) * (n_in / 16) + 2 * step);
@@ -94,6 +99,18 @@ __device__ __forceinline__ void dequant(const Raw& r, int step, uint4 (&out)[2][
         out[0][1] = make_uint4(mul4(n1.x, a), mul4(n1.y, a), mul4(n1.z, a), mul4(n1.w, a));
         out[1][0] = make_uint4(mul4(n0.x, b), mul4(n0.y, b), mul4(n0.z, b), mul4(n0.w, b));
         out[1][1] = make_uint4(mul4(n1.x, b), mul4(n1.y, b), mul4(n1.z, b), mul4(n1.w, b));
+    } else if constexpr (T == kQ5_K) {
+        int sc, mn;
+        k4_scale_min(r.meta.y, r.meta.z, r.meta.w, step & 7, sc, mn);
+        const v2s scv = {short(sc), short(sc)}, off = {0, 0};
+        const uint4 q[2] = {q5_codes_lo(n0, r.hb), q5_codes_hi(n1, r.hb)};
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            split6(q[h].x, scv, off, out[0][h].x, out[1][h].x);
+            split6(q[h].y, scv, off, out[0][h].y, out[1][h].y);
+            split6(q[h].z, scv, off, out[0][h].z, out[1][h].z);
+            split6(q[h].w, scv, off, out[0][h].w, out[1][h].w);
+        }
     } else {
         const uint4 nib[2] = {n0, n1};
 #pragma unroll
@@ -114,10 +131,10 @@ __device__ __forceinline__ void dequant(const Raw& r, int step, uint4 (&out)[2][
 
 // Dequantisation in parts, so that it can be spread over a stage's MFMAs:
 // prep once per item, then part j (0..3) writes its 16-byte pieces.
-//   Q4_K: part j = plane j >> 1 of half j & 1;  Q6_K: parts 0, 1 = both planes of half j.
+//   Q4_K: part j = plane j >> 1 of half j & 1;  Q5_K, Q6_K: parts 0, 1 = both planes of half j.
 struct DqPrep {
     uint32_t f[2];   // Q4_K: packed 16-bit factors a, b of the two planes
-    short s6[2];     // Q6_K: the two 16-value scales
+    short s6[2];     // Q6_K: the two 16-value scales; Q5_K: the group scale (both)
 };
 
 template <uint32_t T>
@@ -128,6 +145,10 @@ __device__ __forceinline__ DqPrep dequant_prep(const Raw& r, int step) {
         k4_scale_min(r.meta.y, r.meta.z, r.meta.w, step & 7, sc, mn);
         p.f[0] = uint32_t(sc >> 3) * 0x00010001u;
         p.f[1] = uint32_t(sc & 7) * 0x00010001u;
+    } else if constexpr (T == kQ5_K) {
+        int sc, mn;
+        k4_scale_min(r.meta.y, r.meta.z, r.meta.w, step & 7, sc, mn);
+        p.s6[0] = p.s6[1] = short(sc);
     } else {
         p.s6[0] = short(int8_t(r.sc2 & 0xFF));
         p.s6[1] = short(int8_t((r.sc2 >> 8) & 0xFF));
@@ -152,11 +173,18 @@ __device__ __forceinline__ void dequant_part(const Raw& r, const DqPrep& p, int 
         const uint4 n = h ? make_uint4((c.x >> 4) & 0x0F0F0F0Fu, (c.y >> 4) & 0x0F0F0F0Fu, (c.z >> 4) & 0x0F0F0F0Fu,
                                        (c.w >> 4) & 0x0F0F0F0Fu)
                           : make_uint4(c.x & 0x0F0F0F0Fu, c.y & 0x0F0F0F0Fu, c.z & 0x0F0F0F0Fu, c.w & 0x0F0F0F0Fu);
-        const uint32_t qh = h ? r.qh.y : r.qh.x;
-        const uint4 q = make_uint4(n.x | ((qh & 0x03030303u) << 4), n.y | (((qh >> 2) & 0x03030303u) << 4),
-                                   n.z | (((qh >> 4) & 0x03030303u) << 4), n.w | (((qh >> 6) & 0x03030303u) << 4));
+        uint4 q;
+        if constexpr (T == kQ5_K) {
+            q = h ? q5_codes_hi(n, r.hb) : q5_codes_lo(n, r.hb);
+        } else {
+            const uint32_t qh = h ? r.qh.y : r.qh.x;
+            q = make_uint4(n.x | ((qh & 0x03030303u) << 4), n.y | (((qh >> 2) & 0x03030303u) << 4),
+                           n.z | (((qh >> 4) & 0x03030303u) << 4), n.w | (((qh >> 6) & 0x03030303u) << 4));
+        }
         const short s = p.s6[h];
-        const v2s scv = {s, s}, off = {short(-32 * s), short(-32 * s)};
+        // Q6_K: sc * (q - 32); Q5_K: sc * q
+        const short o = (T == kQ5_K) ? short(0) : short(-32 * s);
+        const v2s scv = {s, s}, off = {o, o};
         uint4 hi, lo;
         split6(q.x, scv, off, hi.x, lo.x);
         split6(q.y, scv, off, hi.y, lo.y);
@@ -174,14 +202,14 @@ __global__ __launch_bounds__(64 * WT * WR) __attribute__((amdgpu_waves_per_eu(2)
     constexpr int RWG = 32 * WR;                      // rows per workgroup
     constexpr int ITEMS = RWG * SSTEPS;               // (row, step) items per stage
     constexpr int IPT = (ITEMS + 64 * NW - 1) / (64 * NW);
-    constexpr int SHIFT = (T == kQ4_K) ? 3 : 6;
+    constexpr int SHIFT = (T == kQ4_K) ? 3 : 6;  // I = 8 H + L (Q4_K) or 64 H + L
     // [stage][plane][step][half][row] of 16-byte pieces
     __shared__ uint4 s_b[RING * 2 * SSTEPS * 2 * RWG];
     // per super-block epilogue data, loaded during its first stage:
     // row meta (Q4_K d, dmin, scales; Q6_K d in .x), token scales, mins operands
     __shared__ uint4 s_meta[RWG];
     __shared__ float4 s_xd[2 * WT * 2 * 4];
-    __shared__ uint4 s_j[(T == kQ4_K) ? 2 * WT * 64 : 1];
+    __shared__ uint4 s_j[has_mins(T) ? 2 * WT * 64 : 1];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int l32 = lane & 31, half = lane >> 5;
@@ -313,7 +341,7 @@ __global__ __launch_bounds__(64 * WT * WR) __attribute__((amdgpu_waves_per_eu(2)
 
     // epilogue data of super-block sb: global -> registers (issued with its
     // first stage) -> LDS (after that stage's MFMAs)
-    constexpr int EJ = (T == kQ4_K) ? 2 * WT * 64 : 0;  // mins-operand pieces
+    constexpr int EJ = has_mins(T) ? 2 * WT * 64 : 0;  // mins-operand pieces
     constexpr int EX = 2 * WT * 2 * 4;                   // token-scale pieces
     uint4 e_meta = make_uint4(0, 0, 0, 0), e_j = make_uint4(0, 0, 0, 0);
     float4 e_x = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -322,9 +350,9 @@ __global__ __launch_bounds__(64 * WT * WR) __attribute__((amdgpu_waves_per_eu(2)
     // no divergent branch, so no wait for all outstanding loads
     auto load_epi = [&](int sb) {
         const size_t r = size_t(min(row0 + tid % RWG, n_out - 1));
-        if constexpr (T == kQ4_K) e_meta = *reinterpret_cast<const uint4*>(W.aux + (r * n_sb + sb) * 16);
+        if constexpr (has_mins(T)) e_meta = *reinterpret_cast<const uint4*>(W.aux + (r * n_sb + sb) * 16);
         else e_meta.x = W.d[r * n_sb + sb];
-        if constexpr (T == kQ4_K)
+        if constexpr (has_mins(T))
             e_j = *reinterpret_cast<const uint4*>(A.gJ + ((size_t(e_tb) * n_sb + sb) * 64 + lane) * 8);
         const int xi = tid % EX, b = xi >> 3, q = xi & 7;  // block of the workgroup, 16-byte piece of its 128 bytes
         const int tbb = min(tok_tile * (2 * WT) + b, A.n_tb - 1);
@@ -332,7 +360,7 @@ __global__ __launch_bounds__(64 * WT * WR) __attribute__((amdgpu_waves_per_eu(2)
     };
     auto store_epi = [&]() {
         s_meta[tid % RWG] = e_meta;
-        if constexpr (T == kQ4_K) s_j[tid % EJ] = e_j;
+        if constexpr (has_mins(T)) s_j[tid % EJ] = e_j;
         s_xd[tid % EX] = e_x;
     };
 
@@ -341,7 +369,7 @@ __global__ __launch_bounds__(64 * WT * WR) __attribute__((amdgpu_waves_per_eu(2)
         float d, dmin = 0.0f;
         v8h bj;
         const uint4 m = s_meta[wr * 32 + l32];
-        if constexpr (T == kQ4_K) {
+        if constexpr (has_mins(T)) {
             d = f16_bits_to_f32(uint16_t(m.x & 0xFFFF));
             dmin = f16_bits_to_f32(uint16_t(m.x >> 16));
             const _Float16 f = half ? _Float16(1.0f) : _Float16(64.0f);
@@ -364,7 +392,7 @@ __global__ __launch_bounds__(64 * WT * WR) __attribute__((amdgpu_waves_per_eu(2)
                 xd[4 * q] = v.x; xd[4 * q + 1] = v.y; xd[4 * q + 2] = v.z; xd[4 * q + 3] = v.w;
             }
             v16f J = v16f{};
-            if constexpr (T == kQ4_K) {
+            if constexpr (has_mins(T)) {
                 const v8h aj = __builtin_bit_cast(v8h, s_j[wb * 64 + lane]);
                 J = __builtin_amdgcn_mfma_f32_32x32x16_f16(aj, bj, v16f{}, 0, 0, 0);
             }
@@ -372,7 +400,7 @@ __global__ __launch_bounds__(64 * WT * WR) __attribute__((amdgpu_waves_per_eu(2)
             for (int i = 0; i < 16; ++i) {
                 const float fi = float((accH[b][i] << SHIFT) + accL[b][i]);
                 float t = d * fi;
-                if constexpr (T == kQ4_K) t = fmaf(-dmin, J[i], t);
+                if constexpr (has_mins(T)) t = fmaf(-dmin, J[i], t);
                 accY[b][i] = fmaf(xd[i], t, accY[b][i]);
             }
             accH[b] = v16i{};
@@ -457,6 +485,7 @@ hipError_t launch_gemm_group(int n, const void* const* ws, const WeightLayout* W
     const ActPtrs A = act_ptrs(act, AL);
     switch (type) {
         case kQ4_K: return gemm_launch<kQ4_K, 2, 2>(G, n_outs, A, n_in, n_tok, s);
+        case kQ5_K: return gemm_launch<kQ5_K, 2, 2>(G, n_outs, A, n_in, n_tok, s);
         // Q6_K (no mins MFMA, heavier dequantization): four token wavefronts share each
         // dequantized stage (measured 8-11 % faster on the 4096 x 14336 down projection)
         case kQ6_K: return gemm_launch<kQ6_K, 4, 1>(G, n_outs, A, n_in, n_tok, s);

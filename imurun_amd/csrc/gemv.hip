@@ -115,12 +115,12 @@ __global__ __launch_bounds__(256) void gemv_kernel(WeightPtrs W, ActPtrs A, int 
     }
 }
 
-// Per-block integers for token 0 of A: Q8_0/Q4_0 one per 32-block; Q4_K two
-// per super-block (sum_g sc_g dot_g, sum_g m_g bsum_g); Q6_K one per super-block.
+// Per-block integers for token 0 of A: Q8_0/Q4_0 one per 32-block; Q4_K / Q5_K
+// two per super-block (sum_g sc_g dot_g, sum_g m_g bsum_g); Q6_K one per super-block.
 template <uint32_t T>
 __global__ void block_ints_kernel(WeightPtrs W, ActPtrs A, int n_in, int n_out, int32_t* __restrict__ out) {
     const long gid = long(blockIdx.x) * blockDim.x + threadIdx.x;
-    constexpr bool kq = (T == kQ4_K || T == kQ6_K);
+    constexpr bool kq = kquant_type(T);
     const int per_row = kq ? n_in / 256 : n_in / 32;
     if (gid >= long(n_out) * per_row) return;
     const int row = int(gid / per_row), b = int(gid % per_row);
@@ -135,14 +135,14 @@ __global__ void block_ints_kernel(WeightPtrs W, ActPtrs A, int n_in, int n_out, 
             const int c = 8 * b + g;
             const Frag f = load_group<T>(W, row, c, n_in);
             const ActFrag a = load_act<T>(A, 0, c, n_in);
-            if constexpr (T == kQ4_K) {
-                sumi += f.sca * dot_q4_k(f.w0, a.a0, a.a1);
+            if constexpr (has_mins(T)) {
+                sumi += f.sca * (T == kQ4_K ? dot_q4_k(f.w0, a.a0, a.a1) : dot_q5_k(f.w0, f.hb, a.a0, a.a1));
                 mins += f.scb * (a.s + a.s2);
             } else {
                 sumi += isum_q6_k(f.w0, f.qh, a.a0, a.a1, a.s, a.s2, f.sca, f.scb);
             }
         }
-        if constexpr (T == kQ4_K) {
+        if constexpr (has_mins(T)) {
             out[2 * gid] = sumi;
             out[2 * gid + 1] = mins;
         } else {
@@ -229,7 +229,7 @@ struct GemvXGroup {
 template <uint32_t T, int LPR, int MAXC, int RB, int XV>
 __global__ __launch_bounds__(64 * kGemvXWaves) void gemv_x_kernel(GemvXGroup G, const float* __restrict__ x,
                                                                   int n_in) {
-    constexpr bool kq = (T == kQ4_K || T == kQ6_K);
+    constexpr bool kq = kquant_type(T);
     constexpr int RPP = 64 / LPR;
     __shared__ uint4 s_codes[2 * kGemvXMaxGroups];  // [half][group]: elements 16 h .. 16 h + 15
     __shared__ float s_d[kGemvXMaxGroups];           // Q8Act d per group / Q8ActK d per super-block
@@ -379,6 +379,7 @@ hipError_t launch_gemv(const void* w, const WeightLayout& WL, const void* act, i
         case kQ8_0: return gemv_pick_nt<kQ8_0>(nt, W, A, WL.n_in, n_out, n_tok, map, yb, y, ldy, s);
         case kQ4_0: return gemv_pick_nt<kQ4_0>(nt, W, A, WL.n_in, n_out, n_tok, map, yb, y, ldy, s);
         case kQ4_K: return gemv_pick_nt<kQ4_K>(nt, W, A, WL.n_in, n_out, n_tok, map, yb, y, ldy, s);
+        case kQ5_K: return gemv_pick_nt<kQ5_K>(nt, W, A, WL.n_in, n_out, n_tok, map, yb, y, ldy, s);
         case kQ6_K: return gemv_pick_nt<kQ6_K>(nt, W, A, WL.n_in, n_out, n_tok, map, yb, y, ldy, s);
         default: return hipErrorInvalidValue;
     }
@@ -396,6 +397,7 @@ hipError_t launch_block_ints(const void* w, const WeightLayout& WL, const void* 
         case kQ8_0: hipLaunchKernelGGL(block_ints_kernel<kQ8_0>, grid, block, 0, s, W, A, WL.n_in, WL.n_out, out); break;
         case kQ4_0: hipLaunchKernelGGL(block_ints_kernel<kQ4_0>, grid, block, 0, s, W, A, WL.n_in, WL.n_out, out); break;
         case kQ4_K: hipLaunchKernelGGL(block_ints_kernel<kQ4_K>, grid, block, 0, s, W, A, WL.n_in, WL.n_out, out); break;
+        case kQ5_K: hipLaunchKernelGGL(block_ints_kernel<kQ5_K>, grid, block, 0, s, W, A, WL.n_in, WL.n_out, out); break;
         case kQ6_K: hipLaunchKernelGGL(block_ints_kernel<kQ6_K>, grid, block, 0, s, W, A, WL.n_in, WL.n_out, out); break;
         default: return hipErrorInvalidValue;
     }
@@ -425,6 +427,7 @@ hipError_t launch_gemv_x(int n, const void* const* ws, const WeightLayout* WLs, 
         case kQ8_0: return gemv_x_pick<kQ8_0>(G, x, WLs[0].n_in, s);
         case kQ4_0: return gemv_x_pick<kQ4_0>(G, x, WLs[0].n_in, s);
         case kQ4_K: return gemv_x_pick<kQ4_K>(G, x, WLs[0].n_in, s);
+        case kQ5_K: return gemv_x_pick<kQ5_K>(G, x, WLs[0].n_in, s);
         case kQ6_K: return gemv_x_pick<kQ6_K>(G, x, WLs[0].n_in, s);
         default: return hipErrorInvalidValue;
     }

@@ -223,7 +223,7 @@ __global__ __launch_bounds__(64 * kMoe1UpWaves) void moe1_gate_up_kernel(
     const float* __restrict__ x, const float* __restrict__ logits, int n_embd, int n_ff, int n_expert, int k,
     int norm, WeightPtrs Wg, WeightPtrs Wu, int wgs_per_slot, MoeRouting r, float* __restrict__ g_out,
     float* __restrict__ u_out, float* __restrict__ h_out) {
-    constexpr bool kq = (T == kQ4_K || T == kQ6_K);
+    constexpr bool kq = kquant_type(T);
     constexpr int RPP = 64 / LPR, TH = 64 * kMoe1UpWaves;
     __shared__ uint4 s_codes[2 * kGemvXMaxGroups];
     __shared__ float s_d[kGemvXMaxGroups];
@@ -349,7 +349,7 @@ __global__ __launch_bounds__(64 * kMoe1DownWaves) void moe1_down_kernel(const fl
                                                                         int n_embd, int n_ff, int k, WeightPtrs Wd,
                                                                         MoeRouting r, float* __restrict__ dn,
                                                                         float* __restrict__ out) {
-    constexpr bool kq = (T == kQ4_K || T == kQ6_K);
+    constexpr bool kq = kquant_type(T);
     constexpr int RPP = 64 / LPR, TH = 64 * kMoe1DownWaves;
     constexpr int R = kMoe1DownWaves / KMAX, ROWS = R * RPP;         // row groups, rows per workgroup
     constexpr int MG = XV > 0 ? XV * TH * 4 / 32 : kMoe1MaxGroups;  // LDS groups
@@ -663,6 +663,7 @@ hipError_t moe1_type(uint32_t t, int n_in, const float* a, const ActPtrs& act, c
         case kQ8_0: return MOE1_TYPE(kQ8_0);
         case kQ4_0: return MOE1_TYPE(kQ4_0);
         case kQ4_K: return MOE1_TYPE(kQ4_K);
+        case kQ5_K: return MOE1_TYPE(kQ5_K);
         case kQ6_K: return MOE1_TYPE(kQ6_K);
         default: return hipErrorInvalidValue;
     }

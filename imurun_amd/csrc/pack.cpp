@@ -1,10 +1,11 @@
 // Host-side block writer: FISH's quantize_row (quantize.cpp:400-416) for the
-// four weight types of this path, used to prepare weights (benchmark inputs,
+// five weight types of this path, used to prepare weights (benchmark inputs,
 // conversion of f32 tensors) before upload. Byte-identical to FISH's packer:
 //   Q8_0  d = f16(amax / 127), q = clamp(round(x / d), -128, 127)     (:118-125)
 //   Q4_0  d = f16(max-magnitude value / -8), q = clamp(round(x/d)+8, 0, 15)  (:141-151)
 //   Q4_K  per 32-group a min/max start and four least-squares refinements of
-//         (scale, offset); 6-bit scales/mins under f16 super-scales (:180-256)
+//   Q5_K  (scale, offset) for codes 0..15 (Q4_K) or 0..31 (Q5_K); 6-bit
+//         scales/mins under f16 super-scales (:189-262)
 //   Q6_K  per 16-group the max-magnitude value to -32 and one least-squares
 //         scale refinement; int8 scales under an f16 super-scale (:301-347)
 // round() is round-half-away-from-zero (std::lround); the f16 encoder rounds
@@ -23,6 +24,7 @@ namespace {
 
 using fishhip::kQ4_0;
 using fishhip::kQ4_K;
+using fishhip::kQ5_K;
 using fishhip::kQ6_K;
 using fishhip::kQ8_0;
 
@@ -82,7 +84,7 @@ void pack_q4_0(const float* x, uint8_t* b) {
 }
 
 // Least-squares fit of x ~ scale * q - m over one 32-group (q in [0, 15]).
-void fit32(const float* x, float& scale, float& m) {
+void fit32(const float* x, int nmax, float& scale, float& m) {
     float lo = 0.0f, hi = x[0];
     for (int i = 0; i < 32; ++i) {
         if (x[i] < lo) lo = x[i];
@@ -93,12 +95,12 @@ void fit32(const float* x, float& scale, float& m) {
         m = -lo;
         return;
     }
-    float s = (hi - lo) / 15.0f, b = lo;
+    float s = (hi - lo) / float(nmax), b = lo;
     for (int it = 0; it < 4; ++it) {
         double cq = 0, cqq = 0, cx = 0, cqx = 0;
         const float inv = 1.0f / s;
         for (int i = 0; i < 32; ++i) {
-            const int q = clampi(iround((x[i] - b) * inv), 0, 15);
+            const int q = clampi(iround((x[i] - b) * inv), 0, nmax);
             cq += q;
             cqq += double(q) * q;
             cx += x[i];
@@ -120,10 +122,12 @@ void fit32(const float* x, float& scale, float& m) {
     m = -b;
 }
 
-void pack_q4_K(const float* x, uint8_t* b) {
+// d, dmin and the 12 scale bytes of a Q4_K / Q5_K super-block (bytes 0..15,
+// the same in both) and its codes q[256] in 0..nmax
+void pack_k45(const float* x, int nmax, uint8_t* b, int* q) {
     float sc[8], mn[8], top_s = 0.0f, top_m = 0.0f;
     for (int g = 0; g < 8; ++g) {
-        fit32(x + 32 * g, sc[g], mn[g]);
+        fit32(x + 32 * g, nmax, sc[g], mn[g]);
         if (top_s < sc[g]) top_s = sc[g];
         if (top_m < mn[g]) top_m = mn[g];
     }
@@ -131,12 +135,12 @@ void pack_q4_K(const float* x, uint8_t* b) {
     put16(b, hd);
     put16(b + 2, hm);
     const float dd = f16_to_f32(hd), dm = f16_to_f32(hm);
-    int ls[8], lm[8], q[256];
+    int ls[8], lm[8];
     for (int g = 0; g < 8; ++g) {
         ls[g] = dd > 0 ? clampi(iround(sc[g] / dd), 0, 63) : 0;
         lm[g] = dm > 0 ? clampi(iround(mn[g] / dm), 0, 63) : 0;
         const float s = dd * float(ls[g]), m = dm * float(lm[g]);
-        for (int i = 0; i < 32; ++i) q[32 * g + i] = s > 0 ? clampi(iround((x[32 * g + i] + m) / s), 0, 15) : 0;
+        for (int i = 0; i < 32; ++i) q[32 * g + i] = s > 0 ? clampi(iround((x[32 * g + i] + m) / s), 0, nmax) : 0;
     }
     uint8_t* s12 = b + 4;
     std::memset(s12, 0, 12);
@@ -150,8 +154,28 @@ void pack_q4_K(const float* x, uint8_t* b) {
             s12[j] |= uint8_t((lm[j] >> 4) << 6);
         }
     }
+}
+
+void pack_q4_K(const float* x, uint8_t* b) {
+    int q[256];
+    pack_k45(x, 15, b, q);
     for (int j = 0; j < 4; ++j)
         for (int l = 0; l < 32; ++l) b[16 + 32 * j + l] = uint8_t(q[64 * j + l] | (q[64 * j + 32 + l] << 4));
+}
+
+// Q5_K: qh[32] at byte 16 (bit g of qh[l]: the fifth bit of element 32 g + l),
+// then Q4_K's nibble layout at byte 48
+void pack_q5_K(const float* x, uint8_t* b) {
+    int q[256];
+    pack_k45(x, 31, b, q);
+    uint8_t* qh = b + 16;
+    std::memset(qh, 0, 32);
+    for (int j = 0; j < 4; ++j)
+        for (int l = 0; l < 32; ++l) {
+            const int lo = q[64 * j + l], hi = q[64 * j + 32 + l];
+            b[48 + 32 * j + l] = uint8_t((lo & 15) | ((hi & 15) << 4));
+            qh[l] = uint8_t(qh[l] | ((lo >> 4) << (2 * j)) | ((hi >> 4) << (2 * j + 1)));
+        }
 }
 
 // Q6_K element e = 128n + 32r + l sits in scale group 8n + l/16 + 2r.
@@ -211,6 +235,7 @@ bool pack_row(uint32_t type, const float* x, uint8_t* dst, int n) {
         case kQ8_0: for (int i = 0; i < n; i += 32, dst += 34) pack_q8_0(x + i, dst); return true;
         case kQ4_0: for (int i = 0; i < n; i += 32, dst += 18) pack_q4_0(x + i, dst); return true;
         case kQ4_K: for (int i = 0; i < n; i += 256, dst += 144) pack_q4_K(x + i, dst); return true;
+        case kQ5_K: for (int i = 0; i < n; i += 256, dst += 176) pack_q5_K(x + i, dst); return true;
         case kQ6_K: for (int i = 0; i < n; i += 256, dst += 210) pack_q6_K(x + i, dst); return true;
         default: return false;
     }
@@ -225,6 +250,7 @@ extern "C" int fish_hip_quantize_rows(uint32_t type, const float* x, void* dst, 
     if (n_threads < 1) n_threads = 1;
     if (n_threads > 64) n_threads = 64;
     uint8_t* out = static_cast<uint8_t*>(dst);
+    if (!pack_row(type, x, out, 0)) return FISH_HIP_ERR_ARG;  // a type without a block writer
     auto work = [&](int r0, int r1) {
         for (int r = r0; r < r1; ++r) pack_row(type, x + size_t(r) * n_in, out + size_t(r) * rb, n_in);
     };

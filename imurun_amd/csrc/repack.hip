@@ -3,7 +3,7 @@
 // fine here because GGUF blocks are only 2-byte aligned.
 //
 // Source layouts: quant.h:28-37 (block structs), quant.cpp:83-90 (Q4_0),
-// :129-133 (Q8_0), :136-163 (Q4_K), :194-216 (Q6_K).
+// :129-133 (Q8_0), :136-163 (Q4_K), :165-192 (Q5_K), :194-216 (Q6_K).
 #include "common.h"
 #include "kernels.h"
 
@@ -15,6 +15,14 @@ __device__ __forceinline__ int q4k_code(const uint8_t* sb, int e) {
     const int g = e >> 5, l = e & 31;
     const uint8_t byte = sb[16 + 32 * (g >> 1) + l];
     return (g & 1) ? (byte >> 4) : (byte & 15);
+}
+
+// Q5_K: the low nibble as Q4_K's (after the 32 qh bytes), fifth bit l of qh[g]
+__device__ __forceinline__ int q5k_code(const uint8_t* sb, int e) {
+    const int g = e >> 5, l = e & 31;
+    const uint8_t byte = sb[48 + 32 * (g >> 1) + l];
+    const int lo = (g & 1) ? (byte >> 4) : (byte & 15);
+    return lo | (((sb[16 + l] >> g) & 1) << 4);
 }
 
 __device__ __forceinline__ int q6k_code(const uint8_t* sb, int e) {
@@ -58,6 +66,24 @@ __global__ void repack_kernel(uint32_t type, const uint8_t* __restrict__ src, in
             const uint8_t* sb = row + size_t(s) * 144;
             for (int l = 0; l < 32; ++l) q[l] = uint8_t(q4k_code(sb, 32 * g + l));
             for (int j = 0; j < 16; ++j) codes[j] = uint8_t(q[j] | (q[j + 16] << 4));
+            if (g == 0) {
+                uint8_t* meta = dst + L.aux + (size_t(r) * (n_in / 256) + s) * 16;
+                for (int k = 0; k < 16; ++k) meta[k] = sb[k];
+            }
+            return;
+        }
+        case kQ5_K: {
+            const int s = c >> 3, g = c & 7;
+            const uint8_t* sb = row + size_t(s) * 176;
+            for (int l = 0; l < 32; ++l) q[l] = uint8_t(q5k_code(sb, 32 * g + l));
+            for (int j = 0; j < 16; ++j) codes[j] = uint8_t((q[j] & 15) | ((q[j + 16] & 15) << 4));
+            uint32_t h = 0;  // bit 8b + k: element 4k + b; bit 8b + 4 + k: element 16 + 4k + b
+            for (int k = 0; k < 4; ++k)
+                for (int b = 0; b < 4; ++b) {
+                    h |= uint32_t(q[4 * k + b] >> 4) << (8 * b + k);
+                    h |= uint32_t(q[16 + 4 * k + b] >> 4) << (8 * b + 4 + k);
+                }
+            *reinterpret_cast<uint32_t*>(dst + L.hb + (size_t(r) * groups + c) * 4) = h;
             if (g == 0) {
                 uint8_t* meta = dst + L.aux + (size_t(r) * (n_in / 256) + s) * 16;
                 for (int k = 0; k < 16; ++k) meta[k] = sb[k];

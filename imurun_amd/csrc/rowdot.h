@@ -15,17 +15,18 @@ struct Frag {
     uint4 w0, w1;   // codes (Q8_0 uses both)
     uint4 meta;     // Q4_K: d, dmin, scales[12]
     uint2 qh;       // Q6_K high bits
+    uint32_t hb;    // Q5_K fifth bits
     uint32_t raw;   // as loaded: f16 d (Q8_0, Q4_0, Q6_K); one Q4_K meta dword (wavefront form)
     uint32_t raw2;  // as loaded: Q6_K's two int8 16-group scales
     float d, dmin;  // f32 weight scales
-    int sca, scb;   // integer group scales (Q4_K: sc, min; Q6_K: two 16-group scales)
+    int sca, scb;   // integer group scales (Q4_K / Q5_K: sc, min; Q6_K: two 16-group scales)
 };
 
 // Loads of one group, with no arithmetic on what they return, so that a
 // caller can issue every load of a wavefront before the first wait (the
 // memory counter is waited on in order: decoding one group right after its
 // load would serialise the loads behind it). finish_group decodes.
-// WAVE (Q4_K only): for wavefront-synchronous callers whose lanes 8j..8j+7
+// WAVE (Q4_K / Q5_K only): for wavefront-synchronous callers whose lanes 8j..8j+7
 // hold the eight groups of one super-block (lane sub takes groups sub,
 // sub + LPR, ... with LPR a multiple of 8): the meta is loaded as one dword
 // per lane and assembled with four shuffles in finish_group, so a wavefront
@@ -42,8 +43,9 @@ __device__ __forceinline__ Frag load_group_raw(const WeightPtrs& W, int row, int
     } else if constexpr (T == kQ4_0) {
         f.w0 = *reinterpret_cast<const uint4*>(W.codes + gi * 16);
         f.raw = W.d[gi];
-    } else if constexpr (T == kQ4_K) {
+    } else if constexpr (has_mins(T)) {
         f.w0 = *reinterpret_cast<const uint4*>(W.codes + gi * 16);
+        if constexpr (T == kQ5_K) f.hb = W.hb[gi];
         const uint8_t* m = W.aux + (size_t(row) * (n_in / 256) + (c >> 3)) * 16;
         if constexpr (WAVE) f.raw = reinterpret_cast<const uint32_t*>(m)[lane & 3];
         else f.meta = *reinterpret_cast<const uint4*>(m);
@@ -62,7 +64,7 @@ template <uint32_t T, bool WAVE>
 __device__ __forceinline__ void finish_group(Frag& f, int c, int lane) {
     if constexpr (T == kQ8_0 || T == kQ4_0) {
         f.d = f16_bits_to_f32(uint16_t(f.raw));
-    } else if constexpr (T == kQ4_K) {
+    } else if constexpr (has_mins(T)) {
         if constexpr (WAVE) {
             const int base = lane & ~7;
             f.meta = make_uint4(__shfl(f.raw, base), __shfl(f.raw, base + 1), __shfl(f.raw, base + 2),
@@ -96,7 +98,7 @@ struct ActFrag {
 template <uint32_t T>
 __device__ __forceinline__ ActFrag load_act(const ActPtrs& A, int t, int c, int n_in) {
     ActFrag a;
-    if constexpr (T == kQ8_0 || T == kQ4_0) {
+    if constexpr (!kquant_type(T)) {
         const uint4* p = reinterpret_cast<const uint4*>(A.q32 + size_t(t) * n_in + size_t(c) * 32);
         a.a0 = p[0];
         a.a1 = p[1];
@@ -123,8 +125,8 @@ __device__ __forceinline__ float group_dot(const Frag& f, const ActFrag& a) {
         return float(isum_q8_0(f.w0, f.w1, a.a0, a.a1)) * (f.d * a.d);
     } else if constexpr (T == kQ4_0) {
         return float(isum_q4_0(f.w0, a.a0, a.a1, a.s)) * (f.d * a.d);
-    } else if constexpr (T == kQ4_K) {
-        const int sumi = f.sca * dot_q4_k(f.w0, a.a0, a.a1);
+    } else if constexpr (has_mins(T)) {
+        const int sumi = f.sca * (T == kQ4_K ? dot_q4_k(f.w0, a.a0, a.a1) : dot_q5_k(f.w0, f.hb, a.a0, a.a1));
         const int mins = f.scb * (a.s + a.s2);
         return a.d * (f.d * float(sumi) - f.dmin * float(mins));
     } else {
@@ -148,7 +150,7 @@ __device__ __forceinline__ ActFrag lds_act(const LdsAct& L, int c) {
     ActFrag a;
     a.a0 = L.codes[c];
     a.a1 = L.codes[L.maxg + c];
-    if constexpr (T == kQ8_0 || T == kQ4_0) {
+    if constexpr (!kquant_type(T)) {
         a.d = L.d[c];
         a.s = L.s[c];
         a.s2 = 0;

@@ -10,7 +10,7 @@
  * Citations are files of the reference repository under model/fish/.
  *
  * Conventions
- *   type       GGUF type id (gguf.h:25-33): 2 Q4_0, 8 Q8_0, 12 Q4_K, 14 Q6_K
+ *   type       GGUF type id (gguf.h:25-33): 2 Q4_0, 8 Q8_0, 12 Q4_K, 13 Q5_K, 14 Q6_K
  *   n_in (K)   reduction length; n_out (N) weight rows; n_tok (M) tokens
  *   y          f32 [n_tok][n_out], row-major (ops.h:78-84)
  *   stream     a hipStream_t passed as void*, NULL = the null stream
@@ -109,7 +109,7 @@ FISH_HIP_API int fish_hip_matmul_tensors(uint32_t type, int n, const void* const
 
 /* The per-block integers of FISH's AVX2 kernels (quant_x86.cpp:280-495) for
  * every row of w against token 0 of act: Q8_0/Q4_0 one int32 per 32-block,
- * Q4_K two per super-block (sum sc*dot, sum m*bsum), Q6_K one per super-block. */
+ * Q4_K / Q5_K two per super-block (sum sc*dot, sum m*bsum), Q6_K one per super-block. */
 FISH_HIP_API int fish_hip_block_ints(uint32_t type, const void* w, const void* act, int n_in, int n_out,
                                      int32_t* out, void* stream);
 

@@ -37,7 +37,7 @@ def test_identity():
     assert L.fish_hip_kernel_name() == b"hip-gfx950"
 
 
-@pytest.mark.parametrize("t", [fh.Q8_0, fh.Q4_0, fh.Q4_K, fh.Q6_K])
+@pytest.mark.parametrize("t", [fh.Q8_0, fh.Q4_0, fh.Q4_K, fh.Q5_K, fh.Q6_K])
 @pytest.mark.parametrize("n_in,n_out", [(4096, 4096), (4096, 14336), (14336, 4096), (768, 2048), (2048, 768)])
 def test_weight_layout_size_matches_gguf(t, n_in, n_out):
     # the repacked copy holds exactly the GGUF bytes plus at most 4 alignment pads
@@ -59,7 +59,9 @@ def test_bad_arguments_return_errors_without_device_work():
     assert L.fish_hip_quantize(None, 1, 4096, None, None, None, None) == -1
     assert "bad arguments" in fh.last_error()
     assert L.fish_hip_matmul(fh.Q4_K, None, None, 1, 4000, 16, None, None) == -1
-    assert L.fish_hip_supports(fh.Q4_K) == 1 and L.fish_hip_supports(3) == 0
+    assert L.fish_hip_supports(fh.Q4_K) == 1 and L.fish_hip_supports(fh.Q5_K) == 1 and L.fish_hip_supports(3) == 0
+    # a type without a block writer is refused
+    assert L.fish_hip_quantize_rows(3, 1 << 20, 1 << 20, 1, 256, 1) == -1
     # moe_ffn: a workspace that is not 256-byte aligned is refused before any device work
     # (the pointers are never dereferenced on this path)
     n_tok, E, F, NE, K = 4, 256, 256, 8, 2
@@ -85,7 +87,7 @@ def test_bad_arguments_return_errors_without_device_work():
     assert "bad arguments" in fh.last_error()
 
 
-@pytest.mark.parametrize("t", [fh.Q8_0, fh.Q4_0, fh.Q4_K, fh.Q6_K])
+@pytest.mark.parametrize("t", [fh.Q8_0, fh.Q4_0, fh.Q4_K, fh.Q5_K, fh.Q6_K])
 def test_block_writer_matches_golden_and_oracle(golden, oracle, t):
     """The library's host packer (input preparation) writes FISH's bytes."""
     g = golden("pack")

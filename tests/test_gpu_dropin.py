@@ -21,7 +21,7 @@ pytestmark = [pytest.mark.gpu,
               pytest.mark.skipif(not DropIn.available(), reason="oracle/_ref/libfishref_hip.so not built")]
 
 TOL = 1e-4
-Q5_K = 13  # a type FISH has and this backend does not take
+F16 = 1  # a weight type FISH multiplies (f32 path) and this backend does not take
 
 
 @pytest.fixture(scope="module")
@@ -44,7 +44,7 @@ def check(got, want, what):
     assert err <= TOL * scale, f"{what}: max err {err:.3e} vs {TOL} * {scale:.3e}"
 
 
-@pytest.mark.parametrize("t", [fh.Q8_0, fh.Q4_0, fh.Q4_K, fh.Q6_K])
+@pytest.mark.parametrize("t", [fh.Q8_0, fh.Q4_0, fh.Q4_K, fh.Q5_K, fh.Q6_K])
 @pytest.mark.parametrize("n_in,n_out", [(1024, 384), (4096, 512)])
 def test_matmul_tensor_through_fish_routing(drop, t, n_in, n_out):
     packed = fh.quantize_rows(t, normal(300 + t + n_in, (n_out, n_in), 0.02))
@@ -89,10 +89,9 @@ def test_matmul_tensors_gate_up_group(drop, t, m):
 
 def test_unsupported_type_stays_on_the_cpu(drop):
     # supports() is false, upload() is never attempted, matmul_tensor takes FISH's CPU path
-    from oracle.oracle import Oracle
     n_in, n_out = 512, 64
-    packed = Oracle().quantize_rows(Q5_K, normal(340, (n_out, n_in), 0.02))
-    h = drop.tensor(Q5_K, packed, n_in, n_out)
+    packed = normal(340, (n_out, n_in), 0.02).astype(np.float16).view(np.uint8).reshape(-1)
+    h = drop.tensor(F16, packed, n_in, n_out)
     try:
         assert not drop.upload(h) and not drop.resident(h)
         x = normal(341, (3, n_in), 1.0)

@@ -230,6 +230,13 @@ def test_moe_decode_hidden_sizes(torch_dev, oracle, n_embd, n_ff, k, types):
     run_case(torch_dev, oracle, 1, n_embd, n_ff, 8, k, types, 6000 + n_ff + k)
 
 
+@pytest.mark.parametrize("n_tok", [1, 20, 160])
+def test_moe_q5_k_experts(torch_dev, oracle, n_tok):
+    """Q5_K gate/up with Q6_K down (a Q5_K_M file's experts): the one-token
+    kernels, the grouped few-token kernel and the grouped GEMM."""
+    run_case(torch_dev, oracle, n_tok, 512, 1024, 8, 2, (fh.Q5_K, fh.Q5_K, fh.Q6_K), 8000 + n_tok)
+
+
 @pytest.mark.parametrize("n_tok,n_expert,k,favour", [(100, 8, 2, 0), (96, 32, 8, 5), (40, 8, 2, 7)])
 def test_moe_skewed_routing(torch_dev, oracle, n_tok, n_expert, k, favour):
     """One expert chosen by every token: its slots span several work-list items

@@ -13,7 +13,8 @@ from imurun_amd.synth import normal, uniform
 pytestmark = pytest.mark.gpu
 
 TOL = 1e-4
-TYPES = [fh.Q8_0, fh.Q4_0, fh.Q4_K, fh.Q6_K]
+TYPES = [fh.Q8_0, fh.Q4_0, fh.Q4_K, fh.Q5_K, fh.Q6_K]
+GOLDEN_TYPES = [fh.Q8_0, fh.Q4_0, fh.Q4_K, fh.Q6_K]  # tests/golden/matmul.npz
 
 
 @pytest.fixture(scope="module")
@@ -47,7 +48,7 @@ def random_rows(t, n_out, n_in, seed):
     sc = sc.reshape(nb, 2)
     d_off = 208 if t == fh.Q6_K else 0
     blocks[:, d_off:d_off + 2] = sc[:, :1].view(np.uint8).reshape(nb, 2)
-    if t == fh.Q4_K:
+    if t in (fh.Q4_K, fh.Q5_K):
         blocks[:, 2:4] = sc[:, 1:].view(np.uint8).reshape(nb, 2)
     return blocks.reshape(-1)
 
@@ -116,7 +117,7 @@ def test_block_ints_bit_exact(torch_dev, oracle, t, n_in, mode):
 @pytest.mark.parametrize("t", TYPES)
 @pytest.mark.parametrize("n_tok", [1, 2, 3, 4, 5, 8, 9, 16, 33, 130])
 def test_matmul_matches_oracle(torch_dev, oracle, t, n_tok):
-    n_in, n_out = (768 if t in (fh.Q4_K, fh.Q6_K) else 736), 96
+    n_in, n_out = (768 if fh.BLOCK_ELEMS[t] == 256 else 736), 96
     rows = packed_weights(oracle, t, n_out, n_in, 300 + n_tok)
     x = normal(400 + n_tok, (n_tok, n_in))
     got = gpu_matmul(torch_dev, t, rows, x, n_out)
@@ -146,7 +147,7 @@ def test_matmul_random_codes(torch_dev, oracle, t):
     check_close(got, want, f"{fh.TYPE_NAMES[t]} random codes")
 
 
-@pytest.mark.parametrize("t", TYPES)
+@pytest.mark.parametrize("t", GOLDEN_TYPES)
 @pytest.mark.parametrize("k", [512, 768])
 def test_matmul_matches_reference_golden(torch_dev, golden, t, k):
     g = golden("matmul")
@@ -165,6 +166,9 @@ def test_matmul_matches_reference_golden(torch_dev, golden, t, k):
     (fh.Q4_0, 14336, 4096, 512),
     (fh.Q4_K, 14336, 4096, 64),
     (fh.Q4_0, 32784, 512, 130),
+    (fh.Q5_K, 14336, 4096, 512),
+    (fh.Q5_K, 4096, 14336, 1),
+    (fh.Q5_K, 14336, 4096, 40),
 ])
 def test_full_size_shapes(torch_dev, oracle, t, n_out, n_in, n_tok):
     """Full-size shapes: all rows on the GPU; a row/token sample checked against
@@ -186,7 +190,8 @@ def test_full_size_shapes(torch_dev, oracle, t, n_out, n_in, n_tok):
     assert np.array_equal(y_part, y[:, :1024])
 
 
-@pytest.mark.parametrize("t,n_tok", [(fh.Q4_K, 130), (fh.Q6_K, 200), (fh.Q4_K, 512), (fh.Q4_K, 3), (fh.Q4_0, 70)])
+@pytest.mark.parametrize("t,n_tok", [(fh.Q4_K, 130), (fh.Q6_K, 200), (fh.Q4_K, 512), (fh.Q4_K, 3), (fh.Q4_0, 70),
+                                     (fh.Q5_K, 130), (fh.Q5_K, 20)])
 def test_matmul_group_matches_single(torch_dev, oracle, t, n_tok):
     """matmul_group over tensors of different heights (one grouped GEMM launch
     for many-token K-quants, per-tensor launches otherwise): every output is
@@ -209,7 +214,7 @@ def test_matmul_group_matches_single(torch_dev, oracle, t, n_tok):
 def test_matmul_tensors_one_token_fused(torch_dev, oracle, t, n_in):
     """One token on f32 input: every workgroup quantizes x itself; the outputs
     are bit-identical to quantize + matmul and close to the oracle."""
-    if t in (fh.Q4_K, fh.Q6_K) and n_in % 256:
+    if fh.BLOCK_ELEMS[t] == 256 and n_in % 256:
         pytest.skip("K-quants need n_in % 256 == 0")
     n_outs = [200, 64]
     rows = [packed_weights(oracle, t, n, n_in, 1400 + i) for i, n in enumerate(n_outs)]
@@ -224,7 +229,7 @@ def test_matmul_tensors_one_token_fused(torch_dev, oracle, t, n_in):
         check_close(got, oracle.matmul_f32(t, r, x, n), f"{fh.TYPE_NAMES[t]} fused K={n_in}")
 
 
-@pytest.mark.parametrize("t", [fh.Q4_0, fh.Q8_0, fh.Q4_K, fh.Q6_K])
+@pytest.mark.parametrize("t", [fh.Q4_0, fh.Q8_0, fh.Q4_K, fh.Q5_K, fh.Q6_K])
 @pytest.mark.parametrize("n_in", [2048, 4096])
 def test_matmul_tensors_one_token_many_rows(torch_dev, oracle, t, n_in):
     """Gate/up-sized row counts (more workgroups than fit on the device at
