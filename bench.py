@@ -229,6 +229,36 @@ def run_kquant_gemv(args, torch, fh, dev, t, name):
             "down_pct_hbm": round(100 * b_dn / dn_us / 1e3 / HBM_PEAK_GBS, 2)}
 
 
+def run_f32path_gemv(args, torch, fh, dev):
+    """Types FISH multiplies in f32: one 14336x4096 (Llama-3-8B gate) matrix at M = 1, GGUF
+    bytes dequantised in the kernel, f32 x; random code bytes with sane scales (the kernel's work
+    does not depend on the values); copies rotated past the MALL."""
+    from imurun_amd.synth import uniform
+    out = {"workload": "14336x4096 GEMV, M=1, f32 x, weights dequantised in-kernel (FISH's f32 path)"}
+    x = torch.randn((1, E), device=dev)
+    y = torch.empty((1, F), dtype=torch.float32, device=dev)
+    for t in (fh.Q4_1, fh.Q5_0, fh.Q3_K, fh.IQ4_NL, fh.MXFP4, fh.F16):
+        nbytes = fh.gguf_row_bytes(t, E) * F
+        raw = (uniform(230 + t, nbytes) * 256).astype(np.uint8)
+        be, bb = fh.BLOCK_ELEMS[t], fh.BLOCK_BYTES[t]
+        blocks = raw.reshape(-1, bb)
+        h = np.array([0.01], np.float16).view(np.uint8)
+        if t == fh.MXFP4:
+            blocks[:, 0] = 127
+        elif t == fh.F16:
+            blocks[:] = h
+        else:  # f16 scale fields set to a sane value
+            off = 108 if t == fh.Q3_K else 0
+            blocks[:, off:off + 2] = h
+        copies = int(2 * MALL_BYTES // nbytes) + 2
+        g = torch.from_numpy(raw).to(dev)
+        ws = [fh.repack(t, g, E, F) for _ in range(copies)]
+        us = graph_time_seq(torch, [lambda w=w: fh.matmul_tensors(t, [w], x, [F], ys=[y]) for w in ws], 20)
+        out[fh.TYPE_NAMES[t]] = {"us": round(us, 2), "gbs": round(nbytes / us / 1e3, 1),
+                                 "pct_hbm": round(100 * nbytes / us / 1e3 / HBM_PEAK_GBS, 2)}
+    return out
+
+
 def run_q5k_prefill(args, torch, fh, dev):
     """Q5_K gate+up (2 x 14336x4096, a Q5_K_M layer's FFN input side) at M = 512 as one
     grouped GEMM launch on activations quantized once; 1024 distinct packed rows repeated."""
@@ -456,6 +486,7 @@ def main() -> int:
         out["q4_k_gemv"] = run_kquant_gemv(args, torch, fh, dev, fh.Q4_K, "Q4_K")
         out["q5_k_gemv"] = run_kquant_gemv(args, torch, fh, dev, fh.Q5_K, "Q5_K")
         out["q6_k_gemv"] = run_kquant_gemv(args, torch, fh, dev, fh.Q6_K, "Q6_K")
+        out["f32_path_gemv"] = run_f32path_gemv(args, torch, fh, dev)
         out["moe_mixtral"] = run_moe(args, torch, fh, dev, "Mixtral-8x7B", 8, 2, 4096, 14336,
                                      (fh.Q4_K, fh.Q4_K, fh.Q4_K), (1, 64))
         out["moe_qwen3"] = run_moe(args, torch, fh, dev, "Qwen3-30B-A3B", 128, 8, 2048, 768,

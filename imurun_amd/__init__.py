@@ -23,9 +23,16 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libfish_hip.so")
 
 Q4_0, Q8_0, Q4_K, Q5_K, Q6_K = 2, 8, 12, 13, 14
-TYPE_NAMES = {Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K"}
-BLOCK_ELEMS = {Q4_0: 32, Q8_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256}
-BLOCK_BYTES = {Q4_0: 18, Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210}
+# types FISH multiplies in f32 (no int8 kernel; kept as GGUF bytes on the device)
+F32, F16, Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, IQ4_NL, BF16, MXFP4 = 0, 1, 3, 6, 7, 10, 11, 20, 30, 39
+F32_PATH_TYPES = (Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, IQ4_NL, MXFP4, F32, F16, BF16)
+TYPE_NAMES = {Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K", F32: "F32", F16: "F16",
+              Q4_1: "Q4_1", Q5_0: "Q5_0", Q5_1: "Q5_1", Q2_K: "Q2_K", Q3_K: "Q3_K", IQ4_NL: "IQ4_NL", BF16: "BF16",
+              MXFP4: "MXFP4"}
+BLOCK_ELEMS = {Q4_0: 32, Q8_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256, F32: 1, F16: 1, BF16: 1, Q4_1: 32, Q5_0: 32,
+               Q5_1: 32, Q2_K: 256, Q3_K: 256, IQ4_NL: 32, MXFP4: 32}
+BLOCK_BYTES = {Q4_0: 18, Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210, F32: 4, F16: 2, BF16: 2, Q4_1: 20, Q5_0: 22,
+               Q5_1: 24, Q2_K: 84, Q3_K: 110, IQ4_NL: 18, MXFP4: 17}
 
 _P = ctypes.c_void_p
 _lib = None
@@ -205,7 +212,8 @@ def matmul_group(t: int, ws, act, n_tok: int, n_in: int, n_outs, ys=None, stream
 
 def matmul_tensors(t: int, ws, x, n_outs, ys=None, act=None, stream=None):
     """f32 x [n_tok, n_in] quantized and multiplied by 1..4 tensors (matmul_tensors / the
-    convenience matmul_batch); one token runs as one fused launch without a workspace."""
+    convenience matmul_batch); one token runs as one fused launch without a workspace.
+    Types FISH multiplies in f32 (F32_PATH_TYPES) take x as it is."""
     import torch
     assert x.is_cuda and x.dtype == torch.float32 and x.dim() == 2 and x.is_contiguous()
     n_tok, n_in = x.shape
@@ -219,7 +227,7 @@ def matmul_tensors(t: int, ws, x, n_outs, ys=None, act=None, stream=None):
         ys = [torch.empty((n_tok, n_out), dtype=torch.float32, device=x.device) for n_out in n_outs]
     for y, n_out in zip(ys, n_outs):
         assert y.numel() >= n_tok * n_out and y.is_contiguous()
-    if act is None and n_tok > 1:
+    if act is None and n_tok > 1 and t not in F32_PATH_TYPES:
         act = torch.empty(act_bytes(n_tok, n_in), dtype=torch.uint8, device=x.device)
     wp = (ctypes.c_void_p * n)(*[w.data_ptr() for w in ws])
     yp = (ctypes.c_void_p * n)(*[y.data_ptr() for y in ys])

@@ -39,8 +39,20 @@ int hip_fail(hipError_t e, const char* what) {
 
 hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
 
-bool type_ok(uint32_t type) {
+// Types with an int8 path (repacked device planes, quantized activations).
+bool int8_type(uint32_t type) {
     return type == kQ8_0 || type == kQ4_0 || type == kQ4_K || type == kQ5_K || type == kQ6_K;
+}
+// Everything the backend multiplies: the int8 types and FISH's f32-path types
+// (kept on the device as their GGUF bytes).
+bool type_ok(uint32_t type) { return int8_type(type) || f32path_type(type); }
+
+// GGUF bytes of an f32-path tensor, 0 when n_in is not whole 32-value sub-blocks
+// (256 for Q2_K / Q3_K) or the type is not an f32-path type.
+size_t f32path_bytes(uint32_t type, int n_in, int n_out) {
+    if (!f32path_type(type) || n_in <= 0 || n_out <= 0 || n_in % 32) return 0;
+    if ((type == kQ2_K || type == kQ3_K) && n_in % 256) return 0;
+    return gguf_row_bytes(type, n_in) * size_t(n_out);
 }
 
 // Matmul dispatch on an already quantized activation buffer: up to
@@ -198,7 +210,15 @@ public:
         std::lock_guard<std::mutex> lk(mu_);
         if (!ensure_init() || !key || !data || !type_ok(type) || n_expert < 1) return false;
         if (map_.count(key)) return true;
-        const WeightLayout L = weight_layout(type, n_in, n_out * n_expert);
+        WeightLayout L = weight_layout(type, n_in, n_out * n_expert);
+        if (f32path_type(type)) {
+            // f32-path types stay in their GGUF bytes
+            L = WeightLayout{};
+            L.type = type;
+            L.n_in = n_in;
+            L.n_out = n_out * n_expert;
+            L.total = f32path_bytes(type, n_in, n_out * n_expert);
+        }
         if (!L.total) return false;
         const size_t src_bytes = gguf_row_bytes(type, n_in) * size_t(n_out) * size_t(n_expert);
         Resident r;
@@ -209,7 +229,10 @@ public:
         if (hipMalloc(&r.dev, L.total) != hipSuccess) { r.dev = nullptr; return false; }
         if (hipMalloc(&staging, src_bytes) != hipSuccess) { (void)hipFree(r.dev); return false; }
         hipError_t e = hipMemcpyAsync(staging, data, src_bytes, hipMemcpyHostToDevice, stream_);
-        if (e == hipSuccess) e = launch_repack(type, staging, n_in, n_out * n_expert, r.dev, stream_);
+        if (e == hipSuccess && f32path_type(type))
+            e = hipMemcpyAsync(r.dev, staging, src_bytes, hipMemcpyDeviceToDevice, stream_);
+        else if (e == hipSuccess)
+            e = launch_repack(type, staging, n_in, n_out * n_expert, r.dev, stream_);
         if (e == hipSuccess) e = hipStreamSynchronize(stream_);
         (void)hipFree(staging);
         if (e != hipSuccess) {
@@ -258,15 +281,19 @@ public:
         }
         const ActLayout AL = act_layout(n_tok, n_in);
         if (!AL.total) return false;
-        for (int i = 0; i < n; ++i)
+        bool any_int8 = false;
+        for (int i = 0; i < n; ++i) {
             if (is_kquant(rs[size_t(i)]->layout.type) && !AL.has256) return false;
+            any_int8 = any_int8 || int8_type(rs[size_t(i)]->layout.type);
+        }
         const size_t x_bytes = size_t(n_tok) * size_t(n_in) * 4;
         if (!reserve(x_bytes, AL.total, y_total * 4)) return false;
         // one token, one type: each workgroup quantizes x itself (one launch)
-        bool fused = n_tok == 1 && n <= kGemmGroupMax && gemv_x_supported(rs[0]->layout);
+        bool fused = n_tok == 1 && n <= kGemmGroupMax && int8_type(rs[0]->layout.type) &&
+                     gemv_x_supported(rs[0]->layout);
         for (int i = 1; i < n && fused; ++i) fused = rs[size_t(i)]->layout.type == rs[0]->layout.type;
         hipError_t e = hipMemcpyAsync(d_x_, x, x_bytes, hipMemcpyHostToDevice, stream_);
-        if (e == hipSuccess && !fused)
+        if (e == hipSuccess && !fused && any_int8)
             e = launch_quantize(static_cast<const float*>(d_x_), n_tok, n_in, n_in, d_act_, nullptr, nullptr, stream_,
                                 planes_for_tokens(n_tok, n_in));
         // y_i at consecutive offsets of the staging buffer; tensors of one
@@ -278,7 +305,7 @@ public:
             dys[size_t(i)] = static_cast<float*>(d_y_) + off;
             off += size_t(n_tok) * size_t(n_outs[i]);
             one_group = one_group && rs[size_t(i)]->layout.type == rs[0]->layout.type &&
-                        uses_gemm(rs[size_t(i)]->layout, n_tok);
+                        int8_type(rs[size_t(i)]->layout.type) && uses_gemm(rs[size_t(i)]->layout, n_tok);
         }
         if (e == hipSuccess && fused) {
             const void* ws[kGemmGroupMax];
@@ -299,9 +326,13 @@ public:
             }
             e = launch_gemm_group(n, ws, Ls, d_act_, n_tok, dys.data(), ldy, stream_);
         } else {
-            for (int i = 0; i < n && e == hipSuccess; ++i)
-                e = dispatch_matmul(rs[size_t(i)]->dev, rs[size_t(i)]->layout, d_act_, n_tok, dys[size_t(i)],
-                                    n_outs[i], stream_);
+            for (int i = 0; i < n && e == hipSuccess; ++i) {
+                const Resident& r = *rs[size_t(i)];
+                e = f32path_type(r.layout.type)
+                        ? launch_dq_matmul(r.layout.type, r.dev, static_cast<const float*>(d_x_), n_tok, n_in,
+                                           n_outs[i], dys[size_t(i)], stream_)
+                        : dispatch_matmul(r.dev, r.layout, d_act_, n_tok, dys[size_t(i)], n_outs[i], stream_);
+            }
         }
         if (e == hipSuccess) e = hipStreamSynchronize(stream_);
         if (e != hipSuccess) {
@@ -381,7 +412,9 @@ int fish_hip_abi_version(void) { return FISH_HIP_ABI_VERSION; }
 const char* fish_hip_kernel_name(void) { return "hip-gfx950"; }
 const char* fish_hip_last_error(void) { return g_err.c_str(); }
 
-uint64_t fish_hip_weight_bytes(uint32_t type, int n_in, int n_out) { return weight_layout(type, n_in, n_out).total; }
+uint64_t fish_hip_weight_bytes(uint32_t type, int n_in, int n_out) {
+    return f32path_type(type) ? f32path_bytes(type, n_in, n_out) : weight_layout(type, n_in, n_out).total;
+}
 uint64_t fish_hip_act_bytes(int n_tok, int n_in) { return act_layout(n_tok, n_in).total; }
 
 int fish_hip_quantize(const float* x, int n_tok, int n_in, void* act, void* q32_fish, void* q256_fish, void* stream) {
@@ -392,6 +425,12 @@ int fish_hip_quantize(const float* x, int n_tok, int n_in, void* act, void* q32_
 }
 
 int fish_hip_repack(uint32_t type, const void* gguf, int n_in, int n_out, void* w, void* stream) {
+    if (f32path_type(type)) {  // kept as GGUF bytes: a device copy
+        const size_t bytes = f32path_bytes(type, n_in, n_out);
+        if (!gguf || !w || !bytes) return fail(FISH_HIP_ERR_ARG, "repack: bad arguments");
+        const hipError_t e = hipMemcpyAsync(w, gguf, bytes, hipMemcpyDeviceToDevice, as_stream(stream));
+        return e == hipSuccess ? 0 : hip_fail(e, "repack");
+    }
     if (!gguf || !w || !weight_layout(type, n_in, n_out).total) return fail(FISH_HIP_ERR_ARG, "repack: bad arguments");
     const hipError_t e = launch_repack(type, gguf, n_in, n_out, w, as_stream(stream));
     return e == hipSuccess ? 0 : hip_fail(e, "repack");
@@ -434,6 +473,17 @@ int fish_hip_matmul_tensors(uint32_t type, int n, const void* const* ws, const f
     if (n <= 0 || n > kGemmGroupMax || !ws || !x || !n_outs || !ys || n_tok <= 0 || n_in <= 0 || n_in % 32)
         return fail(FISH_HIP_ERR_ARG, "matmul_tensors: bad arguments");
     if (is_kquant(type) && n_in % 256) return fail(FISH_HIP_ERR_ARG, "matmul_tensors: K-quant needs n_in % 256 == 0");
+    if (f32path_type(type)) {
+        // FISH's f32 path: dequantised weights times the f32 x, no quantization
+        if (reinterpret_cast<uintptr_t>(x) % 16) return fail(FISH_HIP_ERR_ARG, "matmul_tensors: x not 16-byte aligned");
+        hipError_t e = hipSuccess;
+        for (int i = 0; i < n && e == hipSuccess; ++i) {
+            if (!ws[i] || !ys[i] || !f32path_bytes(type, n_in, n_outs[i]))
+                return fail(FISH_HIP_ERR_ARG, "matmul_tensors: bad tensor");
+            e = launch_dq_matmul(type, ws[i], x, n_tok, n_in, n_outs[i], ys[i], as_stream(stream));
+        }
+        return e == hipSuccess ? 0 : hip_fail(e, "matmul_tensors");
+    }
     WeightLayout L[kGemmGroupMax];
     for (int i = 0; i < n; ++i) {
         L[i] = weight_layout(type, n_in, n_outs[i]);
@@ -475,7 +525,7 @@ int fish_hip_moe_ffn(const float* x, const float* logits, int n_tok, int n_embd,
         return fail(FISH_HIP_ERR_ARG, "moe_ffn: bad arguments");
     if (workspace_bytes < w.total) return fail(FISH_HIP_ERR_ARG, "moe_ffn: workspace too small");
     if (reinterpret_cast<uintptr_t>(workspace) % 256) return fail(FISH_HIP_ERR_ARG, "moe_ffn: workspace not 256-byte aligned");
-    if (!type_ok(t_gate) || !type_ok(t_up) || !type_ok(t_down) ||
+    if (!int8_type(t_gate) || !int8_type(t_up) || !int8_type(t_down) ||
         ((is_kquant(t_gate) || is_kquant(t_up)) && n_embd % 256) || (is_kquant(t_down) && n_ff % 256))
         return fail(FISH_HIP_ERR_ARG, "moe_ffn: unsupported weight type/shape");
     const hipError_t e = moe_ffn(x, logits, n_tok, n_embd, n_ff, n_expert, k, norm, t_gate, w_gate, t_up, w_up,

@@ -43,6 +43,8 @@
 namespace fishhip {
 
 enum : uint32_t { kF32 = 0, kF16 = 1, kQ4_0 = 2, kQ8_0 = 8, kQ4_K = 12, kQ5_K = 13, kQ6_K = 14 };
+// types FISH multiplies in f32 (dequantise, then f32 dot; ops.cpp:219-250)
+enum : uint32_t { kQ4_1 = 3, kQ5_0 = 6, kQ5_1 = 7, kQ2_K = 10, kQ3_K = 11, kIQ4_NL = 20, kBF16 = 30, kMXFP4 = 39 };
 
 // K-quants: 256-value super-blocks, multiplied with the Q8ActK activations.
 constexpr bool kquant_type(uint32_t t) { return t == kQ4_K || t == kQ5_K || t == kQ6_K; }
@@ -113,6 +115,15 @@ inline size_t gguf_row_bytes(uint32_t type, int n_in) {
         case kQ4_K: return size_t(n_in / 256) * 144;
         case kQ5_K: return size_t(n_in / 256) * 176;
         case kQ6_K: return size_t(n_in / 256) * 210;
+        case kF32: return size_t(n_in) * 4;
+        case kF16: case kBF16: return size_t(n_in) * 2;
+        case kQ4_1: return size_t(n_in / 32) * 20;
+        case kQ5_0: return size_t(n_in / 32) * 22;
+        case kQ5_1: return size_t(n_in / 32) * 24;
+        case kIQ4_NL: return size_t(n_in / 32) * 18;
+        case kMXFP4: return size_t(n_in / 32) * 17;
+        case kQ2_K: return size_t(n_in / 256) * 84;
+        case kQ3_K: return size_t(n_in / 256) * 110;
         default: return 0;
     }
 }

@@ -50,6 +50,13 @@ struct MoeRouting {
 hipError_t launch_moe_route(const float* logits, int n_tok, int n_expert, int k, int norm, int item_tokens,
                             const MoeRouting& r, hipStream_t stream);
 
+// matmul_batch's f32 path (ops.cpp:219-250) for the types FISH has no int8
+// kernel for: w = n_out rows of GGUF bytes on the device, x f32 [n_tok][n_in]
+// (16-byte aligned), y f32 [n_tok][n_out]; n_in % 32 == 0 (256 for Q2_K, Q3_K).
+bool f32path_type(uint32_t type);
+hipError_t launch_dq_matmul(uint32_t type, const void* w, const float* x, int n_tok, int n_in, int n_out, float* y,
+                            hipStream_t s);
+
 // logits[t][e] = dot(x[t], w[e]) in f32 over f32 (type 0) or f16 (type 1)
 // router rows (model.cpp:1529); n_embd % 4 == 0, x 16-byte and w 16-byte
 // (f32) or 8-byte (f16) aligned.

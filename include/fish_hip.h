@@ -11,6 +11,11 @@
  *
  * Conventions
  *   type       GGUF type id (gguf.h:25-33): 2 Q4_0, 8 Q8_0, 12 Q4_K, 13 Q5_K, 14 Q6_K
+ *              (int8 path); 0 F32, 1 F16, 3 Q4_1, 6 Q5_0, 7 Q5_1, 10 Q2_K, 11 Q3_K,
+ *              20 IQ4_NL, 30 BF16, 39 MXFP4 (FISH's f32 path, ops.cpp:219-250: the
+ *              device keeps their GGUF bytes; fish_hip_matmul_tensors and the
+ *              backend surface take them, the quantized-activation entry points
+ *              and the expert FFN do not)
  *   n_in (K)   reduction length; n_out (N) weight rows; n_tok (M) tokens
  *   y          f32 [n_tok][n_out], row-major (ops.h:78-84)
  *   stream     a hipStream_t passed as void*, NULL = the null stream
@@ -102,7 +107,11 @@ FISH_HIP_API int fish_hip_matmul_group(uint32_t type, int n, const void* const* 
  * (<= 4) tensors ws[i]. One token with n_in <= 16384 is a single launch in
  * which every workgroup quantizes x itself (no workspace; act_workspace may
  * be NULL); otherwise act_workspace (fish_hip_act_bytes(n_tok, n_in) bytes)
- * receives the quantized activations first. */
+ * receives the quantized activations first. For the f32-path types ws[i] are
+ * GGUF bytes (fish_hip_repack copies them) and x (16-byte aligned) is used as
+ * it is: each weight row is dequantised with FISH's float expressions
+ * (dequant_row, quant.cpp:491-527) and dotted with x in f32, no workspace;
+ * n_in % 32 == 0 (256 for Q2_K, Q3_K). */
 FISH_HIP_API int fish_hip_matmul_tensors(uint32_t type, int n, const void* const* ws, const float* x, int n_tok,
                                          int n_in, const int* n_outs, float* const* ys, void* act_workspace,
                                          uint64_t act_workspace_bytes, void* stream);

@@ -20,6 +20,10 @@
  *   or_vec_dot_q8 / or_matmul_batch  golden per-row dots and matmul outputs.
  *   or_moe_ffn            golden output of a tiny MoE layer composed from the
  *       reference's own primitives in the order of model.cpp:1523-1580.
+ *   or_dequant_row / or_matmul_f32path (Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, IQ4_NL,
+ *       MXFP4, F32, F16, BF16)  golden dequant_row values bit for bit, golden
+ *       one-token matmul_batch outputs bit for bit, more tokens within f32
+ *       rounding, and a float64 dot of the dequantised values.
  *   or_router_logits      golden matmul_batch outputs on f32 / f16 router
  *       rows (to f32 rounding: the reference's installed dot sums in another
  *       order) and a float64 dot of the same operands.
@@ -32,11 +36,22 @@
 #include <stdlib.h>
 #include <string.h>
 
+#define OR_F32 0u
+#define OR_F16 1u
 #define OR_Q4_0 2u
+#define OR_Q4_1 3u
+#define OR_Q5_0 6u
+#define OR_Q5_1 7u
 #define OR_Q8_0 8u
+#define OR_Q2_K 10u
+#define OR_Q3_K 11u
 #define OR_Q4_K 12u
 #define OR_Q5_K 13u
 #define OR_Q6_K 14u
+#define OR_IQ4_NL 20u
+#define OR_IQ4_XS 23u
+#define OR_BF16 30u
+#define OR_MXFP4 39u
 
 /* Byte layouts (model/fish/include/fish/quant.h:28-37, :58-70). */
 #define SZ_Q4_0 18
@@ -44,6 +59,14 @@
 #define SZ_Q4_K 144
 #define SZ_Q5_K 176
 #define SZ_Q6_K 210
+#define SZ_Q4_1 20
+#define SZ_Q5_0 22
+#define SZ_Q5_1 24
+#define SZ_Q2_K 84
+#define SZ_Q3_K 110
+#define SZ_IQ4_NL 18
+#define SZ_IQ4_XS 136
+#define SZ_MXFP4 17
 #define SZ_ACT32 40   /* f32 d; i32 sum; i8 qs[32] */
 #define SZ_ACT256 276 /* f32 d; i16 bsums[8]; i8 qs[256] */
 
@@ -192,16 +215,37 @@ static int q6k_code(const uint8_t* blk, int e, int* slot) {
     return lo | (hi << 4);
 }
 
-static int block_elems(uint32_t t) { return (t == OR_Q4_0 || t == OR_Q8_0) ? 32 : 256; }
+static int block_elems(uint32_t t) {
+    switch (t) {
+        case OR_F32: case OR_F16: case OR_BF16: return 1;
+        case OR_Q4_0: case OR_Q8_0: case OR_Q4_1: case OR_Q5_0: case OR_Q5_1: case OR_IQ4_NL: case OR_MXFP4:
+            return 32;
+        default: return 256;
+    }
+}
 static int block_bytes(uint32_t t) {
     switch (t) {
+        case OR_F32: return 4;
+        case OR_F16: case OR_BF16: return 2;
         case OR_Q4_0: return SZ_Q4_0;
         case OR_Q8_0: return SZ_Q8_0;
         case OR_Q4_K: return SZ_Q4_K;
         case OR_Q5_K: return SZ_Q5_K;
         case OR_Q6_K: return SZ_Q6_K;
+        case OR_Q4_1: return SZ_Q4_1;
+        case OR_Q5_0: return SZ_Q5_0;
+        case OR_Q5_1: return SZ_Q5_1;
+        case OR_Q2_K: return SZ_Q2_K;
+        case OR_Q3_K: return SZ_Q3_K;
+        case OR_IQ4_NL: return SZ_IQ4_NL;
+        case OR_IQ4_XS: return SZ_IQ4_XS;
+        case OR_MXFP4: return SZ_MXFP4;
         default: return 0;
     }
+}
+/* types with an int8 kernel in FISH (quant.cpp:475-481): the rest take the f32 path */
+static int int8_type(uint32_t t) {
+    return t == OR_Q4_0 || t == OR_Q8_0 || t == OR_Q4_K || t == OR_Q5_K || t == OR_Q6_K;
 }
 
 uint64_t or_row_bytes(uint32_t type, uint64_t n) {
@@ -248,6 +292,103 @@ static void deq_block(uint32_t t, const uint8_t* b, float* y) {
                 const int q = q6k_code(b, e, &slot);
                 /* (d * sc) * (q - 32): the float order of quant.cpp:206-209 */
                 y[e] = d * (float)(int8_t)b[192 + slot] * (float)(q - 32);
+            }
+            break;
+        }
+        case OR_F32: memcpy(y, b, 4); break;
+        case OR_F16: y[0] = or_fp16_to_fp32(rd16(b)); break;
+        case OR_BF16: { const uint32_t u = (uint32_t)rd16(b) << 16; memcpy(y, &u, 4); break; }
+        case OR_Q4_1:
+        case OR_Q5_1: {
+            /* d * q + m (quant.cpp:92-100, :115-126); Q5_1's fifth bits after d, m */
+            const float d = or_fp16_to_fp32(rd16(b)), m = or_fp16_to_fp32(rd16(b + 2));
+            const int q5 = t == OR_Q5_1;
+            const uint32_t qh = q5 ? (uint32_t)b[4] | ((uint32_t)b[5] << 8) | ((uint32_t)b[6] << 16) | ((uint32_t)b[7] << 24) : 0;
+            const uint8_t* qs = b + (q5 ? 8 : 4);
+            for (int k = 0; k < 16; ++k) {
+                const int lo = (qs[k] & 15) | (int)(((qh >> k) & 1) << 4), hi = (qs[k] >> 4) | (int)(((qh >> (k + 16)) & 1) << 4);
+                y[k] = d * (float)lo + m;
+                y[k + 16] = d * (float)hi + m;
+            }
+            break;
+        }
+        case OR_Q5_0: {
+            /* d * (q - 16), q = nibble | fifth bit << 4 (quant.cpp:102-113) */
+            const float d = or_fp16_to_fp32(rd16(b));
+            const uint32_t qh = (uint32_t)b[2] | ((uint32_t)b[3] << 8) | ((uint32_t)b[4] << 16) | ((uint32_t)b[5] << 24);
+            for (int k = 0; k < 16; ++k) {
+                const int lo = (b[6 + k] & 15) | (int)(((qh >> k) & 1) << 4), hi = (b[6 + k] >> 4) | (int)(((qh >> (k + 16)) & 1) << 4);
+                y[k] = d * (float)(lo - 16);
+                y[k + 16] = d * (float)(hi - 16);
+            }
+            break;
+        }
+        case OR_Q2_K: {
+            /* scales[16] qs[64] d dmin: element 128 n + 32 j + 16 h + l uses scale byte
+             * 8 n + 2 j + h and bits 2 j of qs[32 n + 16 h + l]; (d * sc) * q - dmin * m
+             * (quant.cpp:218-240) */
+            const float d = or_fp16_to_fp32(rd16(b + 80)), dmin = or_fp16_to_fp32(rd16(b + 82));
+            for (int e = 0; e < 256; ++e) {
+                const int n = e >> 7, j = (e >> 5) & 3, h = (e >> 4) & 1, l = e & 15;
+                const int sc = b[8 * n + 2 * j + h];
+                const int q = (b[16 + 32 * n + 16 * h + l] >> (2 * j)) & 3;
+                y[e] = (d * (float)(sc & 15)) * (float)q - dmin * (float)(sc >> 4);
+            }
+            break;
+        }
+        case OR_Q3_K: {
+            /* hmask[32] qs[64] scales[12] d: 6-bit signed scales (low 4 bits from bytes
+             * 0..7, high 2 bits from bytes 8..11), 2-bit codes minus 4 where the hmask bit
+             * is clear (quant.cpp:242-280) */
+            const float dall = or_fp16_to_fp32(rd16(b + 108));
+            int sc[16];
+            for (int i = 0; i < 16; ++i) {
+                const int lo = (i < 8) ? (b[96 + i] & 15) : (b[96 + i - 8] >> 4);
+                const int hi = (b[104 + (i & 3)] >> (2 * (i >> 2))) & 3;
+                sc[i] = (lo | (hi << 4)) - 32;
+            }
+            for (int e = 0; e < 256; ++e) {
+                const int n = e >> 7, j = (e >> 5) & 3, h = (e >> 4) & 1, l = e & 15;
+                const int idx = 16 * h + l;  /* byte within the 32-byte rows */
+                const int q2 = (b[32 + 32 * n + idx] >> (2 * j)) & 3;
+                const int hm = (b[idx] >> (4 * n + j)) & 1;
+                y[e] = (dall * (float)sc[8 * n + 2 * j + h]) * (float)(q2 - (hm ? 0 : 4));
+            }
+            break;
+        }
+        case OR_IQ4_NL:
+        case OR_IQ4_XS: {
+            /* the non-linear 4-bit codebook (quant.cpp:286-316); IQ4_XS adds 6-bit
+             * per-32 scales minus 32 under d */
+            static const int8_t cb[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+            const float d = or_fp16_to_fp32(rd16(b));
+            if (t == OR_IQ4_NL) {
+                for (int k = 0; k < 16; ++k) {
+                    y[k] = d * (float)cb[b[2 + k] & 15];
+                    y[k + 16] = d * (float)cb[b[2 + k] >> 4];
+                }
+            } else {
+                const uint16_t sh = rd16(b + 2);
+                for (int g = 0; g < 8; ++g) {
+                    const int ls = ((b[4 + g / 2] >> (4 * (g % 2))) & 15) | (((sh >> (2 * g)) & 3) << 4);
+                    const float dl = d * (float)(ls - 32);
+                    const uint8_t* qs = b + 8 + 16 * g;
+                    for (int k = 0; k < 16; ++k) {
+                        y[32 * g + k] = dl * (float)cb[qs[k] & 15];
+                        y[32 * g + 16 + k] = dl * (float)cb[qs[k] >> 4];
+                    }
+                }
+            }
+            break;
+        }
+        case OR_MXFP4: {
+            /* e8m0 scale 2^(e - 127) times signed e2m1 codes (quant.cpp:318-331) */
+            static const float e2m1[8] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f};
+            const float d = ldexpf(1.0f, (int)b[0] - 127);
+            for (int k = 0; k < 16; ++k) {
+                const int lo = b[1 + k] & 15, hi = b[1 + k] >> 4;
+                y[k] = d * ((lo & 8) ? -e2m1[lo & 7] : e2m1[lo & 7]);
+                y[k + 16] = d * ((hi & 8) ? -e2m1[hi & 7] : e2m1[hi & 7]);
             }
             break;
         }
@@ -395,7 +536,7 @@ static void* mm_worker(void* p) {
 int or_matmul_batch(uint32_t type, const void* w, const void* acts32, const void* acts256,
                     int n_tok, int n_in, int n_out, float* y, int n_threads) {
     const int be = block_elems(type);
-    if (!block_bytes(type) || n_in % be || n_tok < 0 || n_out < 0) return 0;
+    if (!int8_type(type) || n_in % be || n_tok < 0 || n_out < 0) return 0;
     const void* acts = (be == 32) ? acts32 : acts256;
     if (!acts) return 0;
     if (n_threads < 1) n_threads = 1;
@@ -424,9 +565,6 @@ int or_matmul_batch(uint32_t type, const void* w, const void* acts32, const void
  * partial sums, a scalar tail into the first, then (s0 + s1) + (s2 + s3). The
  * reference installs an AVX2 dot in its place on x86, which sums in another
  * order, so this agrees with it to f32 rounding only. */
-#define OR_F32 0u
-#define OR_F16 1u
-
 static float dot_f32_scalar(const float* a, const float* b, int n) {
     float s0 = 0, s1 = 0, s2 = 0, s3 = 0;
     int i = 0;
@@ -461,6 +599,41 @@ int or_router_logits(uint32_t type, const void* w, const float* x, int n_tok, in
                 v = dot_f32_scalar(row, xt, n_embd);
             }
             logits[(size_t)t * n_expert + e] = v;
+        }
+    }
+    free(row);
+    return 1;
+}
+
+/* matmul_batch for a weight type without an int8 kernel (ops.cpp:219-250;
+ * Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, IQ4_NL, IQ4_XS, MXFP4, F32, F16, BF16):
+ *   n_tok == 1: vec_dot (quant.cpp:530-572): quantized types dequantise one
+ *       block at a time and add its scalar dot_f32 to a running sum
+ *       (dot_blockwise, quant.cpp:341-353); F16 / BF16 the same over 64-value
+ *       chunks; F32 one dot over the row;
+ *   n_tok > 1: the whole row dequantised once, one dot per token.
+ * Every dot is the scalar dot_f32 of quant.cpp:67-78 (FISH installs an AVX2
+ * dot for the whole-row case, so that agrees to f32 rounding only). */
+int or_matmul_f32path(uint32_t type, const void* w, const float* x, int n_tok, int n_in, int n_out, float* y) {
+    const int be = block_elems(type), bb = block_bytes(type);
+    if (!bb || int8_type(type) || n_in % be || n_tok < 1 || n_out < 0) return 0;
+    const uint64_t rb = (uint64_t)(n_in / be) * (uint64_t)bb;
+    float* row = (float*)malloc(sizeof(float) * (size_t)n_in);
+    if (!row) return 0;
+    const int chunk = (type == OR_F16 || type == OR_BF16) ? 64 : (type == OR_F32 ? n_in : be);
+    for (int i = 0; i < n_out; ++i) {
+        const uint8_t* src = (const uint8_t*)w + (size_t)i * rb;
+        for (int k = 0; k < n_in; k += be) deq_block(type, src + (size_t)(k / be) * bb, row + k);
+        for (int t = 0; t < n_tok; ++t) {
+            const float* xt = x + (size_t)t * n_in;
+            float v;
+            if (n_tok == 1) {
+                v = 0.0f;
+                for (int k = 0; k < n_in; k += chunk) v += dot_f32_scalar(row + k, xt + k, n_in - k < chunk ? n_in - k : chunk);
+            } else {
+                v = dot_f32_scalar(row, xt, n_in);
+            }
+            y[(size_t)t * n_out + i] = v;
         }
     }
     free(row);

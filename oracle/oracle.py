@@ -20,8 +20,15 @@ ORACLE_SO = os.path.join(HERE, "liboracle.so")
 REF_SO = os.path.join(HERE, "_ref", "libfishref.so")
 
 Q4_0, Q8_0, Q4_K, Q5_K, Q6_K = 2, 8, 12, 13, 14
-BLOCK_ELEMS = {Q4_0: 32, Q8_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256}
-BLOCK_BYTES = {Q4_0: 18, Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210}
+# weight types FISH multiplies on its f32 path (no int8 kernel). IQ4_XS has a
+# dequantiser (quant.cpp:299-316) but no entry in FISH's type-size table
+# (gguf.cpp:216-241), so matmul_batch cannot address its rows: not listed.
+F32, F16, Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, IQ4_NL, IQ4_XS, BF16, MXFP4 = 0, 1, 3, 6, 7, 10, 11, 20, 23, 30, 39
+F32_PATH_TYPES = [Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, IQ4_NL, MXFP4, F32, F16, BF16]
+BLOCK_ELEMS = {Q4_0: 32, Q8_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256, Q4_1: 32, Q5_0: 32, Q5_1: 32, Q2_K: 256,
+               Q3_K: 256, IQ4_NL: 32, IQ4_XS: 256, MXFP4: 32, F32: 1, F16: 1, BF16: 1}
+BLOCK_BYTES = {Q4_0: 18, Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210, Q4_1: 20, Q5_0: 22, Q5_1: 24, Q2_K: 84,
+               Q3_K: 110, IQ4_NL: 18, IQ4_XS: 136, MXFP4: 17, F32: 4, F16: 2, BF16: 2}
 ACT32, ACT256 = 40, 276
 
 _P = ctypes.c_void_p
@@ -77,6 +84,7 @@ class Oracle:
                                  ctypes.c_int, ctypes.c_uint32, _P, ctypes.c_uint32, _P, ctypes.c_uint32, _P, _P,
                                  ctypes.c_int]
         L.or_router_logits.argtypes = [ctypes.c_uint32, _P, _P, ctypes.c_int, ctypes.c_int, ctypes.c_int, _P]
+        L.or_matmul_f32path.argtypes = [ctypes.c_uint32, _P, _P, ctypes.c_int, ctypes.c_int, ctypes.c_int, _P]
         self.threads = min(16, os.cpu_count() or 1)
 
     # activations -----------------------------------------------------------
@@ -160,6 +168,15 @@ class Oracle:
         if not self.L.or_router_logits(t, _ptr(w), _ptr(x), n_tok, n_embd, w.shape[0], _ptr(out)):
             raise ValueError("bad router arguments")
         return out
+
+    def matmul_f32path(self, t: int, w: np.ndarray, x: np.ndarray, n_out: int) -> np.ndarray:
+        """matmul_batch on a type without an int8 kernel: y [n_tok][n_out] (ops.cpp:219-250)."""
+        x = np.ascontiguousarray(x, np.float32)
+        y = np.zeros((x.shape[0], n_out), np.float32)
+        if not self.L.or_matmul_f32path(t, _ptr(np.ascontiguousarray(w)), _ptr(x), x.shape[0], x.shape[1], n_out,
+                                        _ptr(y)):
+            raise ValueError("bad f32-path arguments")
+        return y
 
     def silu(self, v: float) -> float:
         return self.L.or_silu(v)

@@ -16,6 +16,9 @@ Fixtures (numpy .npz, no pickles):
               (test/test_kernels.cpp:89-107).
   matmul.npz  ActBatch::quantize + matmul_batch outputs, N=32,
               K in {512, 768}, M in {1, 3, 17}.
+  f32path.npz dequant_row and matmul_batch for the types FISH multiplies in f32
+              (Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, IQ4_NL, MXFP4, F32, F16, BF16):
+              random blocks with sane scales, 8 x 512, M in {1, 3}.
   router.npz  matmul_batch on f32 / f16 router rows (NE=8, K in {256, 992},
               M in {1, 5}).
   moe.npz     a tiny expert layer (NE=4, top-2, E=256, F=256, M=6,
@@ -32,7 +35,9 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.dirname(os.path.dirname(HERE)))
 
 from imurun_amd.synth import normal, uniform  # noqa: E402
-from oracle.oracle import Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, Ref  # noqa: E402
+from oracle.oracle import (BF16, F16, F32, F32_PATH_TYPES, MXFP4, Q2_K, Q3_K, Q4_0, Q4_1, Q4_K, Q5_1,  # noqa: E402
+                           Q5_K, Q6_K, Q8_0, Ref)
+from oracle.oracle import BLOCK_BYTES as OBB, BLOCK_ELEMS as OBE  # noqa: E402
 
 TYPES = [Q8_0, Q4_0, Q4_K, Q5_K, Q6_K]
 D_OFF = {Q4_0: 0, Q8_0: 0, Q4_K: 0, Q5_K: 0, Q6_K: 208}
@@ -70,6 +75,33 @@ def random_row(ref: Ref, t: int, n: int, seed: int, mode: int) -> np.ndarray:
     if t in DMIN_OFF:
         blocks[:, DMIN_OFF[t]:DMIN_OFF[t] + 2] = h[:, 1:2].view(np.uint8).reshape(nb, 2)
     return blocks.reshape(-1).copy()
+
+
+def f32path_rows(t: int, n_out: int, n_in: int, seed: int) -> np.ndarray:
+    """n_out rows of type t: random code bytes, f16 scales in a sane range at each block's scale
+    fields (quant.h:29-41), MXFP4 exponents near 2^0, f32 / f16 / bf16 values ~ N(0, 0.05)."""
+    if t in (F32, F16, BF16):
+        v = normal(seed, (n_out * n_in,), 0.05)
+        if t == F32:
+            return v.view(np.uint8).copy()
+        if t == F16:
+            return v.astype(np.float16).view(np.uint8).copy()
+        return (v.view(np.uint32) >> 16).astype(np.uint16).view(np.uint8).copy()
+    be, bb = OBE[t], OBB[t]
+    nb = n_out * n_in // be
+    blocks = (uniform(seed, nb * bb) * 256).astype(np.uint8).reshape(nb, bb)
+    f16 = lambda s_, lo, hi: (lo + uniform(s_, nb) * (hi - lo)).astype(np.float32).astype(np.float16).view(
+        np.uint8).reshape(nb, 2)  # noqa: E731
+    if t == MXFP4:
+        blocks[:, 0] = (118 + uniform(seed + 1, nb) * 12).astype(np.uint8)
+    else:
+        d_off = {Q2_K: 80, Q3_K: 108}.get(t, 0)
+        blocks[:, d_off:d_off + 2] = f16(seed + 1, 0.001, 0.05)
+        if t in (Q4_1, Q5_1):
+            blocks[:, 2:4] = f16(seed + 2, -0.5, 0.5)
+        if t == Q2_K:
+            blocks[:, 82:84] = f16(seed + 2, 0.001, 0.05)
+    return blocks.reshape(-1)
 
 
 def main() -> None:
@@ -157,6 +189,20 @@ def main() -> None:
             for t in (0, 1):
                 d[f"y{t}_{n}_{m}"] = ref.matmul_f32(t, d[f"w{t}_{n}"], x, 8)
     np.savez_compressed(os.path.join(HERE, "router.npz"), **d)
+    # weight types FISH multiplies on its f32 path: random blocks with sane scale fields,
+    # FISH's dequant_row and its ActBatch + matmul_batch (M = 1: vec_dot; M = 3: dequant_row
+    # + dot_f32_fast), 8 rows of 512
+    d = {}
+    n_in, n_out = 512, 8
+    for t in F32_PATH_TYPES:
+        w = f32path_rows(t, n_out, n_in, 9300 + t)
+        d[f"w_{t}"] = w
+        d[f"deq_{t}"] = ref.dequant_row(t, w, n_out * n_in)
+        for m in (1, 3):
+            x = normal(9400 + t + m, (m, n_in), 1.0)
+            d[f"x_{t}_{m}"] = x
+            d[f"y_{t}_{m}"] = ref.matmul_f32(t, w, x, n_out)
+    np.savez_compressed(os.path.join(HERE, "f32path.npz"), **d)
     for f in sorted(os.listdir(HERE)):
         if f.endswith(".npz"):
             print(f, os.path.getsize(os.path.join(HERE, f)))

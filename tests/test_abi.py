@@ -59,9 +59,15 @@ def test_bad_arguments_return_errors_without_device_work():
     assert L.fish_hip_quantize(None, 1, 4096, None, None, None, None) == -1
     assert "bad arguments" in fh.last_error()
     assert L.fish_hip_matmul(fh.Q4_K, None, None, 1, 4000, 16, None, None) == -1
-    assert L.fish_hip_supports(fh.Q4_K) == 1 and L.fish_hip_supports(fh.Q5_K) == 1 and L.fish_hip_supports(3) == 0
+    assert L.fish_hip_supports(fh.Q4_K) == 1 and L.fish_hip_supports(fh.Q5_K) == 1
+    assert all(L.fish_hip_supports(t) == 1 for t in fh.F32_PATH_TYPES)
+    assert L.fish_hip_supports(9) == 0 and L.fish_hip_supports(23) == 0  # Q8_1, IQ4_XS
     # a type without a block writer is refused
-    assert L.fish_hip_quantize_rows(3, 1 << 20, 1 << 20, 1, 256, 1) == -1
+    assert L.fish_hip_quantize_rows(fh.Q4_1, 1 << 20, 1 << 20, 1, 256, 1) == -1
+    # f32-path types: only fish_hip_matmul_tensors and the backend take them
+    assert L.fish_hip_matmul(fh.Q4_1, 1 << 20, 1 << 20, 1, 256, 16, 1 << 20, None) == -1
+    assert L.fish_hip_weight_bytes(fh.Q4_1, 256, 16) == 16 * 8 * 20
+    assert L.fish_hip_weight_bytes(fh.Q3_K, 128, 16) == 0  # whole 256-value blocks only
     # moe_ffn: a workspace that is not 256-byte aligned is refused before any device work
     # (the pointers are never dereferenced on this path)
     n_tok, E, F, NE, K = 4, 256, 256, 8, 2

@@ -14,14 +14,14 @@ import numpy as np
 import pytest
 
 import imurun_amd as fh
-from imurun_amd.synth import normal
+from imurun_amd.synth import normal, uniform
 from oracle.oracle import DropIn
 
 pytestmark = [pytest.mark.gpu,
               pytest.mark.skipif(not DropIn.available(), reason="oracle/_ref/libfishref_hip.so not built")]
 
 TOL = 1e-4
-F16 = 1  # a weight type FISH multiplies (f32 path) and this backend does not take
+Q8_1 = 9  # a type in FISH's size table that neither FISH's matmul nor this backend multiplies
 
 
 @pytest.fixture(scope="module")
@@ -87,11 +87,30 @@ def test_matmul_tensors_gate_up_group(drop, t, m):
             drop.free(h)
 
 
+@pytest.mark.parametrize("t", [fh.Q4_1, fh.Q3_K, fh.MXFP4, fh.F16])
+def test_f32_path_types_through_fish_routing(drop, t):
+    # types FISH multiplies in f32 go to the device as well (their GGUF bytes, dequantised there)
+    from test_gpu_f32path import rows_of
+    n_in, n_out = 1024, 96
+    h = drop.tensor(t, rows_of(t, n_out, n_in, 350 + t), n_in, n_out)
+    try:
+        assert drop.upload(h) and drop.resident(h)
+        for m in (1, 7):
+            x = normal(351 + m, (m, n_in), 1.0)
+            n0 = served()
+            y = drop.matmul_tensor(h, x)
+            assert served() == n0 + 1
+            check(y, drop.matmul_cpu(h, x), f"{fh.TYPE_NAMES[t]} M={m}")
+        drop.release(h)
+    finally:
+        drop.free(h)
+
+
 def test_unsupported_type_stays_on_the_cpu(drop):
     # supports() is false, upload() is never attempted, matmul_tensor takes FISH's CPU path
     n_in, n_out = 512, 64
-    packed = normal(340, (n_out, n_in), 0.02).astype(np.float16).view(np.uint8).reshape(-1)
-    h = drop.tensor(F16, packed, n_in, n_out)
+    packed = (uniform(340, n_out * n_in // 32 * 36) * 256).astype(np.uint8)
+    h = drop.tensor(Q8_1, packed, n_in, n_out)
     try:
         assert not drop.upload(h) and not drop.resident(h)
         x = normal(341, (3, n_in), 1.0)

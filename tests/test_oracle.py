@@ -13,7 +13,7 @@ import pytest
 
 import fishref_np as F
 from imurun_amd.synth import normal
-from oracle.oracle import Q4_0, Q4_K, Q5_K, Q6_K, Q8_0
+from oracle.oracle import F32, F32_PATH_TYPES, Q4_0, Q4_1, Q4_K, Q5_K, Q6_K, Q8_0
 
 TYPES = [Q8_0, Q4_0, Q4_K, Q5_K, Q6_K]
 
@@ -187,3 +187,33 @@ def test_router_catches_a_dropped_term(oracle):
     assert np.any(np.abs(got - dropped) > 1e-6 * bound)
     shifted = x.astype(np.float64) @ np.roll(w, 1, axis=0).astype(np.float64).T
     assert np.all(np.abs(got - shifted) > 1e-6 * bound)
+
+
+@pytest.mark.parametrize("t", F32_PATH_TYPES)
+def test_f32path_dequant_and_matmul_golden(oracle, golden, t):
+    """Types FISH multiplies in f32: dequantised values bit-identical to FISH's
+    dequant_row; one token bit-identical to vec_dot (scalar block dots; F32 rows
+    go through FISH's AVX2 dot); more tokens within f32 rounding of the AVX2 dot."""
+    g = golden("f32path")
+    w = g[f"w_{t}"]
+    n_out, n_in = 8, 512
+    deq = oracle.dequant_row(t, w, n_out * n_in)
+    assert np.array_equal(deq.view(np.uint32), g[f"deq_{t}"].view(np.uint32))
+    for m in (1, 3):
+        x = g[f"x_{t}_{m}"]
+        got = oracle.matmul_f32path(t, w, x, n_out)
+        want = g[f"y_{t}_{m}"]
+        if m == 1 and t != F32:
+            assert np.array_equal(got, want)
+        bound = np.abs(x.astype(np.float64)) @ np.abs(deq.reshape(n_out, n_in).astype(np.float64)).T
+        assert np.all(np.abs(got - want) <= 1e-6 * bound)
+        exact = x.astype(np.float64) @ deq.reshape(n_out, n_in).astype(np.float64).T
+        assert np.all(np.abs(got - exact) <= 1e-6 * bound)
+
+
+def test_int8_matmul_refuses_f32_path_types(oracle):
+    # FISH never gives these types to its int8 kernels (quant.cpp:475-481)
+    x = np.zeros((1, 256), np.float32)
+    q32, q256 = oracle.act_batch(x)
+    with pytest.raises(ValueError):
+        oracle.matmul(Q4_1, np.zeros(20 * 8, np.uint8), q32, q256, 1, 256, 1)
