@@ -25,7 +25,7 @@
 //   gX   [M'/32][K/256][2][16] f32: Q8ActK d in the order of that MFMA's
 //        output registers: [h][i] is token 8 (i / 4) + 4 h + i % 4 of the block
 //   gJ   [M'/32][K/256][64][8] f16: A operands of v_mfma_f32_32x32x16_f16
-//        for the Q4_K mins term: lane l < 32 holds bsum_g >> 6 of token l,
+//        for the Q4_K / Q5_K mins term: lane l < 32 holds 64 (bsum_g >> 6) of token l,
 //        lane 32 + l holds bsum_g & 63, g = 0..7
 // (bsum_g = the Q8ActK per-32 sum; s16 holds per-16 sums, two of which make
 // a bsum; M' = M rounded up to a multiple of 32, the extra tokens all zero).

@@ -15,8 +15,8 @@
 //         -- one packed 16-bit multiply makes four bytes of a plane;
 //   Q6_K  w' = sc * (q - 32) = 64 hi + lo (0 <= lo < 64): I = 64 H + L;
 //   Q5_K  w' = sc * q (<= 1953) = 64 hi + lo the same way.
-// J is exact on one f16 MFMA per super-block: A = (bsum >> 6, bsum & 63) per
-// token (written by the quantizer), B = (64 m_g, m_g) per row, all small
+// J is exact on one f16 MFMA per super-block: A = (64 (bsum >> 6), bsum & 63)
+// per token (written by the quantizer), B = (m_g, m_g) per row, all small
 // integers, so every product and sum is exact in f32.
 //
 // Tiling: a workgroup of WT x WR wavefronts owns 64 WT tokens x 32 WR rows;
@@ -372,12 +372,13 @@ __global__ __launch_bounds__(64 * WT * WR) __attribute__((amdgpu_waves_per_eu(2)
         if constexpr (has_mins(T)) {
             d = f16_bits_to_f32(uint16_t(m.x & 0xFFFF));
             dmin = f16_bits_to_f32(uint16_t(m.x >> 16));
-            const _Float16 f = half ? _Float16(1.0f) : _Float16(64.0f);
+            // the eight 6-bit mins, four per dword (quant.cpp:136-144 packing)
+            const uint32_t mn_lo = m.z & 0x3F3F3F3Fu;
+            const uint32_t mn_hi = ((m.w >> 4) & 0x0F0F0F0Fu) | ((m.z >> 2) & 0x30303030u);
 #pragma unroll
-            for (int g = 0; g < 8; ++g) {
-                int scv, mn;
-                k4_scale_min(m.y, m.z, m.w, g, scv, mn);
-                bj[g] = _Float16(float(mn)) * f;
+            for (int g = 0; g < 4; ++g) {
+                bj[g] = _Float16(float((mn_lo >> (8 * g)) & 0xFF));
+                bj[4 + g] = _Float16(float((mn_hi >> (8 * g)) & 0xFF));
             }
         } else {
             d = f16_bits_to_f32(uint16_t(m.x));

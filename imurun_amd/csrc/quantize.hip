@@ -116,7 +116,8 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float* __restrict__
             if (lane == 0) o.gX[(blk * 2 + ((tt >> 2) & 1)) * 16 + (tt >> 3) * 4 + (tt & 3)] = d;
             if ((lane & 7) == 0) {
                 const int g = lane >> 3;
-                o.gJ[(blk * 64 + tt) * 8 + g] = __builtin_bit_cast(uint16_t, _Float16(float(g32 >> 6)));
+                // 64 (bsum >> 6): a multiple of 64 of magnitude <= 4096, exact in f16
+                o.gJ[(blk * 64 + tt) * 8 + g] = __builtin_bit_cast(uint16_t, _Float16(float((g32 >> 6) * 64)));
                 o.gJ[(blk * 64 + 32 + tt) * 8 + g] = __builtin_bit_cast(uint16_t, _Float16(float(g32 & 63)));
             }
         }
