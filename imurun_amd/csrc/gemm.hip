@@ -19,8 +19,10 @@
 // per token (written by the quantizer), B = (m_g, m_g) per row, all small
 // integers, so every product and sum is exact in f32.
 //
-// Tiling: a workgroup of WT x WR wavefronts owns 64 WT tokens x 32 WR rows;
-// a wavefront owns 64 tokens x 32 rows (two 32x32 blocks). The weight planes
+// Tiling: a wavefront owns TPW x RPW 32x32 blocks (tokens x rows), a
+// workgroup WT x WR wavefronts; Q4_K / Q5_K use four wavefronts of 32 tokens
+// x 64 rows (no activation operand is fetched by two wavefronts of a
+// workgroup), Q6_K four of 64 tokens x 32 rows. The weight planes
 // of a 128-value stage are dequantised once per workgroup into a three-deep
 // LDS ring (one barrier per stage); activations go straight from HBM/L2 into
 // the A-operand registers (the quantizer writes them in operand order), one
@@ -195,21 +197,24 @@ __device__ __forceinline__ void dequant_part(const Raw& r, const DqPrep& p, int 
     }
 }
 
-template <uint32_t T, int WT, int WR>
+// A wavefront owns TPW 32-token blocks x RPW 32-row blocks; a workgroup WT x WR
+// wavefronts (32 TPW WT tokens x 32 RPW WR rows).
+template <uint32_t T, int WT, int WR, int TPW, int RPW>
 __global__ __launch_bounds__(64 * WT * WR) __attribute__((amdgpu_waves_per_eu(2))) void gemm_kq_kernel(
     GemmGroup G, ActPtrs A, int n_in, int n_tok, int tok_tiles) {
     constexpr int NW = WT * WR;
-    constexpr int RWG = 32 * WR;                      // rows per workgroup
+    constexpr int RWG = 32 * RPW * WR;                // rows per workgroup
+    constexpr int TBW = TPW * WT;                     // 32-token blocks per workgroup
     constexpr int ITEMS = RWG * SSTEPS;               // (row, step) items per stage
     constexpr int IPT = (ITEMS + 64 * NW - 1) / (64 * NW);
     constexpr int SHIFT = (T == kQ4_K) ? 3 : 6;  // I = 8 H + L (Q4_K) or 64 H + L
     // [stage][plane][step][half][row] of 16-byte pieces
     __shared__ uint4 s_b[RING * 2 * SSTEPS * 2 * RWG];
     // per super-block epilogue data, loaded during its first stage:
-    // row meta (Q4_K d, dmin, scales; Q6_K d in .x), token scales, mins operands
+    // row meta (Q4_K / Q5_K d, dmin, scales; Q6_K d in .x), token scales, mins operands
     __shared__ uint4 s_meta[RWG];
-    __shared__ float4 s_xd[2 * WT * 2 * 4];
-    __shared__ uint4 s_j[has_mins(T) ? 2 * WT * 64 : 1];
+    __shared__ float4 s_xd[TBW * 2 * 4];
+    __shared__ uint4 s_j[has_mins(T) ? TBW * 64 : 1];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int l32 = lane & 31, half = lane >> 5;
@@ -234,11 +239,11 @@ __global__ __launch_bounds__(64 * WT * WR) __attribute__((amdgpu_waves_per_eu(2)
     const int row0 = row_tile * RWG;
 
     const int steps = n_in / 32, stages = steps / SSTEPS, n_sb = n_in / 256;
-    const int tb0 = tok_tile * (2 * WT) + wt * 2;    // first 32-token block of the wavefront
-    int tb[2];
-    tb[0] = min(tb0, A.n_tb - 1);
-    tb[1] = min(tb0 + 1, A.n_tb - 1);
-    const int my_row = row0 + wr * 32 + l32;         // the lane's output row
+    const int tb0 = tok_tile * TBW + wt * TPW;       // first 32-token block of the wavefront
+    int tb[TPW];
+#pragma unroll
+    for (int b = 0; b < TPW; ++b) tb[b] = min(tb0 + b, A.n_tb - 1);
+    const int wrow = wr * 32 * RPW + l32;            // the lane's row in the workgroup (block 0)
 
     // dequantisation items of this thread: item = tid + 64 NW j -> (row, step)
     int it_row[IPT], it_step[IPT];
@@ -276,53 +281,65 @@ __global__ __launch_bounds__(64 * WT * WR) __attribute__((amdgpu_waves_per_eu(2)
     // A operand of (block b, step s of a stage): 1 KB pieces, lane-contiguous;
     // a uniform stage base plus a per-lane offset and an immediate
     const uint4* gA = reinterpret_cast<const uint4*>(A.gA);
-    int a_off[2];
+    int a_off[TPW];
 #pragma unroll
-    for (int b = 0; b < 2; ++b) a_off[b] = tb[b] * steps * 64 + lane;
-    auto load_a = [&](v4i (&a)[2][SSTEPS], int stage) {
+    for (int b = 0; b < TPW; ++b) a_off[b] = tb[b] * steps * 64 + lane;
+    auto load_a = [&](v4i (&a)[TPW][SSTEPS], int stage) {
         const uint4* base = gA + size_t(stage) * (SSTEPS * 64);
 #pragma unroll
-        for (int b = 0; b < 2; ++b)
+        for (int b = 0; b < TPW; ++b)
 #pragma unroll
             for (int s = 0; s < SSTEPS; ++s) a[b][s] = __builtin_bit_cast(v4i, base[a_off[b] + s * 64]);
     };
 
-    v16i accH[2], accL[2];
-    v16f accY[2];
+    v16i accH[TPW][RPW], accL[TPW][RPW];
+    v16f accY[TPW][RPW];
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
-        accH[b] = v16i{};
-        accL[b] = v16i{};
-        accY[b] = v16f{};
-    }
+    for (int b = 0; b < TPW; ++b)
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) {
+            accH[b][r] = v16i{};
+            accL[b][r] = v16i{};
+            accY[b][r] = v16f{};
+        }
 
-    // MFMAs of one stage; each step's A registers are refilled with the same
-    // step of stage `next` as soon as its MFMAs are issued (one A buffer)
     // MFMAs of one stage from LDS slot `slot`; each step's A registers are
     // refilled with the same step of stage `next` as soon as its MFMAs are
     // issued (one A buffer), the next step's weight operands are read from LDS
     // before the current step's MFMAs, and the dequantisation of `raw` (stage
     // dq_stage) into slot dq_slot is spread over the steps so the wavefront has
     // VALU work between its MFMAs.
-    auto compute_stage = [&](v4i (&a)[2][SSTEPS], int slot, int next, const Raw (&raw)[IPT], int dq_stage,
+    auto compute_stage = [&](v4i (&a)[TPW][SSTEPS], int slot, int next, const Raw (&raw)[IPT], int dq_stage,
                              int dq_slot) {
         const uint4* base = gA + size_t(next) * (SSTEPS * 64);
         DqPrep prep[IPT];
 #pragma unroll
         for (int j = 0; j < IPT; ++j) prep[j] = dequant_prep<T>(raw[j], dq_stage * SSTEPS + it_step[j]);
-        v4i bh = __builtin_bit_cast(v4i, s_b[lds_at(slot, 0, 0, half, wr * 32 + l32)]);
-        v4i bl = __builtin_bit_cast(v4i, s_b[lds_at(slot, 1, 0, half, wr * 32 + l32)]);
+        v4i bh[RPW], bl[RPW];
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) {
+            bh[r] = __builtin_bit_cast(v4i, s_b[lds_at(slot, 0, 0, half, wrow + 32 * r)]);
+            bl[r] = __builtin_bit_cast(v4i, s_b[lds_at(slot, 1, 0, half, wrow + 32 * r)]);
+        }
 #pragma unroll
         for (int s = 0; s < SSTEPS; ++s) {
-            v4i nbh = bh, nbl = bl;
-            if (s + 1 < SSTEPS) {
-                nbh = __builtin_bit_cast(v4i, s_b[lds_at(slot, 0, s + 1, half, wr * 32 + l32)]);
-                nbl = __builtin_bit_cast(v4i, s_b[lds_at(slot, 1, s + 1, half, wr * 32 + l32)]);
+            v4i nbh[RPW], nbl[RPW];
+#pragma unroll
+            for (int r = 0; r < RPW; ++r) {
+                nbh[r] = bh[r];
+                nbl[r] = bl[r];
+                if (s + 1 < SSTEPS) {
+                    nbh[r] = __builtin_bit_cast(v4i, s_b[lds_at(slot, 0, s + 1, half, wrow + 32 * r)]);
+                    nbl[r] = __builtin_bit_cast(v4i, s_b[lds_at(slot, 1, s + 1, half, wrow + 32 * r)]);
+                }
             }
 #pragma unroll
-            for (int b = 0; b < 2; ++b) {
-                accH[b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[b][s], bh, accH[b], 0, 0, 0);
-                accL[b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[b][s], bl, accL[b], 0, 0, 0);
+            for (int b = 0; b < TPW; ++b) {
+#pragma unroll
+                for (int r = 0; r < RPW; ++r) {
+                    accH[b][r] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[b][s], bh[r], accH[b][r], 0, 0, 0);
+                    accL[b][r] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[b][s], bl[r], accL[b][r], 0, 0, 0);
+                }
                 a[b][s] = __builtin_bit_cast(v4i, base[a_off[b] + s * 64]);
             }
 #pragma unroll
@@ -334,18 +351,21 @@ __global__ __launch_bounds__(64 * WT * WR) __attribute__((amdgpu_waves_per_eu(2)
                     s_b[lds_at(dq_slot, plane, it_step[j], h, it_row[j])] = v;
                 });
             }
-            bh = nbh;
-            bl = nbl;
+#pragma unroll
+            for (int r = 0; r < RPW; ++r) {
+                bh[r] = nbh[r];
+                bl[r] = nbl[r];
+            }
         }
     };
 
     // epilogue data of super-block sb: global -> registers (issued with its
     // first stage) -> LDS (after that stage's MFMAs)
-    constexpr int EJ = has_mins(T) ? 2 * WT * 64 : 0;  // mins-operand pieces
-    constexpr int EX = 2 * WT * 2 * 4;                   // token-scale pieces
+    constexpr int EJ = has_mins(T) ? TBW * 64 : 0;  // mins-operand pieces
+    constexpr int EX = TBW * 2 * 4;                 // token-scale pieces
     uint4 e_meta = make_uint4(0, 0, 0, 0), e_j = make_uint4(0, 0, 0, 0);
     float4 e_x = make_float4(0.f, 0.f, 0.f, 0.f);
-    const int e_tb = min(tok_tile * (2 * WT) + (tid >> 6) % (2 * WT), A.n_tb - 1);
+    const int e_tb = min(tok_tile * TBW + (tid >> 6) % TBW, A.n_tb - 1);
     // every thread loads and stores (duplicate copies of the same values):
     // no divergent branch, so no wait for all outstanding loads
     auto load_epi = [&](int sb) {
@@ -355,7 +375,7 @@ __global__ __launch_bounds__(64 * WT * WR) __attribute__((amdgpu_waves_per_eu(2)
         if constexpr (has_mins(T))
             e_j = *reinterpret_cast<const uint4*>(A.gJ + ((size_t(e_tb) * n_sb + sb) * 64 + lane) * 8);
         const int xi = tid % EX, b = xi >> 3, q = xi & 7;  // block of the workgroup, 16-byte piece of its 128 bytes
-        const int tbb = min(tok_tile * (2 * WT) + b, A.n_tb - 1);
+        const int tbb = min(tok_tile * TBW + b, A.n_tb - 1);
         e_x = reinterpret_cast<const float4*>(A.gX + (size_t(tbb) * n_sb + sb) * 32)[q];
     };
     auto store_epi = [&]() {
@@ -366,46 +386,55 @@ __global__ __launch_bounds__(64 * WT * WR) __attribute__((amdgpu_waves_per_eu(2)
 
     // super-block epilogue: y += xd * (d * I - dmin * J)   (Q6_K: y += xd * (d * I))
     auto epilogue = [&]() {
-        float d, dmin = 0.0f;
-        v8h bj;
-        const uint4 m = s_meta[wr * 32 + l32];
-        if constexpr (has_mins(T)) {
-            d = f16_bits_to_f32(uint16_t(m.x & 0xFFFF));
-            dmin = f16_bits_to_f32(uint16_t(m.x >> 16));
-            // the eight 6-bit mins, four per dword (quant.cpp:136-144 packing)
-            const uint32_t mn_lo = m.z & 0x3F3F3F3Fu;
-            const uint32_t mn_hi = ((m.w >> 4) & 0x0F0F0F0Fu) | ((m.z >> 2) & 0x30303030u);
+        float d[RPW], dmin[RPW];
+        v8h bj[RPW];
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                bj[g] = _Float16(float((mn_lo >> (8 * g)) & 0xFF));
-                bj[4 + g] = _Float16(float((mn_hi >> (8 * g)) & 0xFF));
+        for (int r = 0; r < RPW; ++r) {
+            const uint4 m = s_meta[wrow + 32 * r];
+            dmin[r] = 0.0f;
+            if constexpr (has_mins(T)) {
+                d[r] = f16_bits_to_f32(uint16_t(m.x & 0xFFFF));
+                dmin[r] = f16_bits_to_f32(uint16_t(m.x >> 16));
+                // the eight 6-bit mins, four per dword (quant.cpp:136-144 packing)
+                const uint32_t mn_lo = m.z & 0x3F3F3F3Fu;
+                const uint32_t mn_hi = ((m.w >> 4) & 0x0F0F0F0Fu) | ((m.z >> 2) & 0x30303030u);
+                v8h v;
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    v[g] = _Float16(float((mn_lo >> (8 * g)) & 0xFF));
+                    v[4 + g] = _Float16(float((mn_hi >> (8 * g)) & 0xFF));
+                }
+                bj[r] = v;
+            } else {
+                d[r] = f16_bits_to_f32(uint16_t(m.x));
             }
-        } else {
-            d = f16_bits_to_f32(uint16_t(m.x));
         }
 #pragma unroll
-        for (int b = 0; b < 2; ++b) {
-            const int wb = wt * 2 + b;  // block index within the workgroup
+        for (int b = 0; b < TPW; ++b) {
+            const int wb = wt * TPW + b;  // block index within the workgroup
             float xd[16];
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const float4 v = s_xd[wb * 8 + half * 4 + q];
                 xd[4 * q] = v.x; xd[4 * q + 1] = v.y; xd[4 * q + 2] = v.z; xd[4 * q + 3] = v.w;
             }
-            v16f J = v16f{};
-            if constexpr (has_mins(T)) {
-                const v8h aj = __builtin_bit_cast(v8h, s_j[wb * 64 + lane]);
-                J = __builtin_amdgcn_mfma_f32_32x32x16_f16(aj, bj, v16f{}, 0, 0, 0);
-            }
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const float fi = float((accH[b][i] << SHIFT) + accL[b][i]);
-                float t = d * fi;
-                if constexpr (has_mins(T)) t = fmaf(-dmin, J[i], t);
-                accY[b][i] = fmaf(xd[i], t, accY[b][i]);
+            for (int r = 0; r < RPW; ++r) {
+                v16f J = v16f{};
+                if constexpr (has_mins(T)) {
+                    const v8h aj = __builtin_bit_cast(v8h, s_j[wb * 64 + lane]);
+                    J = __builtin_amdgcn_mfma_f32_32x32x16_f16(aj, bj[r], v16f{}, 0, 0, 0);
+                }
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const float fi = float((accH[b][r][i] << SHIFT) + accL[b][r][i]);
+                    float t = d[r] * fi;
+                    if constexpr (has_mins(T)) t = fmaf(-dmin[r], J[i], t);
+                    accY[b][r][i] = fmaf(xd[i], t, accY[b][r][i]);
+                }
+                accH[b][r] = v16i{};
+                accL[b][r] = v16i{};
             }
-            accH[b] = v16i{};
-            accL[b] = v16i{};
         }
     };
 
@@ -416,7 +445,7 @@ __global__ __launch_bounds__(64 * WT * WR) __attribute__((amdgpu_waves_per_eu(2)
     store_stage(raw0, 0, 0);
     store_stage(raw1, 1, 1);
     load_stage(raw0, min(2, stages - 1));
-    v4i a0[2][SSTEPS];
+    v4i a0[TPW][SSTEPS];
     load_a(a0, 0);
 
     // ---- main loop, one super-block (two stages) per iteration; stage i
@@ -439,28 +468,31 @@ __global__ __launch_bounds__(64 * WT * WR) __attribute__((amdgpu_waves_per_eu(2)
         epilogue();
     }
 
-    // ---- store: lane owns row my_row, register i of block b is token 8 (i / 4) + 4 half + i % 4
-    if (my_row < n_out) {
+    // ---- store: lane owns row block r's row, register i of token block b is token 8 (i / 4) + 4 half + i % 4
 #pragma unroll
-        for (int b = 0; b < 2; ++b)
+    for (int r = 0; r < RPW; ++r) {
+        const int my_row = row0 + wrow + 32 * r;
+        if (my_row >= n_out) continue;
+#pragma unroll
+        for (int b = 0; b < TPW; ++b)
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 const int t = (tb0 + b) * 32 + 8 * (i >> 2) + 4 * half + (i & 3);
-                if (t < n_tok) y[size_t(t) * ldy + my_row] = accY[b][i];
+                if (t < n_tok) y[size_t(t) * ldy + my_row] = accY[b][r][i];
             }
     }
 }
 
-template <uint32_t T, int WT, int WR>
+template <uint32_t T, int WT, int WR, int TPW, int RPW>
 hipError_t gemm_launch(GemmGroup G, const int* n_outs, const ActPtrs& A, int n_in, int n_tok, hipStream_t s) {
     int tiles = 0;
     for (int j = 0; j < G.n; ++j) {
-        tiles += (n_outs[j] + 32 * WR - 1) / (32 * WR);
+        tiles += (n_outs[j] + 32 * RPW * WR - 1) / (32 * RPW * WR);
         G.tiles_end[j] = tiles;
     }
-    const int tok_tiles = (n_tok + 64 * WT - 1) / (64 * WT);
-    hipLaunchKernelGGL((gemm_kq_kernel<T, WT, WR>), dim3(unsigned(tiles * tok_tiles)), dim3(64 * WT * WR), 0, s, G, A,
-                       n_in, n_tok, tok_tiles);
+    const int tok_tiles = (n_tok + 32 * TPW * WT - 1) / (32 * TPW * WT);
+    hipLaunchKernelGGL((gemm_kq_kernel<T, WT, WR, TPW, RPW>), dim3(unsigned(tiles * tok_tiles)), dim3(64 * WT * WR),
+                       0, s, G, A, n_in, n_tok, tok_tiles);
     return hipGetLastError();
 }
 
@@ -485,11 +517,11 @@ hipError_t launch_gemm_group(int n, const void* const* ws, const WeightLayout* W
     }
     const ActPtrs A = act_ptrs(act, AL);
     switch (type) {
-        case kQ4_K: return gemm_launch<kQ4_K, 2, 2>(G, n_outs, A, n_in, n_tok, s);
-        case kQ5_K: return gemm_launch<kQ5_K, 2, 2>(G, n_outs, A, n_in, n_tok, s);
+        case kQ4_K: return gemm_launch<kQ4_K, 4, 1, 1, 2>(G, n_outs, A, n_in, n_tok, s);
+        case kQ5_K: return gemm_launch<kQ5_K, 4, 1, 1, 2>(G, n_outs, A, n_in, n_tok, s);
         // Q6_K (no mins MFMA, heavier dequantization): four token wavefronts share each
         // dequantized stage (measured 8-11 % faster on the 4096 x 14336 down projection)
-        case kQ6_K: return gemm_launch<kQ6_K, 4, 1>(G, n_outs, A, n_in, n_tok, s);
+        case kQ6_K: return gemm_launch<kQ6_K, 4, 1, 2, 1>(G, n_outs, A, n_in, n_tok, s);
         default: return hipErrorInvalidValue;
     }
 }
