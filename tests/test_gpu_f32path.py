@@ -102,3 +102,24 @@ def test_backend_upload_and_group(torch_dev, oracle, t):
     finally:
         for k in keys:
             b.release(k)
+
+
+@pytest.mark.parametrize("t", [fh.Q4_1, fh.Q3_K, fh.MXFP4, fh.F16])
+def test_full_size_gate_matrix(torch_dev, oracle, t):
+    """14336 x 4096 (a Llama-3-8B gate) at one token and at 40 tokens: every row on the GPU,
+    a sample of rows against the oracle, and the one-token launch (four rows per wavefront)
+    bit-identical to the first token of the 40-token launch (same sums in the same order)."""
+    torch, d = torch_dev
+    n_out, n_in = 14336, 4096
+    rows = rows_of(t, n_out, n_in, 900 + t)
+    w = fh.repack(t, torch.from_numpy(rows).to(d), n_in, n_out)
+    rb = fh.gguf_row_bytes(t, n_in)
+    sel = np.unique(np.concatenate([np.arange(32), (uniform(901, 48) * n_out).astype(int), [n_out - 1]]))
+    sub = np.concatenate([rows[i * rb:(i + 1) * rb] for i in sel])
+    x = normal(902, (40, n_in), 1.0)
+    ys = {}
+    for m in (1, 40):
+        y = fh.matmul_tensors(t, [w], torch.from_numpy(np.ascontiguousarray(x[:m])).to(d), [n_out])[0].cpu().numpy()
+        check(y[:, sel], oracle.matmul_f32path(t, sub, x[:m], sel.size), f"{fh.TYPE_NAMES[t]} full size M={m}")
+        ys[m] = y
+    assert np.array_equal(ys[1][0], ys[40][0])
