@@ -214,7 +214,10 @@ __global__ __launch_bounds__(64 * WT * WR) __attribute__((amdgpu_waves_per_eu(2)
     // row meta (Q4_K / Q5_K d, dmin, scales; Q6_K d in .x), token scales, mins operands
     __shared__ uint4 s_meta[RWG];
     __shared__ float4 s_xd[TBW * 2 * 4];
-    __shared__ uint4 s_j[has_mins(T) ? TBW * 64 : 1];
+    // mins operands: straight from the thread's own load when the thread's wavefront
+    // owns one token block (thread tid loads block tid / 64, the wavefront's own)
+    constexpr bool J_REG = TPW == 1 && WR == 1;
+    __shared__ uint4 s_j[has_mins(T) && !J_REG ? TBW * 64 : 1];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int l32 = lane & 31, half = lane >> 5;
@@ -380,7 +383,7 @@ __global__ __launch_bounds__(64 * WT * WR) __attribute__((amdgpu_waves_per_eu(2)
     };
     auto store_epi = [&]() {
         s_meta[tid % RWG] = e_meta;
-        if constexpr (has_mins(T)) s_j[tid % EJ] = e_j;
+        if constexpr (has_mins(T) && !J_REG) s_j[tid % EJ] = e_j;
         s_xd[tid % EX] = e_x;
     };
 
@@ -422,7 +425,7 @@ __global__ __launch_bounds__(64 * WT * WR) __attribute__((amdgpu_waves_per_eu(2)
             for (int r = 0; r < RPW; ++r) {
                 v16f J = v16f{};
                 if constexpr (has_mins(T)) {
-                    const v8h aj = __builtin_bit_cast(v8h, s_j[wb * 64 + lane]);
+                    const v8h aj = __builtin_bit_cast(v8h, J_REG ? e_j : s_j[wb * 64 + lane]);
                     J = __builtin_amdgcn_mfma_f32_32x32x16_f16(aj, bj[r], v16f{}, 0, 0, 0);
                 }
 #pragma unroll
