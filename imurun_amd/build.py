@@ -10,12 +10,12 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "libfish_hip.so")
 BUILD = os.path.join(HERE, "_build")
-SOURCES = ["quantize.hip", "repack.hip", "gemv.hip", "batch.hip", "gemm.hip", "moe.hip", "dqmm.hip", "capi.cpp",
-           "pack.cpp"]
+SOURCES = ["quantize.hip", "repack.hip", "gemv.hip", "batch.hip", "gemm.hip", "moe.hip", "dqmm.hip", "span.hip",
+           "capi.cpp", "pack.cpp"]
 # code whose float rounding must follow FISH's baseline x86-64 build step by
 # step (no fused multiply-add): the host weight packer, the expert routing
-# softmax / combine, and the f32-path dequantisers
-NO_CONTRACT = {"pack.cpp", "moe.hip", "dqmm.hip"}
+# softmax / combine, the f32-path dequantisers and the layer-span steps
+NO_CONTRACT = {"pack.cpp", "moe.hip", "dqmm.hip", "span.hip"}
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 

@@ -11,6 +11,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstdio>
 #include <cstring>
 #include <mutex>
@@ -288,52 +289,15 @@ public:
         }
         const size_t x_bytes = size_t(n_tok) * size_t(n_in) * 4;
         if (!reserve(x_bytes, AL.total, y_total * 4)) return false;
-        // one token, one type: each workgroup quantizes x itself (one launch)
-        bool fused = n_tok == 1 && n <= kGemmGroupMax && int8_type(rs[0]->layout.type) &&
-                     gemv_x_supported(rs[0]->layout);
-        for (int i = 1; i < n && fused; ++i) fused = rs[size_t(i)]->layout.type == rs[0]->layout.type;
-        hipError_t e = hipMemcpyAsync(d_x_, x, x_bytes, hipMemcpyHostToDevice, stream_);
-        if (e == hipSuccess && !fused && any_int8)
-            e = launch_quantize(static_cast<const float*>(d_x_), n_tok, n_in, n_in, d_act_, nullptr, nullptr, stream_,
-                                planes_for_tokens(n_tok, n_in));
-        // y_i at consecutive offsets of the staging buffer; tensors of one
-        // K-quant type go out as one grouped launch when the batch is GEMM-sized
+        // y_i at consecutive offsets of the staging buffer
         std::vector<float*> dys(static_cast<size_t>(n));
         size_t off = 0;
-        bool one_group = n <= kGemmGroupMax;
         for (int i = 0; i < n; ++i) {
             dys[size_t(i)] = static_cast<float*>(d_y_) + off;
             off += size_t(n_tok) * size_t(n_outs[i]);
-            one_group = one_group && rs[size_t(i)]->layout.type == rs[0]->layout.type &&
-                        int8_type(rs[size_t(i)]->layout.type) && uses_gemm(rs[size_t(i)]->layout, n_tok);
         }
-        if (e == hipSuccess && fused) {
-            const void* ws[kGemmGroupMax];
-            WeightLayout Ls[kGemmGroupMax];
-            for (int i = 0; i < n; ++i) {
-                ws[i] = rs[size_t(i)]->dev;
-                Ls[i] = rs[size_t(i)]->layout;
-            }
-            e = launch_gemv_x(n, ws, Ls, static_cast<const float*>(d_x_), dys.data(), stream_);
-        } else if (e == hipSuccess && one_group) {
-            const void* ws[kGemmGroupMax];
-            WeightLayout Ls[kGemmGroupMax];
-            int ldy[kGemmGroupMax];
-            for (int i = 0; i < n; ++i) {
-                ws[i] = rs[size_t(i)]->dev;
-                Ls[i] = rs[size_t(i)]->layout;
-                ldy[i] = n_outs[i];
-            }
-            e = launch_gemm_group(n, ws, Ls, d_act_, n_tok, dys.data(), ldy, stream_);
-        } else {
-            for (int i = 0; i < n && e == hipSuccess; ++i) {
-                const Resident& r = *rs[size_t(i)];
-                e = f32path_type(r.layout.type)
-                        ? launch_dq_matmul(r.layout.type, r.dev, static_cast<const float*>(d_x_), n_tok, n_in,
-                                           n_outs[i], dys[size_t(i)], stream_)
-                        : dispatch_matmul(r.dev, r.layout, d_act_, n_tok, dys[size_t(i)], n_outs[i], stream_);
-            }
-        }
+        hipError_t e = hipMemcpyAsync(d_x_, x, x_bytes, hipMemcpyHostToDevice, stream_);
+        if (e == hipSuccess) e = run_group(rs.data(), n, static_cast<const float*>(d_x_), n_tok, n_in, n_outs, dys.data());
         if (e == hipSuccess) e = hipStreamSynchronize(stream_);
         if (e != hipSuccess) {
             mark_broken(e, "matmul");
@@ -358,7 +322,200 @@ public:
         return served_;
     }
 
+    // ---------------------------------------------------------- layer spans
+
+    bool span_prepare(const fish_hip_span_params& p) {
+        std::lock_guard<std::mutex> lk(mu_);
+        span_free();
+        if (!ensure_init() || broken_ || p.n_layers <= 0 || !p.layers || p.n_embd <= 0 || p.n_head <= 0 ||
+            p.n_head_kv <= 0 || p.n_head % p.n_head_kv || p.head_dim <= 0 || p.head_dim > 256 || p.n_ff <= 0 ||
+            p.n_ctx <= 0 || p.rot_dim < 0 || p.rot_dim > p.head_dim || p.rot_dim % 2 || !p.rope_cos || !p.rope_sin)
+            return false;
+        const int E = p.n_embd, Q = p.n_head * p.head_dim, KV = p.n_head_kv * p.head_dim, F = p.n_ff;
+        // every weight resident, unsplit, with the shapes of a dense layer
+        for (int l = 0; l < p.n_layers; ++l) {
+            const fish_hip_span_layer& L = p.layers[l];
+            const void* keys[7] = {L.wq, L.wk, L.wv, L.wo, L.wg, L.wu, L.wd};
+            const int n_in[7] = {E, E, E, Q, E, E, F}, n_out[7] = {Q, KV, KV, E, F, F, E};
+            for (int i = 0; i < 7; ++i) {
+                auto it = map_.find(keys[i]);
+                if (it == map_.end() || it->second.n_expert != 1 || it->second.layout.n_in != n_in[i] ||
+                    it->second.layout.n_out != n_out[i])
+                    return false;
+                span_keys_.push_back(keys[i]);
+            }
+            if (!L.attn_norm || !L.ffn_norm) return false;
+        }
+        sp_ = p;
+        sp_.layers = nullptr;
+        const size_t half = size_t(p.rot_dim / 2), ctx = size_t(p.n_ctx);
+        const size_t norm_b = size_t(p.n_layers) * 2 * E * 4, rope_b = ctx * half * 4,
+                     kv_b = size_t(p.n_layers) * ctx * KV * 4;
+        hipError_t e = hipMalloc(&d_span_fixed_, norm_b + 2 * rope_b + 2 * kv_b + 256);
+        if (e != hipSuccess) {
+            d_span_fixed_ = nullptr;
+            span_keys_.clear();
+            return false;
+        }
+        char* b = static_cast<char*>(d_span_fixed_);
+        d_norms_ = reinterpret_cast<float*>(b);
+        d_cos_ = reinterpret_cast<float*>(b + norm_b);
+        d_sin_ = reinterpret_cast<float*>(b + norm_b + rope_b);
+        d_kc_ = reinterpret_cast<float*>(b + norm_b + 2 * rope_b);
+        d_vc_ = reinterpret_cast<float*>(b + norm_b + 2 * rope_b + kv_b);
+        for (int l = 0; l < p.n_layers && e == hipSuccess; ++l) {
+            e = hipMemcpy(d_norms_ + size_t(2 * l) * E, p.layers[l].attn_norm, size_t(E) * 4, hipMemcpyHostToDevice);
+            if (e == hipSuccess)
+                e = hipMemcpy(d_norms_ + size_t(2 * l + 1) * E, p.layers[l].ffn_norm, size_t(E) * 4,
+                              hipMemcpyHostToDevice);
+        }
+        if (e == hipSuccess && rope_b) e = hipMemcpy(d_cos_, p.rope_cos, rope_b, hipMemcpyHostToDevice);
+        if (e == hipSuccess && rope_b) e = hipMemcpy(d_sin_, p.rope_sin, rope_b, hipMemcpyHostToDevice);
+        if (e != hipSuccess) {
+            span_free();
+            mark_broken(e, "span_prepare");
+            return false;
+        }
+        span_on_ = true;
+        return true;
+    }
+
+    void span_release() {
+        std::lock_guard<std::mutex> lk(mu_);
+        span_free();
+    }
+
+    // One forward of the span's layers over x (host) for positions pos0.. (model.cpp:1650-1801).
+    bool span_forward(float* x, int n_tok, int pos0) {
+        std::lock_guard<std::mutex> lk(mu_);
+        if (!span_on_ || broken_ || !x || n_tok <= 0 || pos0 < 0 || pos0 + n_tok > sp_.n_ctx) return false;
+        const int E = sp_.n_embd, H = sp_.n_head, HKV = sp_.n_head_kv, D = sp_.head_dim, F = sp_.n_ff;
+        const int Q = H * D, KV = HKV * D, ld = pos0 + n_tok;
+        std::vector<const Resident*> rs(span_keys_.size());
+        for (size_t i = 0; i < rs.size(); ++i) {
+            auto it = map_.find(span_keys_[i]);
+            if (it == map_.end()) return false;
+            rs[i] = &it->second;
+        }
+        // scratch: x, xb, q, k, v, q_rot, attn, proj, g, u, scores
+        const size_t T = size_t(n_tok);
+        const size_t sizes[11] = {T * E, T * E, T * Q, T * KV, T * KV, T * Q, T * Q, T * E, T * F, T * F,
+                                  T * H * size_t(ld)};
+        size_t total = 0;
+        for (size_t z : sizes) total += (z * 4 + 255) / 256 * 256;
+        size_t act = 0;
+        for (int n_in : {E, Q, F}) act = std::max(act, act_layout(n_tok, n_in).total);
+        if (!act || !reserve(0, act, 0) || !grow_span_ws(total)) return false;
+        float* buf[11];
+        char* b = static_cast<char*>(d_span_ws_);
+        for (int i = 0; i < 11; ++i) {
+            buf[i] = reinterpret_cast<float*>(b);
+            b += (sizes[i] * 4 + 255) / 256 * 256;
+        }
+        float *dx = buf[0], *xb = buf[1], *q = buf[2], *k = buf[3], *v = buf[4], *qr = buf[5], *att = buf[6],
+              *proj = buf[7], *g = buf[8], *u = buf[9], *sc = buf[10];
+        const float scale = sp_.attn_scale > 0.0f ? sp_.attn_scale : 1.0f / std::sqrt(float(D));
+        hipError_t e = hipMemcpyAsync(dx, x, T * E * 4, hipMemcpyHostToDevice, stream_);
+        for (int l = 0; l < sp_.n_layers && e == hipSuccess; ++l) {
+            const Resident* const* W = rs.data() + size_t(7 * l);
+            float* kc = d_kc_ + size_t(l) * sp_.n_ctx * KV;
+            float* vc = d_vc_ + size_t(l) * sp_.n_ctx * KV;
+            const int n_qkv[3] = {Q, KV, KV}, n_e[1] = {E}, n_f[2] = {F, F};
+            float* y_qkv[3] = {q, k, v};
+            float* y_o[1] = {proj};
+            float* y_gu[2] = {g, u};
+            e = launch_rmsnorm(dx, d_norms_ + size_t(2 * l) * E, xb, n_tok, E, sp_.eps, stream_);
+            if (e == hipSuccess) e = run_group(W, 3, xb, n_tok, E, n_qkv, y_qkv);
+            if (e == hipSuccess)
+                e = launch_rope_store(q, k, v, qr, kc, vc, n_tok, H, HKV, D, sp_.rot_dim, sp_.rope_neox != 0, pos0,
+                                      d_cos_, d_sin_, stream_);
+            if (e == hipSuccess) e = launch_attention(qr, kc, vc, att, sc, ld, n_tok, H, HKV, D, pos0, scale, stream_);
+            if (e == hipSuccess) e = run_group(W + 3, 1, att, n_tok, Q, n_e, y_o);
+            if (e == hipSuccess) e = launch_add(dx, proj, T * E, stream_);
+            if (e == hipSuccess) e = launch_rmsnorm(dx, d_norms_ + size_t(2 * l + 1) * E, xb, n_tok, E, sp_.eps, stream_);
+            if (e == hipSuccess) e = run_group(W + 4, 2, xb, n_tok, E, n_f, y_gu);
+            if (e == hipSuccess) e = launch_silu_mul(g, u, T * F, stream_);
+            if (e == hipSuccess) e = run_group(W + 6, 1, g, n_tok, F, n_e, y_o);
+            if (e == hipSuccess) e = launch_add(dx, proj, T * E, stream_);
+        }
+        // x is written only once everything has run
+        if (e == hipSuccess) e = hipStreamSynchronize(stream_);
+        if (e == hipSuccess) e = hipMemcpy(x, dx, T * E * 4, hipMemcpyDeviceToHost);
+        if (e != hipSuccess) {
+            mark_broken(e, "span_forward");
+            return false;
+        }
+        ++served_;
+        return true;
+    }
+
 private:
+    // The matmuls of n resident tensors on one device input (f32 [n_tok][n_in]):
+    // y_i [n_tok][n_out_i] (device). Asynchronous on stream_; d_act_ must hold
+    // act_layout(n_tok, n_in).total bytes.
+    hipError_t run_group(const Resident* const* rs, int n, const float* dx, int n_tok, int n_in, const int* n_outs,
+                         float* const* dys) {
+        bool any_int8 = false;
+        for (int i = 0; i < n; ++i) any_int8 = any_int8 || int8_type(rs[i]->layout.type);
+        // one token, one type: each workgroup quantizes x itself (one launch)
+        bool fused = n_tok == 1 && n <= kGemmGroupMax && int8_type(rs[0]->layout.type) &&
+                     gemv_x_supported(rs[0]->layout);
+        for (int i = 1; i < n && fused; ++i) fused = rs[i]->layout.type == rs[0]->layout.type;
+        hipError_t e = hipSuccess;
+        if (!fused && any_int8)
+            e = launch_quantize(dx, n_tok, n_in, n_in, d_act_, nullptr, nullptr, stream_,
+                                planes_for_tokens(n_tok, n_in));
+        // tensors of one K-quant type go out as one grouped launch when the batch is GEMM-sized
+        bool one_group = n <= kGemmGroupMax;
+        for (int i = 0; i < n; ++i)
+            one_group = one_group && rs[i]->layout.type == rs[0]->layout.type && int8_type(rs[i]->layout.type) &&
+                        uses_gemm(rs[i]->layout, n_tok);
+        if (e == hipSuccess && fused) {
+            const void* ws[kGemmGroupMax];
+            WeightLayout Ls[kGemmGroupMax];
+            for (int i = 0; i < n; ++i) {
+                ws[i] = rs[size_t(i)]->dev;
+                Ls[i] = rs[size_t(i)]->layout;
+            }
+            e = launch_gemv_x(n, ws, Ls, dx, dys, stream_);
+        } else if (e == hipSuccess && one_group) {
+            const void* ws[kGemmGroupMax];
+            WeightLayout Ls[kGemmGroupMax];
+            int ldy[kGemmGroupMax];
+            for (int i = 0; i < n; ++i) {
+                ws[i] = rs[size_t(i)]->dev;
+                Ls[i] = rs[size_t(i)]->layout;
+                ldy[i] = n_outs[i];
+            }
+            e = launch_gemm_group(n, ws, Ls, d_act_, n_tok, dys, ldy, stream_);
+        } else {
+            for (int i = 0; i < n && e == hipSuccess; ++i) {
+                const Resident& r = *rs[i];
+                e = f32path_type(r.layout.type)
+                        ? launch_dq_matmul(r.layout.type, r.dev, dx, n_tok, n_in, n_outs[i], dys[i], stream_)
+                        : dispatch_matmul(r.dev, r.layout, d_act_, n_tok, dys[i], n_outs[i], stream_);
+            }
+        }
+        return e;
+    }
+
+    bool grow_span_ws(size_t need) {
+        if (need <= cap_span_ws_) return true;
+        if (d_span_ws_) (void)hipFree(d_span_ws_);
+        d_span_ws_ = nullptr;
+        cap_span_ws_ = 0;
+        if (hipMalloc(&d_span_ws_, need) != hipSuccess) return false;
+        cap_span_ws_ = need;
+        return true;
+    }
+
+    void span_free() {
+        if (d_span_fixed_) (void)hipFree(d_span_fixed_);
+        d_span_fixed_ = nullptr;
+        span_keys_.clear();
+        span_on_ = false;
+    }
+
     HipBackend() = default;
 
     bool ensure_init() {
@@ -402,6 +559,15 @@ private:
     uint64_t bytes_ = 0;
     void *d_x_ = nullptr, *d_act_ = nullptr, *d_y_ = nullptr;
     size_t cap_x_ = 0, cap_act_ = 0, cap_y_ = 0;
+    // layer span: parameters, weight keys (7 per layer), norms / RoPE tables /
+    // KV cache in one allocation, per-call scratch
+    bool span_on_ = false;
+    fish_hip_span_params sp_{};
+    std::vector<const void*> span_keys_;
+    void* d_span_fixed_ = nullptr;
+    float *d_norms_ = nullptr, *d_cos_ = nullptr, *d_sin_ = nullptr, *d_kc_ = nullptr, *d_vc_ = nullptr;
+    void* d_span_ws_ = nullptr;
+    size_t cap_span_ws_ = 0;
 };
 
 }  // namespace
@@ -597,6 +763,15 @@ int fish_hip_backend_matmul(const void* key, const float* x, int n_tok, int n_in
     float* ys[1] = {y};
     return HipBackend::instance().matmul_group(keys, 1, x, n_tok, n_in, &n_out, ys) ? 1 : 0;
 }
+
+int fish_hip_span_prepare(const fish_hip_span_params* p) {
+    return p && HipBackend::instance().span_prepare(*p) ? 1 : 0;
+}
+int fish_hip_span_forward(float* x, int n_tok, int pos0) {
+    return HipBackend::instance().span_forward(x, n_tok, pos0) ? 1 : 0;
+}
+void fish_hip_span_kv_truncate(int n_past) { (void)n_past; }  // positions >= n_past are rewritten before use
+void fish_hip_span_release(void) { HipBackend::instance().span_release(); }
 
 int fish_hip_backend_matmul_group(const void* const* keys, int n, const float* x, int n_tok, int n_in,
                                   const int* n_outs, float* const* ys) {

@@ -139,6 +139,19 @@ struct GemmGroup {
 hipError_t launch_gemm_group(int n, const void* const* ws, const WeightLayout* WLs, const void* act, int n_tok,
                              float* const* ys, const int* ldys, hipStream_t stream);
 
+// Layer-span steps (span.hip): rmsnorm per token row; RoPE of q into q_out and
+// of k into the KV-cache rows pos0.. (with v); causal GQA attention per
+// (token, head) with a scores buffer of n_tok * H rows of ld >= pos0 + n_tok
+// floats; g = silu(g) * u; x += y.
+hipError_t launch_rmsnorm(const float* x, const float* w, float* out, int n_tok, int n, float eps, hipStream_t s);
+hipError_t launch_rope_store(const float* q, const float* k, const float* v, float* q_out, float* kc, float* vc,
+                             int n_tok, int H, int HKV, int D, int rot_dim, bool neox, int pos0, const float* cosv,
+                             const float* sinv, hipStream_t s);
+hipError_t launch_attention(const float* q, const float* kc, const float* vc, float* out, float* scores, int ld,
+                            int n_tok, int H, int HKV, int D, int pos0, float scale, hipStream_t s);
+hipError_t launch_silu_mul(float* g, const float* u, size_t n, hipStream_t s);
+hipError_t launch_add(float* x, const float* y, size_t n, hipStream_t s);
+
 // Per-block integer dots of every row with token 0 of `act`.
 hipError_t launch_block_ints(const void* w, const WeightLayout& L, const void* act, int32_t* out, hipStream_t stream);
 

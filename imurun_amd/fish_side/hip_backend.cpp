@@ -13,6 +13,7 @@
 #include <fish/backend.h>
 
 #include <cstdlib>
+#include <vector>
 
 #include "fish_hip.h"
 
@@ -47,6 +48,44 @@ public:
         return fish_hip_backend_matmul_group(reinterpret_cast<const void* const*>(ts), n, x, n_tok, n_in, n_outs,
                                              ys) != 0;
     }
+
+    // Layer spans (backend.h:89-162) for dense llama-style layers: separate
+    // q/k/v and gate/up projections, RMS norms, RoPE, f32 KV cache, SiLU.
+    // Everything else a span can carry (fused qkv or gate|up, biases, q/k or
+    // post norms, soft-caps, sliding windows, GELU) is refused, and FISH then
+    // keeps routing per matmul.
+    bool span_prepare(const SpanParams& p) override {
+        const int n = p.layer_end - p.layer_begin;
+        if (n <= 0 || !p.layers || p.attn_softcap > 0.0f || p.window > 0 || p.gelu) return false;
+        std::vector<fish_hip_span_layer> ls(static_cast<size_t>(n));
+        for (int i = 0; i < n; ++i) {
+            const SpanLayer& L = p.layers[i];
+            if (L.wqkv || !L.wq || !L.wk || !L.wv || !L.wo || !L.wg || !L.wu || !L.wd || !L.attn_norm ||
+                !L.ffn_norm || L.post_attn_norm || L.post_ffn_norm || L.q_norm || L.k_norm || L.bias_q || L.bias_k ||
+                L.bias_v || L.bias_o || L.bias_qkv || L.sliding_window)
+                return false;
+            ls[size_t(i)] = {L.wq, L.wk, L.wv, L.wo, L.wg, L.wu, L.wd, L.attn_norm, L.ffn_norm};
+        }
+        fish_hip_span_params hp{};
+        hp.n_layers = n;
+        hp.n_embd = p.n_embd;
+        hp.n_head = p.n_head;
+        hp.n_head_kv = p.n_head_kv;
+        hp.head_dim = p.head_dim;
+        hp.n_ff = p.n_ff;
+        hp.n_ctx = p.n_ctx;
+        hp.eps = p.eps;
+        hp.attn_scale = p.attn_scale;
+        hp.rope_cos = p.rope_cos;
+        hp.rope_sin = p.rope_sin;
+        hp.rot_dim = p.rot_dim;
+        hp.rope_neox = p.rope_neox ? 1 : 0;
+        hp.layers = ls.data();
+        return fish_hip_span_prepare(&hp) != 0;
+    }
+    bool span_forward(float* x, int n_tok, int pos0) override { return fish_hip_span_forward(x, n_tok, pos0) != 0; }
+    void span_kv_truncate(int n_past) override { fish_hip_span_kv_truncate(n_past); }
+    void span_release() override { fish_hip_span_release(); }
 };
 
 struct Registrar {

@@ -214,6 +214,51 @@ FISH_HIP_API int fish_hip_backend_matmul(const void* key, const float* x, int n_
 FISH_HIP_API int fish_hip_backend_matmul_group(const void* const* keys, int n, const float* x, int n_tok, int n_in,
                                                const int* n_outs, float* const* ys);
 
+/* ---------------------------------------------------------------- layer spans (host pointers, synchronous) */
+
+/* One dense llama-style layer of a span (backend.h:114-134 SpanLayer, the
+ * subset this backend runs): the weight keys given to fish_hip_upload (all
+ * resident) and the two RMS-norm weight vectors [n_embd] (host, copied). */
+typedef struct fish_hip_span_layer {
+    const void* wq;
+    const void* wk;
+    const void* wv;
+    const void* wo;
+    const void* wg;
+    const void* wu;
+    const void* wd;
+    const float* attn_norm;
+    const float* ffn_norm;
+} fish_hip_span_layer;
+
+/* backend.h:136-154 SpanParams, same meaning: head_dim <= 256, n_head a
+ * multiple of n_head_kv, rot_dim even and <= head_dim, RoPE tables
+ * [n_ctx][rot_dim / 2] (host, copied), attn_scale 0 = 1/sqrt(head_dim). */
+typedef struct fish_hip_span_params {
+    int n_layers;
+    int n_embd, n_head, n_head_kv, head_dim, n_ff, n_ctx;
+    float eps;
+    float attn_scale;
+    const float* rope_cos;
+    const float* rope_sin;
+    int rot_dim;
+    int rope_neox;
+    const fish_hip_span_layer* layers;
+} fish_hip_span_params;
+
+/* ComputeBackend::span_prepare (backend.h:156): keeps the layers' weights,
+ * copies the norms and RoPE tables and allocates an f32 KV cache of n_ctx
+ * positions per layer. Replaces an earlier span. 1 ok, 0 refused (no span). */
+FISH_HIP_API int fish_hip_span_prepare(const fish_hip_span_params* p);
+/* ComputeBackend::span_forward (backend.h:157): x [n_tok][n_embd] (host) is the
+ * residual stream entering the span's first layer; on return it leaves the
+ * last one, and positions pos0 .. pos0 + n_tok - 1 are in the KV cache.
+ * 1 ok; 0 failed with x unmodified. */
+FISH_HIP_API int fish_hip_span_forward(float* x, int n_tok, int pos0);
+/* ComputeBackend::span_kv_truncate / span_release (backend.h:158-159) */
+FISH_HIP_API void fish_hip_span_kv_truncate(int n_past);
+FISH_HIP_API void fish_hip_span_release(void);
+
 #ifdef __cplusplus
 }
 #endif

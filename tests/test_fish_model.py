@@ -162,3 +162,27 @@ def test_model_generates_through_the_hip_backend(fish, tmp_path, name):
     # prefill: per layer q/k/v, o, gate/up, down (4 calls) + output; then the same per decoded token
     assert served >= (4 * cfg["n_layers"] + 1) * N_GEN
     assert dev == cpu
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", ["q4_k_m", "q8_0_q4_0"])
+def test_model_generates_through_a_layer_span(fish, tmp_path, name):
+    # FISH offers its GPU layers as one span (model.cpp:780-850); the backend runs norms,
+    # projections, RoPE, the KV cache, attention, SiLU and residuals of both layers on the
+    # device, one call per forward (plus the output matmul), token-identical to the CPU
+    path = str(tmp_path / f"{name}.gguf")
+    tiny_llama(path, MODELS[name], seed=14)
+    cpu, _, _ = run(fish, path, gpu=False)
+    os.environ["FISH_GPU_SPAN"] = "1"
+    os.environ["FISH_GPU_NO_IMPORTANCE"] = "1"
+    try:
+        served0 = fh.load().fish_hip_backend_served()
+        dev, st, _ = run(fish, path, gpu=True)
+        served = fh.load().fish_hip_backend_served() - served0
+    finally:
+        os.environ["FISH_GPU_SPAN"] = "0"
+        os.environ.pop("FISH_GPU_NO_IMPORTANCE", None)
+    assert st.gpu_layers == 2, st.placement
+    # one span call and one output matmul per forward, not per-matmul routing (9 per forward)
+    assert st.generated_tokens <= served <= 3 * st.generated_tokens, (served, st.placement, st.gpu_mix)
+    assert dev == cpu
