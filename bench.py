@@ -276,6 +276,75 @@ def run_q5k_prefill(args, torch, fh, dev):
             "tops": round(ops / us / 1e6, 1), "pct_int8_peak": round(100 * ops / us / 1e6 / INT8_PEAK_TOPS, 2)}
 
 
+def run_span_decode(args, torch, fh, dev):
+    """Llama-3-8B layers as one layer span (Q4_K_M mix: q, k, o, gate, up Q4_K; v, down Q6_K) through
+    the backend's C ABI: a 512-token prefill, then decode tokens at position 512, each call moving x
+    host -> device -> host. Beside it, the same layer routed per matmul (four synchronous backend calls
+    with host round trips, FISH's path without spans; its CPU attention is not counted)."""
+    from imurun_amd.synth import normal
+    L_, H_, HKV_, D_, CTX = 4, 32, 8, 128, 2048
+    Qd, KVd = H_ * D_, HKV_ * D_
+    types = dict(wq=fh.Q4_K, wk=fh.Q4_K, wv=fh.Q6_K, wo=fh.Q4_K, wg=fh.Q4_K, wu=fh.Q4_K, wd=fh.Q6_K)
+    shapes = dict(wq=(Qd, E), wk=(KVd, E), wv=(KVd, E), wo=(E, Qd), wg=(F, E), wu=(F, E), wd=(E, F))
+    be = fh.HipBackend()
+    host, layer_bytes = {}, 0
+    for i, n in enumerate(types):
+        n_out, n_in = shapes[n]
+        base = fh.quantize_rows(types[n], normal(300 + i, (min(1024, n_out), n_in), 0.02))
+        host[n] = np.tile(base, n_out // min(1024, n_out))
+        layer_bytes += host[n].size
+    layers = []
+    for l in range(L_):
+        names = []
+        for n in types:
+            assert be.upload(f"span{l}.{n}", types[n], host[n], shapes[n][1], shapes[n][0])
+            names.append(f"span{l}.{n}")
+        layers.append((names, np.ones(E, np.float32), np.ones(E, np.float32)))
+    half = D_ // 2
+    th = np.arange(CTX)[:, None] * (500000.0 ** (-np.arange(half) * 2 / D_))[None, :]
+    assert be.span_prepare(layers, E, H_, HKV_, D_, F, CTX, np.cos(th), np.sin(th), rope_neox=False)
+    try:
+        assert be.span_forward(normal(309, (512, E), 1.0), 0)  # first call sizes the scratch
+        x = normal(310, (512, E), 1.0)
+        t0 = time.perf_counter()
+        assert be.span_forward(x, 0)
+        prefill_ms = (time.perf_counter() - t0) * 1e3
+        xs = [normal(311 + i, (1, E), 1.0) for i in range(24)]
+        times = []
+        for xi in xs:
+            t0 = time.perf_counter()
+            assert be.span_forward(xi, 512)
+            times.append(time.perf_counter() - t0)
+        dec_us = float(np.median(times[4:])) * 1e6
+        # the same layer routed per matmul with host round trips
+        x1 = normal(330, (1, E), 1.0)
+        h1 = normal(331, (1, F), 1.0)
+        a1 = normal(332, (1, Qd), 1.0)
+        names = layers[0][0]
+        rt = []
+        for _ in range(20):
+            t0 = time.perf_counter()
+            be.matmul_group(names[0:3], x1, [Qd, KVd, KVd])
+            be.matmul_group(names[3:4], a1, [E])
+            be.matmul_group(names[4:6], x1, [F, F])
+            be.matmul_group(names[6:7], h1, [E])
+            rt.append(time.perf_counter() - t0)
+        routed_us = float(np.median(rt[4:])) * 1e6
+    finally:
+        be.span_release()
+        for names, _, _ in layers:
+            for n in names:
+                be.release(n)
+    per_layer = dec_us / L_
+    return {"workload": f"Llama-3-8B layer span, {L_} layers, Q4_K_M mix, decode at position 512 "
+                        "(x host->device->host per call)",
+            "decode_us_per_token": round(dec_us, 1), "us_per_layer": round(per_layer, 2),
+            "layer_weight_bytes": layer_bytes, "gbs": round(layer_bytes / per_layer / 1e3, 1),
+            "routed_per_matmul_us_per_layer": round(routed_us, 2),
+            "prefill_512_ms": round(prefill_ms, 2),
+            "prefill_tok_per_s": round(512 / prefill_ms * 1e3, 1)}
+
+
 def run_moe(args, torch, fh, dev, name, NE, K, E, F_, types, cases):
     """Expert FFN layer at the given token counts; one distinct expert replicated (same traffic)."""
     from imurun_amd.synth import normal
@@ -487,6 +556,7 @@ def main() -> int:
         out["q5_k_gemv"] = run_kquant_gemv(args, torch, fh, dev, fh.Q5_K, "Q5_K")
         out["q6_k_gemv"] = run_kquant_gemv(args, torch, fh, dev, fh.Q6_K, "Q6_K")
         out["f32_path_gemv"] = run_f32path_gemv(args, torch, fh, dev)
+        out["span_decode"] = run_span_decode(args, torch, fh, dev)
         out["moe_mixtral"] = run_moe(args, torch, fh, dev, "Mixtral-8x7B", 8, 2, 4096, 14336,
                                      (fh.Q4_K, fh.Q4_K, fh.Q4_K), (1, 64))
         out["moe_qwen3"] = run_moe(args, torch, fh, dev, "Qwen3-30B-A3B", 128, 8, 2048, 768,

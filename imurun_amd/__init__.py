@@ -91,6 +91,10 @@ def load() -> ctypes.CDLL:
         "fish_hip_backend_served": ([], ctypes.c_uint64),
         "fish_hip_backend_matmul": ([_P, _P, ctypes.c_int, ctypes.c_int, ctypes.c_int, _P], ctypes.c_int),
         "fish_hip_backend_matmul_group": ([_P, ctypes.c_int, _P, ctypes.c_int, ctypes.c_int, _P, _P], ctypes.c_int),
+        "fish_hip_span_prepare": ([_P], ctypes.c_int),
+        "fish_hip_span_forward": ([_P, ctypes.c_int, ctypes.c_int], ctypes.c_int),
+        "fish_hip_span_kv_truncate": ([ctypes.c_int], None),
+        "fish_hip_span_release": ([], None),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)
@@ -342,6 +346,21 @@ def silu_mul_quantize(g, u, stream=None):
 
 # ------------------------------------------------------------------ backend (host buffers)
 
+class SpanLayer(ctypes.Structure):
+    """fish_hip_span_layer (include/fish_hip.h)."""
+    _fields_ = [(n, ctypes.c_void_p) for n in ("wq", "wk", "wv", "wo", "wg", "wu", "wd")] + \
+               [("attn_norm", ctypes.c_void_p), ("ffn_norm", ctypes.c_void_p)]
+
+
+class SpanParams(ctypes.Structure):
+    """fish_hip_span_params (include/fish_hip.h)."""
+    _fields_ = [("n_layers", ctypes.c_int), ("n_embd", ctypes.c_int), ("n_head", ctypes.c_int),
+                ("n_head_kv", ctypes.c_int), ("head_dim", ctypes.c_int), ("n_ff", ctypes.c_int),
+                ("n_ctx", ctypes.c_int), ("eps", ctypes.c_float), ("attn_scale", ctypes.c_float),
+                ("rope_cos", ctypes.c_void_p), ("rope_sin", ctypes.c_void_p), ("rot_dim", ctypes.c_int),
+                ("rope_neox", ctypes.c_int), ("layers", ctypes.c_void_p)]
+
+
 class HipBackend:
     """ComputeBackend over host numpy buffers (backend.h:26-163)."""
 
@@ -398,6 +417,32 @@ class HipBackend:
         y = np.empty((n_tok, n_out), np.float32)
         ok = self.L.fish_hip_backend_matmul(self._key(name), x.ctypes.data, n_tok, n_in, n_out, y.ctypes.data)
         return y if ok else None
+
+    def span_prepare(self, layers, n_embd, n_head, n_head_kv, head_dim, n_ff, n_ctx, rope_cos, rope_sin,
+                     rope_neox=False, eps=1e-5, attn_scale=0.0) -> bool:
+        """ComputeBackend::span_prepare over uploaded tensors: layers = [(names of
+        wq, wk, wv, wo, wg, wu, wd), attn_norm, ffn_norm]; RoPE tables [n_ctx][rot_dim / 2]."""
+        arr = (SpanLayer * len(layers))()
+        keep = []
+        for i, (names, an, fn) in enumerate(layers):
+            an = np.ascontiguousarray(an, np.float32)
+            fn = np.ascontiguousarray(fn, np.float32)
+            keep += [an, fn]
+            arr[i] = SpanLayer(*[self._key(n).value for n in names], an.ctypes.data, fn.ctypes.data)
+        rc = np.ascontiguousarray(rope_cos, np.float32)
+        rs = np.ascontiguousarray(rope_sin, np.float32)
+        p = SpanParams(len(layers), n_embd, n_head, n_head_kv, head_dim, n_ff, n_ctx, eps, attn_scale,
+                       rc.ctypes.data, rs.ctypes.data, 2 * rc.shape[1], 1 if rope_neox else 0,
+                       ctypes.cast(arr, ctypes.c_void_p))
+        return bool(self.L.fish_hip_span_prepare(ctypes.byref(p)))
+
+    def span_forward(self, x: np.ndarray, pos0: int) -> bool:
+        """ComputeBackend::span_forward: x [n_tok, n_embd] float32, updated in place."""
+        assert x.dtype == np.float32 and x.flags.c_contiguous
+        return bool(self.L.fish_hip_span_forward(x.ctypes.data, x.shape[0], pos0))
+
+    def span_release(self) -> None:
+        self.L.fish_hip_span_release()
 
     def matmul_group(self, names, x: np.ndarray, n_outs):
         x = np.ascontiguousarray(x, np.float32)

@@ -461,6 +461,31 @@ private:
         bool fused = n_tok == 1 && n <= kGemmGroupMax && int8_type(rs[0]->layout.type) &&
                      gemv_x_supported(rs[0]->layout);
         for (int i = 1; i < n && fused; ++i) fused = rs[i]->layout.type == rs[0]->layout.type;
+        // one token, int8 types mixed (q/k in Q4_K, v in Q6_K): one fused launch per type
+        bool per_type = !fused && n_tok == 1 && n <= kGemmGroupMax;
+        for (int i = 0; i < n && per_type; ++i)
+            per_type = int8_type(rs[i]->layout.type) && gemv_x_supported(rs[i]->layout);
+        if (per_type) {
+            hipError_t e = hipSuccess;
+            bool done[kGemmGroupMax] = {};
+            for (int i = 0; i < n && e == hipSuccess; ++i) {
+                if (done[i]) continue;
+                const void* ws[kGemmGroupMax];
+                WeightLayout Ls[kGemmGroupMax];
+                float* ys[kGemmGroupMax];
+                int m = 0;
+                for (int j = i; j < n; ++j) {
+                    if (done[j] || rs[j]->layout.type != rs[i]->layout.type) continue;
+                    done[j] = true;
+                    ws[m] = rs[j]->dev;
+                    Ls[m] = rs[j]->layout;
+                    ys[m] = dys[j];
+                    ++m;
+                }
+                e = launch_gemv_x(m, ws, Ls, dx, ys, stream_);
+            }
+            return e;
+        }
         hipError_t e = hipSuccess;
         if (!fused && any_int8)
             e = launch_quantize(dx, n_tok, n_in, n_in, d_act_, nullptr, nullptr, stream_,

@@ -7,7 +7,7 @@
 //   RoPE + KV    ops.cpp:126-152 (table rotation, neox or adjacent pairs) and the
 //                KV-cache store of model.cpp:1726-1734
 //   attention    ops.cpp:303-357 (causal, GQA head groups, max-subtracted exp,
-//                p = e / sum, o = sum_j p_j v_j)
+//                p = e * (1 / sum), o = sum_j p_j v_j)
 //   silu * up    ops.cpp:25-30, model.cpp:1504-1508
 //   residual add model.cpp:1772-1776, :1797-1801
 // The file is compiled without floating-point contraction, so every
@@ -97,56 +97,96 @@ __global__ __launch_bounds__(kTh) void rope_store_kernel(const float* __restrict
     }
 }
 
-// One workgroup per (token, head): scores over positions 0..pos into the
-// workgroup's row of `scores` (stride ld), softmax, then o = sum_j p_j v_j
-// with the positions split over D-wide thread groups and summed in LDS.
-// Needs D <= kTh.
+// One workgroup (four wavefronts) per (token, head). Lanes run over the
+// head's D values (DL = D / 64 per lane, rounded up; lanes past D hold
+// zeros), so every K or V row is one coalesced load; wavefront w takes the
+// positions j = w, w + 4, ... up to pos.
+//   scores: per position a lane-partial dot, summed over the wavefront with
+//           xor shuffles, scaled, kept in the workgroup's row of `scores`;
+//   softmax: max and sum over the workgroup; p_j = e_j * (1 / sum);
+//   o:      each wavefront sums p_j v_j over its positions in registers; the
+//           four partial vectors are added in LDS.
+// Needs D <= 256.
+template <int DL>
 __global__ __launch_bounds__(kTh) void attention_kernel(const float* __restrict__ q, const float* __restrict__ kc,
                                                         const float* __restrict__ vc, float* __restrict__ out,
                                                         float* __restrict__ scores, int ld, int H, int HKV, int D,
                                                         int pos0, float scale) {
-    __shared__ float s_q[kTh];
     __shared__ float red[kTh];
-    __shared__ float part[kTh];
+    __shared__ float s_o[4][64 * DL];
     const int item = blockIdx.x, t = item / H, h = item % H;
     const int pos = pos0 + t, kvh = h / (H / HKV), KV = HKV * D, Q = H * D;
-    const int tid = threadIdx.x;
-    if (tid < D) s_q[tid] = q[size_t(t) * Q + size_t(h) * D + tid];
-    __syncthreads();
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    float qv[DL];
+#pragma unroll
+    for (int i = 0; i < DL; ++i) {
+        const int d = lane + 64 * i;
+        qv[i] = d < D ? q[size_t(t) * Q + size_t(h) * D + d] : 0.0f;
+    }
     float* sc = scores + size_t(item) * ld;
     const float* kb = kc + size_t(kvh) * D;
     const float* vb = vc + size_t(kvh) * D;
 
+    // PB positions per wavefront step, all their row loads issued before the
+    // first use (clamped to pos: unconditional loads, extra positions dropped)
+    constexpr int PB = 16;
     float m = -INFINITY;
-    for (int j = tid; j <= pos; j += kTh) {
-        const float* kr = kb + size_t(j) * KV;
-        float dot = 0.0f;
-        for (int d = 0; d < D; ++d) dot += s_q[d] * kr[d];
-        const float sv = dot * scale;
-        sc[j] = sv;
-        m = fmaxf(m, sv);
+    for (int j0 = w; j0 <= pos; j0 += 4 * PB) {
+        float kv[PB][DL];
+#pragma unroll
+        for (int b = 0; b < PB; ++b) {
+            const float* kr = kb + size_t(min(j0 + 4 * b, pos)) * KV;
+#pragma unroll
+            for (int i = 0; i < DL; ++i) kv[b][i] = lane + 64 * i < D ? kr[lane + 64 * i] : 0.0f;
+        }
+#pragma unroll
+        for (int b = 0; b < PB; ++b) {
+            float part = 0.0f;
+#pragma unroll
+            for (int i = 0; i < DL; ++i) part += qv[i] * kv[b][i];
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) part += __shfl_xor(part, off);
+            const float sv = part * scale;
+            const int j = j0 + 4 * b;
+            if (j <= pos) {
+                if (lane == 0) sc[j] = sv;
+                m = fmaxf(m, sv);
+            }
+        }
     }
-    const float mx = block_reduce_f(m, red, true);
+    const float mx = block_reduce_f(m, red, true);  // its barriers also order the sc writes
     float sum = 0.0f;
     for (int j = tid; j <= pos; j += kTh) {
         const float e = expf(sc[j] - mx);
         sc[j] = e;
         sum += e;
     }
-    const float tot = block_reduce_f(sum, red, false);  // its barriers also order the sc writes
+    const float tot = block_reduce_f(sum, red, false);
     const float inv = tot > 0.0f ? 1.0f / tot : 0.0f;
 
-    const int groups = kTh / D, g = tid / D, d = tid % D;
-    float acc = 0.0f;
-    if (g < groups)
-        for (int j = g; j <= pos; j += groups) acc += (sc[j] * inv) * vb[size_t(j) * KV + d];
-    part[tid] = acc;
-    __syncthreads();
-    if (tid < D) {
-        float o = 0.0f;
-        for (int gg = 0; gg < groups; ++gg) o += part[gg * D + tid];
-        out[size_t(t) * Q + size_t(h) * D + tid] = o;
+    float acc[DL];
+#pragma unroll
+    for (int i = 0; i < DL; ++i) acc[i] = 0.0f;
+    for (int j0 = w; j0 <= pos; j0 += 4 * PB) {
+        float vv[PB][DL], pp[PB];
+#pragma unroll
+        for (int b = 0; b < PB; ++b) {
+            const int j = min(j0 + 4 * b, pos);
+            pp[b] = j0 + 4 * b <= pos ? sc[j] * inv : 0.0f;
+            const float* vr = vb + size_t(j) * KV;
+#pragma unroll
+            for (int i = 0; i < DL; ++i) vv[b][i] = lane + 64 * i < D ? vr[lane + 64 * i] : 0.0f;
+        }
+#pragma unroll
+        for (int b = 0; b < PB; ++b)
+#pragma unroll
+            for (int i = 0; i < DL; ++i) acc[i] += pp[b] * vv[b][i];
     }
+#pragma unroll
+    for (int i = 0; i < DL; ++i) s_o[w][lane + 64 * i] = acc[i];
+    __syncthreads();
+    for (int d = tid; d < D; d += kTh)
+        out[size_t(t) * Q + size_t(h) * D + d] = (s_o[0][d] + s_o[1][d]) + (s_o[2][d] + s_o[3][d]);
 }
 
 // g = silu(g) * u
@@ -186,8 +226,10 @@ hipError_t launch_rope_store(const float* q, const float* k, const float* v, flo
 hipError_t launch_attention(const float* q, const float* kc, const float* vc, float* out, float* scores, int ld,
                             int n_tok, int H, int HKV, int D, int pos0, float scale, hipStream_t s) {
     if (n_tok <= 0 || D <= 0 || D > kTh || HKV <= 0 || H % HKV || ld < pos0 + n_tok) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(attention_kernel, dim3(unsigned(n_tok * H)), dim3(kTh), 0, s, q, kc, vc, out, scores, ld, H,
-                       HKV, D, pos0, scale);
+    const dim3 grid(unsigned(n_tok * H)), block(kTh);
+    if (D <= 64) hipLaunchKernelGGL(attention_kernel<1>, grid, block, 0, s, q, kc, vc, out, scores, ld, H, HKV, D, pos0, scale);
+    else if (D <= 128) hipLaunchKernelGGL(attention_kernel<2>, grid, block, 0, s, q, kc, vc, out, scores, ld, H, HKV, D, pos0, scale);
+    else hipLaunchKernelGGL(attention_kernel<4>, grid, block, 0, s, q, kc, vc, out, scores, ld, H, HKV, D, pos0, scale);
     return hipGetLastError();
 }
 
