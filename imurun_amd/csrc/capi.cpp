@@ -297,7 +297,8 @@ public:
             off += size_t(n_tok) * size_t(n_outs[i]);
         }
         hipError_t e = hipMemcpyAsync(d_x_, x, x_bytes, hipMemcpyHostToDevice, stream_);
-        if (e == hipSuccess) e = run_group(rs.data(), n, static_cast<const float*>(d_x_), n_tok, n_in, n_outs, dys.data());
+        if (e == hipSuccess)
+            e = run_group(rs.data(), n, static_cast<const float*>(d_x_), n_tok, n_in, n_outs, dys.data(), d_act_);
         if (e == hipSuccess) e = hipStreamSynchronize(stream_);
         if (e != hipSuccess) {
             mark_broken(e, "matmul");
@@ -389,58 +390,23 @@ public:
     bool span_forward(float* x, int n_tok, int pos0) {
         std::lock_guard<std::mutex> lk(mu_);
         if (!span_on_ || broken_ || !x || n_tok <= 0 || pos0 < 0 || pos0 + n_tok > sp_.n_ctx) return false;
-        const int E = sp_.n_embd, H = sp_.n_head, HKV = sp_.n_head_kv, D = sp_.head_dim, F = sp_.n_ff;
-        const int Q = H * D, KV = HKV * D, ld = pos0 + n_tok;
+        const int E = sp_.n_embd, Q = sp_.n_head * sp_.head_dim, F = sp_.n_ff;
         std::vector<const Resident*> rs(span_keys_.size());
         for (size_t i = 0; i < rs.size(); ++i) {
             auto it = map_.find(span_keys_[i]);
             if (it == map_.end()) return false;
             rs[i] = &it->second;
         }
-        // scratch: x, xb, q, k, v, q_rot, attn, proj, g, u, scores
-        const size_t T = size_t(n_tok);
-        const size_t sizes[11] = {T * E, T * E, T * Q, T * KV, T * KV, T * Q, T * Q, T * E, T * F, T * F,
-                                  T * H * size_t(ld)};
-        size_t total = 0;
-        for (size_t z : sizes) total += (z * 4 + 255) / 256 * 256;
+        if (n_tok == 1) return span_decode(x, pos0, rs);
         size_t act = 0;
         for (int n_in : {E, Q, F}) act = std::max(act, act_layout(n_tok, n_in).total);
-        if (!act || !reserve(0, act, 0) || !grow_span_ws(total)) return false;
-        float* buf[11];
-        char* b = static_cast<char*>(d_span_ws_);
-        for (int i = 0; i < 11; ++i) {
-            buf[i] = reinterpret_cast<float*>(b);
-            b += (sizes[i] * 4 + 255) / 256 * 256;
-        }
-        float *dx = buf[0], *xb = buf[1], *q = buf[2], *k = buf[3], *v = buf[4], *qr = buf[5], *att = buf[6],
-              *proj = buf[7], *g = buf[8], *u = buf[9], *sc = buf[10];
-        const float scale = sp_.attn_scale > 0.0f ? sp_.attn_scale : 1.0f / std::sqrt(float(D));
-        hipError_t e = hipMemcpyAsync(dx, x, T * E * 4, hipMemcpyHostToDevice, stream_);
-        for (int l = 0; l < sp_.n_layers && e == hipSuccess; ++l) {
-            const Resident* const* W = rs.data() + size_t(7 * l);
-            float* kc = d_kc_ + size_t(l) * sp_.n_ctx * KV;
-            float* vc = d_vc_ + size_t(l) * sp_.n_ctx * KV;
-            const int n_qkv[3] = {Q, KV, KV}, n_e[1] = {E}, n_f[2] = {F, F};
-            float* y_qkv[3] = {q, k, v};
-            float* y_o[1] = {proj};
-            float* y_gu[2] = {g, u};
-            e = launch_rmsnorm(dx, d_norms_ + size_t(2 * l) * E, xb, n_tok, E, sp_.eps, stream_);
-            if (e == hipSuccess) e = run_group(W, 3, xb, n_tok, E, n_qkv, y_qkv);
-            if (e == hipSuccess)
-                e = launch_rope_store(q, k, v, qr, kc, vc, n_tok, H, HKV, D, sp_.rot_dim, sp_.rope_neox != 0, pos0,
-                                      d_cos_, d_sin_, stream_);
-            if (e == hipSuccess) e = launch_attention(qr, kc, vc, att, sc, ld, n_tok, H, HKV, D, pos0, scale, stream_);
-            if (e == hipSuccess) e = run_group(W + 3, 1, att, n_tok, Q, n_e, y_o);
-            if (e == hipSuccess) e = launch_add(dx, proj, T * E, stream_);
-            if (e == hipSuccess) e = launch_rmsnorm(dx, d_norms_ + size_t(2 * l + 1) * E, xb, n_tok, E, sp_.eps, stream_);
-            if (e == hipSuccess) e = run_group(W + 4, 2, xb, n_tok, E, n_f, y_gu);
-            if (e == hipSuccess) e = launch_silu_mul(g, u, T * F, stream_);
-            if (e == hipSuccess) e = run_group(W + 6, 1, g, n_tok, F, n_e, y_o);
-            if (e == hipSuccess) e = launch_add(dx, proj, T * E, stream_);
-        }
+        if (!act || !reserve(0, act, 0) || !grow_span_ws(span_ws_bytes(n_tok, pos0 + n_tok))) return false;
+        SpanBufs B = span_bufs(d_span_ws_, n_tok, pos0 + n_tok);
+        hipError_t e = hipMemcpyAsync(B.x, x, size_t(n_tok) * E * 4, hipMemcpyHostToDevice, stream_);
+        if (e == hipSuccess) e = span_layers(rs, B, n_tok, pos0, nullptr, d_act_);
         // x is written only once everything has run
         if (e == hipSuccess) e = hipStreamSynchronize(stream_);
-        if (e == hipSuccess) e = hipMemcpy(x, dx, T * E * 4, hipMemcpyDeviceToHost);
+        if (e == hipSuccess) e = hipMemcpy(x, B.x, size_t(n_tok) * E * 4, hipMemcpyDeviceToHost);
         if (e != hipSuccess) {
             mark_broken(e, "span_forward");
             return false;
@@ -450,11 +416,135 @@ public:
     }
 
 private:
+    // Device scratch of one span call: x, xb, q, k, v, q_rot, attn, proj, g, u,
+    // attention partials (positions < ld), each 256-byte aligned; then the position.
+    struct SpanBufs {
+        float *x, *xb, *q, *k, *v, *qr, *att, *proj, *g, *u, *sc;
+        int* pos;
+        int ld;
+    };
+    void span_sizes(int n_tok, int ld, size_t (&z)[11]) const {
+        const size_t T = size_t(n_tok), E = size_t(sp_.n_embd), Q = size_t(sp_.n_head) * sp_.head_dim,
+                     KV = size_t(sp_.n_head_kv) * sp_.head_dim, F = size_t(sp_.n_ff);
+        const size_t v[11] = {T * E, T * E, T * Q, T * KV, T * KV, T * Q, T * Q, T * E, T * F, T * F,
+                              attention_scratch_floats(n_tok, sp_.n_head, sp_.head_dim, ld)};
+        for (int i = 0; i < 11; ++i) z[i] = (v[i] * 4 + 255) / 256 * 256;
+    }
+    size_t span_ws_bytes(int n_tok, int ld) const {
+        size_t z[11], total = 256;
+        span_sizes(n_tok, ld, z);
+        for (size_t b : z) total += b;
+        return total;
+    }
+    SpanBufs span_bufs(void* base, int n_tok, int ld) const {
+        size_t z[11];
+        span_sizes(n_tok, ld, z);
+        char* b = static_cast<char*>(base);
+        float* p[11];
+        for (int i = 0; i < 11; ++i) {
+            p[i] = reinterpret_cast<float*>(b);
+            b += z[i];
+        }
+        return SpanBufs{p[0], p[1], p[2], p[3], p[4], p[5], p[6], p[7], p[8], p[9], p[10],
+                        reinterpret_cast<int*>(b), ld};
+    }
+
+    // The span's layers on B.x (model.cpp:1650-1801), asynchronous on stream_;
+    // the position comes from pos_dev when it is given.
+    hipError_t span_layers(const std::vector<const Resident*>& rs, const SpanBufs& B, int n_tok, int pos0,
+                           const int* pos_dev, void* act) {
+        const int E = sp_.n_embd, H = sp_.n_head, HKV = sp_.n_head_kv, D = sp_.head_dim, F = sp_.n_ff;
+        const int Q = H * D, KV = HKV * D;
+        const size_t T = size_t(n_tok);
+        const float scale = sp_.attn_scale > 0.0f ? sp_.attn_scale : 1.0f / std::sqrt(float(D));
+        hipError_t e = hipSuccess;
+        for (int l = 0; l < sp_.n_layers && e == hipSuccess; ++l) {
+            const Resident* const* W = rs.data() + size_t(7 * l);
+            float* kc = d_kc_ + size_t(l) * sp_.n_ctx * KV;
+            float* vc = d_vc_ + size_t(l) * sp_.n_ctx * KV;
+            const int n_qkv[3] = {Q, KV, KV}, n_e[1] = {E}, n_f[2] = {F, F};
+            float* y_qkv[3] = {B.q, B.k, B.v};
+            float* y_o[1] = {B.proj};
+            float* y_gu[2] = {B.g, B.u};
+            e = launch_rmsnorm(B.x, d_norms_ + size_t(2 * l) * E, B.xb, n_tok, E, sp_.eps, stream_);
+            if (e == hipSuccess) e = run_group(W, 3, B.xb, n_tok, E, n_qkv, y_qkv, act);
+            if (e == hipSuccess)
+                e = launch_rope_store(B.q, B.k, B.v, B.qr, kc, vc, n_tok, H, HKV, D, sp_.rot_dim, sp_.rope_neox != 0,
+                                      pos0, d_cos_, d_sin_, stream_, pos_dev);
+            if (e == hipSuccess)
+                e = launch_attention(B.qr, kc, vc, B.att, B.sc, B.ld, n_tok, H, HKV, D, pos0, scale, stream_, pos_dev);
+            if (e == hipSuccess) e = run_group(W + 3, 1, B.att, n_tok, Q, n_e, y_o, act);
+            if (e == hipSuccess) e = launch_add(B.x, B.proj, T * E, stream_);
+            if (e == hipSuccess) e = launch_rmsnorm(B.x, d_norms_ + size_t(2 * l + 1) * E, B.xb, n_tok, E, sp_.eps, stream_);
+            if (e == hipSuccess) e = run_group(W + 4, 2, B.xb, n_tok, E, n_f, y_gu, act);
+            if (e == hipSuccess) e = launch_silu_mul(B.g, B.u, T * F, stream_);
+            if (e == hipSuccess) e = run_group(W + 6, 1, B.g, n_tok, F, n_e, y_o, act);
+            if (e == hipSuccess) e = launch_add(B.x, B.proj, T * E, stream_);
+        }
+        return e;
+    }
+
+    // One decode token: the layer sequence is captured once into a HIP graph
+    // over fixed scratch (its own activation buffer, attention partials for n_ctx,
+    // the position in device memory) and replayed per token, so the launches of
+    // all layers cost one graph launch.
+    bool span_decode(float* x, int pos0, const std::vector<const Resident*>& rs) {
+        const int E = sp_.n_embd;
+        hipError_t e = hipSuccess;
+        // the graph holds the weights' device addresses: rebuild it if any changed
+        std::vector<const void*> devs(rs.size());
+        for (size_t i = 0; i < rs.size(); ++i) devs[i] = rs[i]->dev;
+        if (dec_exec_ && devs != dec_devs_) {
+            (void)hipGraphExecDestroy(dec_exec_);
+            dec_exec_ = nullptr;
+            (void)hipFree(d_dec_);
+            d_dec_ = nullptr;
+        }
+        if (!dec_exec_) {
+            size_t act = 0;
+            for (int n_in : {E, sp_.n_head * sp_.head_dim, sp_.n_ff}) act = std::max(act, act_layout(1, n_in).total);
+            const size_t ws = span_ws_bytes(1, sp_.n_ctx);
+            if (!act || hipMalloc(&d_dec_, ws + act) != hipSuccess) {
+                d_dec_ = nullptr;
+                return false;
+            }
+            dec_ = span_bufs(d_dec_, 1, sp_.n_ctx);
+            void* dact = static_cast<char*>(d_dec_) + ws;
+            hipGraph_t g = nullptr;
+            e = hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal);
+            if (e == hipSuccess) {
+                const hipError_t le = span_layers(rs, dec_, 1, 0, dec_.pos, dact);
+                e = hipStreamEndCapture(stream_, &g);
+                if (e == hipSuccess) e = le;
+            }
+            if (e == hipSuccess) e = hipGraphInstantiate(&dec_exec_, g, nullptr, nullptr, 0);
+            if (g) (void)hipGraphDestroy(g);
+            if (e != hipSuccess) {
+                dec_exec_ = nullptr;
+                mark_broken(e, "span graph");
+                return false;
+            }
+            dec_devs_ = devs;
+        }
+        const int pos_host = pos0;
+        e = hipMemcpyAsync(dec_.x, x, size_t(E) * 4, hipMemcpyHostToDevice, stream_);
+        if (e == hipSuccess) e = hipMemcpyAsync(dec_.pos, &pos_host, sizeof(int), hipMemcpyHostToDevice, stream_);
+        if (e == hipSuccess) e = hipGraphLaunch(dec_exec_, stream_);
+        if (e == hipSuccess) e = hipStreamSynchronize(stream_);
+        if (e == hipSuccess) e = hipMemcpy(x, dec_.x, size_t(E) * 4, hipMemcpyDeviceToHost);
+        if (e != hipSuccess) {
+            mark_broken(e, "span_forward");
+            return false;
+        }
+        ++served_;
+        return true;
+    }
+
     // The matmuls of n resident tensors on one device input (f32 [n_tok][n_in]):
     // y_i [n_tok][n_out_i] (device). Asynchronous on stream_; d_act_ must hold
     // act_layout(n_tok, n_in).total bytes.
     hipError_t run_group(const Resident* const* rs, int n, const float* dx, int n_tok, int n_in, const int* n_outs,
-                         float* const* dys) {
+                         float* const* dys, void* act) {
         bool any_int8 = false;
         for (int i = 0; i < n; ++i) any_int8 = any_int8 || int8_type(rs[i]->layout.type);
         // one token, one type: each workgroup quantizes x itself (one launch)
@@ -488,8 +578,7 @@ private:
         }
         hipError_t e = hipSuccess;
         if (!fused && any_int8)
-            e = launch_quantize(dx, n_tok, n_in, n_in, d_act_, nullptr, nullptr, stream_,
-                                planes_for_tokens(n_tok, n_in));
+            e = launch_quantize(dx, n_tok, n_in, n_in, act, nullptr, nullptr, stream_, planes_for_tokens(n_tok, n_in));
         // tensors of one K-quant type go out as one grouped launch when the batch is GEMM-sized
         bool one_group = n <= kGemmGroupMax;
         for (int i = 0; i < n; ++i)
@@ -512,13 +601,13 @@ private:
                 Ls[i] = rs[size_t(i)]->layout;
                 ldy[i] = n_outs[i];
             }
-            e = launch_gemm_group(n, ws, Ls, d_act_, n_tok, dys, ldy, stream_);
+            e = launch_gemm_group(n, ws, Ls, act, n_tok, dys, ldy, stream_);
         } else {
             for (int i = 0; i < n && e == hipSuccess; ++i) {
                 const Resident& r = *rs[i];
                 e = f32path_type(r.layout.type)
                         ? launch_dq_matmul(r.layout.type, r.dev, dx, n_tok, n_in, n_outs[i], dys[i], stream_)
-                        : dispatch_matmul(r.dev, r.layout, d_act_, n_tok, dys[i], n_outs[i], stream_);
+                        : dispatch_matmul(r.dev, r.layout, act, n_tok, dys[i], n_outs[i], stream_);
             }
         }
         return e;
@@ -535,6 +624,10 @@ private:
     }
 
     void span_free() {
+        if (dec_exec_) (void)hipGraphExecDestroy(dec_exec_);
+        dec_exec_ = nullptr;
+        if (d_dec_) (void)hipFree(d_dec_);
+        d_dec_ = nullptr;
         if (d_span_fixed_) (void)hipFree(d_span_fixed_);
         d_span_fixed_ = nullptr;
         span_keys_.clear();
@@ -593,6 +686,11 @@ private:
     float *d_norms_ = nullptr, *d_cos_ = nullptr, *d_sin_ = nullptr, *d_kc_ = nullptr, *d_vc_ = nullptr;
     void* d_span_ws_ = nullptr;
     size_t cap_span_ws_ = 0;
+    // decode graph over fixed scratch (built at the first one-token call)
+    hipGraphExec_t dec_exec_ = nullptr;
+    void* d_dec_ = nullptr;
+    SpanBufs dec_{};
+    std::vector<const void*> dec_devs_;
 };
 
 }  // namespace

@@ -141,14 +141,18 @@ hipError_t launch_gemm_group(int n, const void* const* ws, const WeightLayout* W
 
 // Layer-span steps (span.hip): rmsnorm per token row; RoPE of q into q_out and
 // of k into the KV-cache rows pos0.. (with v); causal GQA attention per
-// (token, head) with a scores buffer of n_tok * H rows of ld >= pos0 + n_tok
-// floats; g = silu(g) * u; x += y.
+// (token, head), split over chunks of positions < ld (ld >= pos0 + n_tok); g = silu(g) * u; x += y. With pos_dev, RoPE and attention read the
+// first position from device memory instead of pos0 (a graph replayed for every
+// decode position; the caller keeps pos_dev[0] + n_tok <= the cache and ld).
 hipError_t launch_rmsnorm(const float* x, const float* w, float* out, int n_tok, int n, float eps, hipStream_t s);
 hipError_t launch_rope_store(const float* q, const float* k, const float* v, float* q_out, float* kc, float* vc,
                              int n_tok, int H, int HKV, int D, int rot_dim, bool neox, int pos0, const float* cosv,
-                             const float* sinv, hipStream_t s);
-hipError_t launch_attention(const float* q, const float* kc, const float* vc, float* out, float* scores, int ld,
-                            int n_tok, int H, int HKV, int D, int pos0, float scale, hipStream_t s);
+                             const float* sinv, hipStream_t s, const int* pos_dev = nullptr);
+// `part` holds attention_scratch_floats(n_tok, H, D, ld) floats.
+size_t attention_scratch_floats(int n_tok, int H, int D, int ld);
+hipError_t launch_attention(const float* q, const float* kc, const float* vc, float* out, float* part, int ld,
+                            int n_tok, int H, int HKV, int D, int pos0, float scale, hipStream_t s,
+                            const int* pos_dev = nullptr);
 hipError_t launch_silu_mul(float* g, const float* u, size_t n, hipStream_t s);
 hipError_t launch_add(float* x, const float* y, size_t n, hipStream_t s);
 

@@ -7,7 +7,7 @@
 //   RoPE + KV    ops.cpp:126-152 (table rotation, neox or adjacent pairs) and the
 //                KV-cache store of model.cpp:1726-1734
 //   attention    ops.cpp:303-357 (causal, GQA head groups, max-subtracted exp,
-//                p = e * (1 / sum), o = sum_j p_j v_j)
+//                softmax-weighted sum of V; split over position chunks)
 //   silu * up    ops.cpp:25-30, model.cpp:1504-1508
 //   residual add model.cpp:1772-1776, :1797-1801
 // The file is compiled without floating-point contraction, so every
@@ -55,7 +55,15 @@ __global__ __launch_bounds__(kTh) void rmsnorm_kernel(const float* __restrict__ 
     const float* xr = x + size_t(blockIdx.x) * n;
     float* orow = out + size_t(blockIdx.x) * n;
     double s = 0.0;
-    for (int i = threadIdx.x; i < n; i += kTh) s += double(xr[i]) * double(xr[i]);
+    if ((n & 3) == 0) {  // 16-byte loads, four in flight per thread
+        for (int i = 4 * threadIdx.x; i < n; i += 4 * kTh) {
+            const float4 v = *reinterpret_cast<const float4*>(xr + i);
+            s += double(v.x) * double(v.x) + double(v.y) * double(v.y) + double(v.z) * double(v.z) +
+                 double(v.w) * double(v.w);
+        }
+    } else {
+        for (int i = threadIdx.x; i < n; i += kTh) s += double(xr[i]) * double(xr[i]);
+    }
     const double sum = block_sum_d(s, red);
     const float scale = 1.0f / sqrtf(float(sum / n) + eps);
     for (int i = threadIdx.x; i < n; i += kTh) orow[i] = xr[i] * scale * w[i];
@@ -76,117 +84,159 @@ __device__ __forceinline__ float rope_elem(const float* __restrict__ src, int f,
     return (d & 1) ? x0 * s[i] + x1 * c[i] : x0 * c[i] - x1 * s[i];
 }
 
-// one workgroup per token t (position pos0 + t): q_out = rope(q), the cache
-// rows of the position get rope(k) and v
+// one workgroup per (token t, head): q heads first, then k heads; q_out =
+// rope(q), the cache rows of position pos0 + t get rope(k) and v
 __global__ __launch_bounds__(kTh) void rope_store_kernel(const float* __restrict__ q, const float* __restrict__ k,
                                                          const float* __restrict__ v, float* __restrict__ q_out,
                                                          float* __restrict__ kc, float* __restrict__ vc, int Q,
                                                          int KV, int D, int half, int neox, int pos0,
+                                                         const int* __restrict__ pos_dev,
                                                          const float* __restrict__ cosv,
                                                          const float* __restrict__ sinv) {
-    const int t = blockIdx.x, pos = pos0 + t;
+    if (pos_dev) pos0 = *pos_dev;
+    const int t = blockIdx.x, hh = blockIdx.y, pos = pos0 + t, H = Q / D;
     const float* c = cosv + size_t(pos) * half;
     const float* s = sinv + size_t(pos) * half;
-    const float* qr = q + size_t(t) * Q;
-    const float* kr = k + size_t(t) * KV;
-    const float* vr = v + size_t(t) * KV;
-    for (int f = threadIdx.x; f < Q; f += kTh) q_out[size_t(t) * Q + f] = rope_elem(qr, f, D, half, neox, c, s);
-    for (int f = threadIdx.x; f < KV; f += kTh) {
-        kc[size_t(pos) * KV + f] = rope_elem(kr, f, D, half, neox, c, s);
-        vc[size_t(pos) * KV + f] = vr[f];
+    if (hh < H) {
+        const float* qr = q + size_t(t) * Q;
+        for (int f = hh * D + threadIdx.x; f < (hh + 1) * D; f += kTh)
+            q_out[size_t(t) * Q + f] = rope_elem(qr, f, D, half, neox, c, s);
+    } else {
+        const float* kr = k + size_t(t) * KV;
+        const float* vr = v + size_t(t) * KV;
+        for (int f = (hh - H) * D + threadIdx.x; f < (hh - H + 1) * D; f += kTh) {
+            kc[size_t(pos) * KV + f] = rope_elem(kr, f, D, half, neox, c, s);
+            vc[size_t(pos) * KV + f] = vr[f];
+        }
     }
 }
 
-// One workgroup (four wavefronts) per (token, head). Lanes run over the
-// head's D values (DL = D / 64 per lane, rounded up; lanes past D hold
-// zeros), so every K or V row is one coalesced load; wavefront w takes the
-// positions j = w, w + 4, ... up to pos.
-//   scores: per position a lane-partial dot, summed over the wavefront with
-//           xor shuffles, scaled, kept in the workgroup's row of `scores`;
-//   softmax: max and sum over the workgroup; p_j = e_j * (1 / sum);
-//   o:      each wavefront sums p_j v_j over its positions in registers; the
-//           four partial vectors are added in LDS.
-// Needs D <= 256.
+// Attention in two steps, split over the positions so that one decode token
+// still spreads over many workgroups (flash-decoding):
+//   attn_part_kernel: one workgroup (four wavefronts) per (token, head, chunk
+//     of kCh positions). Lanes run over the head's D values (DL per lane), so
+//     each K or V row is one coalesced load; every wavefront issues the loads
+//     of its kCh / 4 positions before using them. It writes the chunk's max
+//     score m, its sum l of exp(s - m), and o = sum exp(s - m) v.
+//   attn_combine_kernel: one workgroup per (token, head): M = max m,
+//     L = sum l exp(m - M), out = (sum o exp(m - M)) * (1 / L).
+// Chunks that start past the token's position hold m = -inf, l = 0, o = 0.
+// Mathematically FISH's single-pass softmax (ops.cpp:331-350); the rounding
+// order differs. Needs D <= 256.
+constexpr int kCh = 64;
+
 template <int DL>
-__global__ __launch_bounds__(kTh) void attention_kernel(const float* __restrict__ q, const float* __restrict__ kc,
-                                                        const float* __restrict__ vc, float* __restrict__ out,
-                                                        float* __restrict__ scores, int ld, int H, int HKV, int D,
-                                                        int pos0, float scale) {
-    __shared__ float red[kTh];
+__global__ __launch_bounds__(kTh) void attn_part_kernel(const float* __restrict__ q, const float* __restrict__ kc,
+                                                        const float* __restrict__ vc, float* __restrict__ part,
+                                                        int S, int H, int HKV, int D, int pos0,
+                                                        const int* __restrict__ pos_dev, float scale) {
+    constexpr int PB = kCh / 4;
+    __shared__ float s_e[kCh];
     __shared__ float s_o[4][64 * DL];
-    const int item = blockIdx.x, t = item / H, h = item % H;
+    __shared__ float s_ml[2];
+    if (pos_dev) pos0 = *pos_dev;
+    const int item = blockIdx.x, chunk = blockIdx.y, t = item / H, h = item % H;
     const int pos = pos0 + t, kvh = h / (H / HKV), KV = HKV * D, Q = H * D;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int j0 = chunk * kCh;
+    float* pp = part + (size_t(item) * S + chunk) * size_t(D + 2);
+    if (j0 > pos) {  // uniform over the workgroup
+        for (int d = tid; d < D; d += kTh) pp[d] = 0.0f;
+        if (tid == 0) {
+            pp[D] = -INFINITY;
+            pp[D + 1] = 0.0f;
+        }
+        return;
+    }
+    const int jn = min(pos, j0 + kCh - 1);
     float qv[DL];
 #pragma unroll
-    for (int i = 0; i < DL; ++i) {
-        const int d = lane + 64 * i;
-        qv[i] = d < D ? q[size_t(t) * Q + size_t(h) * D + d] : 0.0f;
-    }
-    float* sc = scores + size_t(item) * ld;
+    for (int i = 0; i < DL; ++i) qv[i] = lane + 64 * i < D ? q[size_t(t) * Q + size_t(h) * D + lane + 64 * i] : 0.0f;
     const float* kb = kc + size_t(kvh) * D;
     const float* vb = vc + size_t(kvh) * D;
 
-    // PB positions per wavefront step, all their row loads issued before the
-    // first use (clamped to pos: unconditional loads, extra positions dropped)
-    constexpr int PB = 16;
-    float m = -INFINITY;
-    for (int j0 = w; j0 <= pos; j0 += 4 * PB) {
-        float kv[PB][DL];
+    // scores of positions j0 + w + 4 b
+    float kv[PB][DL];
 #pragma unroll
-        for (int b = 0; b < PB; ++b) {
-            const float* kr = kb + size_t(min(j0 + 4 * b, pos)) * KV;
+    for (int b = 0; b < PB; ++b) {
+        const float* kr = kb + size_t(min(j0 + w + 4 * b, jn)) * KV;
 #pragma unroll
-            for (int i = 0; i < DL; ++i) kv[b][i] = lane + 64 * i < D ? kr[lane + 64 * i] : 0.0f;
-        }
+        for (int i = 0; i < DL; ++i) kv[b][i] = lane + 64 * i < D ? kr[lane + 64 * i] : 0.0f;
+    }
 #pragma unroll
-        for (int b = 0; b < PB; ++b) {
-            float part = 0.0f;
+    for (int b = 0; b < PB; ++b) {
+        float sum = 0.0f;
 #pragma unroll
-            for (int i = 0; i < DL; ++i) part += qv[i] * kv[b][i];
+        for (int i = 0; i < DL; ++i) sum += qv[i] * kv[b][i];
 #pragma unroll
-            for (int off = 32; off > 0; off >>= 1) part += __shfl_xor(part, off);
-            const float sv = part * scale;
-            const int j = j0 + 4 * b;
-            if (j <= pos) {
-                if (lane == 0) sc[j] = sv;
-                m = fmaxf(m, sv);
-            }
+        for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+        if (lane == 0) s_e[w + 4 * b] = j0 + w + 4 * b <= jn ? sum * scale : -INFINITY;
+    }
+    __syncthreads();
+    if (w == 0) {
+        float m = s_e[lane];
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+        const float e = lane <= jn - j0 ? expf(s_e[lane] - m) : 0.0f;
+        float l = e;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) l += __shfl_xor(l, off);
+        s_e[lane] = e;
+        if (lane == 0) {
+            s_ml[0] = m;
+            s_ml[1] = l;
         }
     }
-    const float mx = block_reduce_f(m, red, true);  // its barriers also order the sc writes
-    float sum = 0.0f;
-    for (int j = tid; j <= pos; j += kTh) {
-        const float e = expf(sc[j] - mx);
-        sc[j] = e;
-        sum += e;
+    __syncthreads();
+    float vv[PB][DL];
+#pragma unroll
+    for (int b = 0; b < PB; ++b) {
+        const float* vr = vb + size_t(min(j0 + w + 4 * b, jn)) * KV;
+#pragma unroll
+        for (int i = 0; i < DL; ++i) vv[b][i] = lane + 64 * i < D ? vr[lane + 64 * i] : 0.0f;
     }
-    const float tot = block_reduce_f(sum, red, false);
-    const float inv = tot > 0.0f ? 1.0f / tot : 0.0f;
-
     float acc[DL];
 #pragma unroll
     for (int i = 0; i < DL; ++i) acc[i] = 0.0f;
-    for (int j0 = w; j0 <= pos; j0 += 4 * PB) {
-        float vv[PB][DL], pp[PB];
 #pragma unroll
-        for (int b = 0; b < PB; ++b) {
-            const int j = min(j0 + 4 * b, pos);
-            pp[b] = j0 + 4 * b <= pos ? sc[j] * inv : 0.0f;
-            const float* vr = vb + size_t(j) * KV;
+    for (int b = 0; b < PB; ++b) {
+        const float e = s_e[w + 4 * b];  // 0 past jn
 #pragma unroll
-            for (int i = 0; i < DL; ++i) vv[b][i] = lane + 64 * i < D ? vr[lane + 64 * i] : 0.0f;
-        }
-#pragma unroll
-        for (int b = 0; b < PB; ++b)
-#pragma unroll
-            for (int i = 0; i < DL; ++i) acc[i] += pp[b] * vv[b][i];
+        for (int i = 0; i < DL; ++i) acc[i] += e * vv[b][i];
     }
 #pragma unroll
     for (int i = 0; i < DL; ++i) s_o[w][lane + 64 * i] = acc[i];
     __syncthreads();
-    for (int d = tid; d < D; d += kTh)
-        out[size_t(t) * Q + size_t(h) * D + d] = (s_o[0][d] + s_o[1][d]) + (s_o[2][d] + s_o[3][d]);
+    for (int d = tid; d < D; d += kTh) pp[d] = (s_o[0][d] + s_o[1][d]) + (s_o[2][d] + s_o[3][d]);
+    if (tid == 0) {
+        pp[D] = s_ml[0];
+        pp[D + 1] = s_ml[1];
+    }
+}
+
+__global__ __launch_bounds__(kTh) void attn_combine_kernel(const float* __restrict__ part, float* __restrict__ out,
+                                                           int S, int H, int D) {
+    __shared__ float red[kTh];
+    const int item = blockIdx.x, t = item / H, h = item % H, tid = threadIdx.x;
+    const float* pp = part + size_t(item) * S * size_t(D + 2);
+    float m = -INFINITY;
+    for (int c = tid; c < S; c += kTh) m = fmaxf(m, pp[size_t(c) * (D + 2) + D]);
+    const float M = block_reduce_f(m, red, true);
+    float l = 0.0f;
+    for (int c = tid; c < S; c += kTh) {
+        const float mc = pp[size_t(c) * (D + 2) + D];
+        l += mc == -INFINITY ? 0.0f : pp[size_t(c) * (D + 2) + D + 1] * expf(mc - M);
+    }
+    const float L = block_reduce_f(l, red, false);
+    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+    for (int d = tid; d < D; d += kTh) {
+        float o = 0.0f;
+        for (int c = 0; c < S; ++c) {
+            const float mc = pp[size_t(c) * (D + 2) + D];
+            if (mc != -INFINITY) o += pp[size_t(c) * (D + 2) + d] * expf(mc - M);
+        }
+        out[size_t(t) * H * D + size_t(h) * D + d] = o * inv;
+    }
 }
 
 // g = silu(g) * u
@@ -216,21 +266,31 @@ hipError_t launch_rmsnorm(const float* x, const float* w, float* out, int n_tok,
 
 hipError_t launch_rope_store(const float* q, const float* k, const float* v, float* q_out, float* kc, float* vc,
                              int n_tok, int H, int HKV, int D, int rot_dim, bool neox, int pos0, const float* cosv,
-                             const float* sinv, hipStream_t s) {
+                             const float* sinv, hipStream_t s, const int* pos_dev) {
     if (n_tok <= 0 || H <= 0 || HKV <= 0 || D <= 0 || rot_dim < 0 || rot_dim > D || rot_dim % 2) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(rope_store_kernel, dim3(unsigned(n_tok)), dim3(kTh), 0, s, q, k, v, q_out, kc, vc, H * D,
-                       HKV * D, D, rot_dim / 2, neox ? 1 : 0, pos0, cosv, sinv);
+    hipLaunchKernelGGL(rope_store_kernel, dim3(unsigned(n_tok), unsigned(H + HKV)), dim3(kTh), 0, s, q, k, v, q_out, kc, vc, H * D,
+                       HKV * D, D, rot_dim / 2, neox ? 1 : 0, pos0, pos_dev, cosv, sinv);
     return hipGetLastError();
 }
 
-hipError_t launch_attention(const float* q, const float* kc, const float* vc, float* out, float* scores, int ld,
-                            int n_tok, int H, int HKV, int D, int pos0, float scale, hipStream_t s) {
+hipError_t launch_attention(const float* q, const float* kc, const float* vc, float* out, float* part, int ld,
+                            int n_tok, int H, int HKV, int D, int pos0, float scale, hipStream_t s,
+                            const int* pos_dev) {
     if (n_tok <= 0 || D <= 0 || D > kTh || HKV <= 0 || H % HKV || ld < pos0 + n_tok) return hipErrorInvalidValue;
-    const dim3 grid(unsigned(n_tok * H)), block(kTh);
-    if (D <= 64) hipLaunchKernelGGL(attention_kernel<1>, grid, block, 0, s, q, kc, vc, out, scores, ld, H, HKV, D, pos0, scale);
-    else if (D <= 128) hipLaunchKernelGGL(attention_kernel<2>, grid, block, 0, s, q, kc, vc, out, scores, ld, H, HKV, D, pos0, scale);
-    else hipLaunchKernelGGL(attention_kernel<4>, grid, block, 0, s, q, kc, vc, out, scores, ld, H, HKV, D, pos0, scale);
+    const int S = (ld + kCh - 1) / kCh;
+    const dim3 grid(unsigned(n_tok * H), unsigned(S)), block(kTh);
+    if (D <= 64)
+        hipLaunchKernelGGL(attn_part_kernel<1>, grid, block, 0, s, q, kc, vc, part, S, H, HKV, D, pos0, pos_dev, scale);
+    else if (D <= 128)
+        hipLaunchKernelGGL(attn_part_kernel<2>, grid, block, 0, s, q, kc, vc, part, S, H, HKV, D, pos0, pos_dev, scale);
+    else
+        hipLaunchKernelGGL(attn_part_kernel<4>, grid, block, 0, s, q, kc, vc, part, S, H, HKV, D, pos0, pos_dev, scale);
+    hipLaunchKernelGGL(attn_combine_kernel, dim3(unsigned(n_tok * H)), block, 0, s, part, out, S, H, D);
     return hipGetLastError();
+}
+
+size_t attention_scratch_floats(int n_tok, int H, int D, int ld) {
+    return size_t(n_tok) * H * size_t((ld + kCh - 1) / kCh) * size_t(D + 2);
 }
 
 hipError_t launch_silu_mul(float* g, const float* u, size_t n, hipStream_t s) {

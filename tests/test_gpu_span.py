@@ -7,9 +7,11 @@ as FISH's matmul_batch on int8-quantized activations (the oracle's
 matmul_f32), RoPE from the same tables (ops.cpp:126-152, neox pairs here;
 the adjacent-pair form is covered by the whole-model test), the KV cache,
 causal GQA attention in float64 (ops.cpp:303-357), SiLU·up and the residual
-adds. Calls: a 37-token prefill (batch kernel), one decode token (fused
-GEMV), then a 100-token prefill at position 38 (GEMM), so later calls attend
-over the cache the earlier ones wrote.
+adds. Calls: a 37-token prefill (batch kernel), three decode tokens (fused
+GEMVs; the span replays one captured HIP graph per token, with the position
+in device memory), a 100-token prefill (GEMM), then one more decode token,
+so later calls attend over the cache the earlier ones wrote and every graph
+replay is checked.
 
 Bar: the layer's update x_out - x_in within 5e-3 of its L-inf norm. The
 device rounds rmsnorm and attention in another order than FISH, so an
@@ -106,7 +108,7 @@ def test_span_layer_matches_fish_forward(oracle, rot_dim):
     ref = RefLayer(oracle, packed, an, fn, cos, sin)
     try:
         pos0 = 0
-        for i, n in enumerate((37, 1, 100)):
+        for i, n in enumerate((37, 1, 1, 1, 100, 1)):
             x = normal(650 + i, (n, E), 1.0)
             want = ref.forward(x, pos0)
             got = x.copy()
