@@ -458,6 +458,8 @@ private:
         const size_t T = size_t(n_tok);
         const float scale = sp_.attn_scale > 0.0f ? sp_.attn_scale : 1.0f / std::sqrt(float(D));
         hipError_t e = hipSuccess;
+        // the FFN residual of layer l - 1 is added by layer l's first rmsnorm
+        const float* pending = nullptr;
         for (int l = 0; l < sp_.n_layers && e == hipSuccess; ++l) {
             const Resident* const* W = rs.data() + size_t(7 * l);
             float* kc = d_kc_ + size_t(l) * sp_.n_ctx * KV;
@@ -466,7 +468,7 @@ private:
             float* y_qkv[3] = {B.q, B.k, B.v};
             float* y_o[1] = {B.proj};
             float* y_gu[2] = {B.g, B.u};
-            e = launch_rmsnorm(B.x, d_norms_ + size_t(2 * l) * E, B.xb, n_tok, E, sp_.eps, stream_);
+            e = launch_rmsnorm(B.x, pending, d_norms_ + size_t(2 * l) * E, B.xb, n_tok, E, sp_.eps, stream_);
             if (e == hipSuccess) e = run_group(W, 3, B.xb, n_tok, E, n_qkv, y_qkv, act);
             if (e == hipSuccess)
                 e = launch_rope_store(B.q, B.k, B.v, B.qr, kc, vc, n_tok, H, HKV, D, sp_.rot_dim, sp_.rope_neox != 0,
@@ -474,13 +476,14 @@ private:
             if (e == hipSuccess)
                 e = launch_attention(B.qr, kc, vc, B.att, B.sc, B.ld, n_tok, H, HKV, D, pos0, scale, stream_, pos_dev);
             if (e == hipSuccess) e = run_group(W + 3, 1, B.att, n_tok, Q, n_e, y_o, act);
-            if (e == hipSuccess) e = launch_add(B.x, B.proj, T * E, stream_);
-            if (e == hipSuccess) e = launch_rmsnorm(B.x, d_norms_ + size_t(2 * l + 1) * E, B.xb, n_tok, E, sp_.eps, stream_);
+            if (e == hipSuccess)
+                e = launch_rmsnorm(B.x, B.proj, d_norms_ + size_t(2 * l + 1) * E, B.xb, n_tok, E, sp_.eps, stream_);
             if (e == hipSuccess) e = run_group(W + 4, 2, B.xb, n_tok, E, n_f, y_gu, act);
             if (e == hipSuccess) e = launch_silu_mul(B.g, B.u, T * F, stream_);
             if (e == hipSuccess) e = run_group(W + 6, 1, B.g, n_tok, F, n_e, y_o, act);
-            if (e == hipSuccess) e = launch_add(B.x, B.proj, T * E, stream_);
+            pending = B.proj;
         }
+        if (e == hipSuccess) e = launch_add(B.x, pending, T * E, stream_);
         return e;
     }
 

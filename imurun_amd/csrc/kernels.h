@@ -144,7 +144,9 @@ hipError_t launch_gemm_group(int n, const void* const* ws, const WeightLayout* W
 // (token, head), split over chunks of positions < ld (ld >= pos0 + n_tok); g = silu(g) * u; x += y. With pos_dev, RoPE and attention read the
 // first position from device memory instead of pos0 (a graph replayed for every
 // decode position; the caller keeps pos_dev[0] + n_tok <= the cache and ld).
-hipError_t launch_rmsnorm(const float* x, const float* w, float* out, int n_tok, int n, float eps, hipStream_t s);
+// rmsnorm with y != nullptr first adds y into x (x += y, written back).
+hipError_t launch_rmsnorm(float* x, const float* y, const float* w, float* out, int n_tok, int n, float eps,
+                          hipStream_t s);
 hipError_t launch_rope_store(const float* q, const float* k, const float* v, float* q_out, float* kc, float* vc,
                              int n_tok, int H, int HKV, int D, int rot_dim, bool neox, int pos0, const float* cosv,
                              const float* sinv, hipStream_t s, const int* pos_dev = nullptr);

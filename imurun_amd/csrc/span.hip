@@ -9,7 +9,7 @@
 //   attention    ops.cpp:303-357 (causal, GQA head groups, max-subtracted exp,
 //                softmax-weighted sum of V; split over position chunks)
 //   silu * up    ops.cpp:25-30, model.cpp:1504-1508
-//   residual add model.cpp:1772-1776, :1797-1801
+//   residual add model.cpp:1772-1776, :1797-1801 (fused into the next rmsnorm)
 // The file is compiled without floating-point contraction, so every
 // expression rounds as FISH's baseline x86-64 build does; exp is the device's
 // expf, within a few ulp of the C library's.
@@ -22,11 +22,13 @@ namespace {
 
 constexpr int kTh = 256;
 
+constexpr int kNormTh = 1024;
+
 __device__ __forceinline__ double block_sum_d(double v, double* red) {
     const int tid = threadIdx.x;
     red[tid] = v;
     __syncthreads();
-    for (int s = kTh / 2; s > 0; s >>= 1) {
+    for (int s = kNormTh / 2; s > 0; s >>= 1) {
         if (tid < s) red[tid] += red[tid + s];
         __syncthreads();
     }
@@ -48,25 +50,28 @@ __device__ __forceinline__ float block_reduce_f(float v, float* red, bool is_max
     return r;
 }
 
-// one workgroup per token
-__global__ __launch_bounds__(kTh) void rmsnorm_kernel(const float* __restrict__ x, const float* __restrict__ w,
-                                                      float* __restrict__ out, int n, float eps) {
-    __shared__ double red[kTh];
-    const float* xr = x + size_t(blockIdx.x) * n;
+// one workgroup of kNormTh threads per token; with y, first x += y (the
+// residual add, written back to x), then out = rmsnorm(x)
+__global__ __launch_bounds__(kNormTh) void rmsnorm_kernel(float* __restrict__ x, const float* __restrict__ y,
+                                                          const float* __restrict__ w, float* __restrict__ out, int n,
+                                                          float eps) {
+    __shared__ double red[kNormTh];
+    float* xr = x + size_t(blockIdx.x) * n;
+    const float* yr = y ? y + size_t(blockIdx.x) * n : nullptr;
     float* orow = out + size_t(blockIdx.x) * n;
     double s = 0.0;
-    if ((n & 3) == 0) {  // 16-byte loads, four in flight per thread
-        for (int i = 4 * threadIdx.x; i < n; i += 4 * kTh) {
-            const float4 v = *reinterpret_cast<const float4*>(xr + i);
-            s += double(v.x) * double(v.x) + double(v.y) * double(v.y) + double(v.z) * double(v.z) +
-                 double(v.w) * double(v.w);
+#pragma unroll 4
+    for (int i = threadIdx.x; i < n; i += kNormTh) {
+        float v = xr[i];
+        if (yr) {
+            v = v + yr[i];
+            xr[i] = v;
         }
-    } else {
-        for (int i = threadIdx.x; i < n; i += kTh) s += double(xr[i]) * double(xr[i]);
+        s += double(v) * double(v);
     }
     const double sum = block_sum_d(s, red);
     const float scale = 1.0f / sqrtf(float(sum / n) + eps);
-    for (int i = threadIdx.x; i < n; i += kTh) orow[i] = xr[i] * scale * w[i];
+    for (int i = threadIdx.x; i < n; i += kNormTh) orow[i] = xr[i] * scale * w[i];
 }
 
 // The rotated value of element f of a row of heads of D values (ops.cpp:126-152).
@@ -217,26 +222,35 @@ __global__ __launch_bounds__(kTh) void attn_part_kernel(const float* __restrict_
 __global__ __launch_bounds__(kTh) void attn_combine_kernel(const float* __restrict__ part, float* __restrict__ out,
                                                            int S, int H, int D) {
     __shared__ float red[kTh];
+    __shared__ float s_w[kTh];
     const int item = blockIdx.x, t = item / H, h = item % H, tid = threadIdx.x;
-    const float* pp = part + size_t(item) * S * size_t(D + 2);
+    const size_t st = size_t(D + 2);
+    const float* pp = part + size_t(item) * S * st;
     float m = -INFINITY;
-    for (int c = tid; c < S; c += kTh) m = fmaxf(m, pp[size_t(c) * (D + 2) + D]);
+    for (int c = tid; c < S; c += kTh) m = fmaxf(m, pp[size_t(c) * st + D]);
     const float M = block_reduce_f(m, red, true);
-    float l = 0.0f;
-    for (int c = tid; c < S; c += kTh) {
-        const float mc = pp[size_t(c) * (D + 2) + D];
-        l += mc == -INFINITY ? 0.0f : pp[size_t(c) * (D + 2) + D + 1] * expf(mc - M);
+    float l = 0.0f, o = 0.0f;
+    for (int c0 = 0; c0 < S; c0 += kTh) {
+        const int c = c0 + tid;
+        float wc = 0.0f;
+        if (c < S) {
+            const float mc = pp[size_t(c) * st + D];
+            wc = mc == -INFINITY ? 0.0f : expf(mc - M);
+            l += pp[size_t(c) * st + D + 1] * wc;
+        }
+        s_w[tid] = wc;
+        __syncthreads();
+        const int nc = min(kTh, S - c0);
+        if (tid < D) {
+            const float* pc = pp + size_t(c0) * st + tid;
+#pragma unroll 8
+            for (int cc = 0; cc < nc; ++cc) o += pc[size_t(cc) * st] * s_w[cc];
+        }
+        __syncthreads();
     }
     const float L = block_reduce_f(l, red, false);
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-    for (int d = tid; d < D; d += kTh) {
-        float o = 0.0f;
-        for (int c = 0; c < S; ++c) {
-            const float mc = pp[size_t(c) * (D + 2) + D];
-            if (mc != -INFINITY) o += pp[size_t(c) * (D + 2) + d] * expf(mc - M);
-        }
-        out[size_t(t) * H * D + size_t(h) * D + d] = o * inv;
-    }
+    if (tid < D) out[size_t(t) * H * D + size_t(h) * D + tid] = o * inv;
 }
 
 // g = silu(g) * u
@@ -258,9 +272,10 @@ unsigned blocks_for(size_t n) { return unsigned((n + kTh - 1) / kTh); }
 
 }  // namespace
 
-hipError_t launch_rmsnorm(const float* x, const float* w, float* out, int n_tok, int n, float eps, hipStream_t s) {
+hipError_t launch_rmsnorm(float* x, const float* y, const float* w, float* out, int n_tok, int n, float eps,
+                          hipStream_t s) {
     if (n_tok <= 0 || n <= 0) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(rmsnorm_kernel, dim3(unsigned(n_tok)), dim3(kTh), 0, s, x, w, out, n, eps);
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(unsigned(n_tok)), dim3(kNormTh), 0, s, x, y, w, out, n, eps);
     return hipGetLastError();
 }
 
