@@ -266,12 +266,15 @@ __global__ __launch_bounds__(64 * kGemvXWaves) void gemv_x_kernel(GemvXGroup G, 
         cv[k] = c < groups;
         cg[k] = cv[k] ? c : groups - 1;
     }
+    // Q4_0 rows of up to 128 groups: non-temporal code loads (5 % faster on the
+    // 2 x 14336x4096 gate+up; slower on longer rows and on the K-quants)
+    constexpr bool NT = T == kQ4_0 && MAXC <= 2;
     Frag f[RB][MAXC];
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
         const int row = min(row_base + rb * RPP, n_out - 1);
 #pragma unroll
-        for (int k = 0; k < MAXC; ++k) f[rb][k] = load_group_raw<T, true>(W, row, cg[k], n_in, lane);
+        for (int k = 0; k < MAXC; ++k) f[rb][k] = load_group_raw<T, true, NT>(W, row, cg[k], n_in, lane);
     }
 
     // every load is issued before the quantization's first use of x

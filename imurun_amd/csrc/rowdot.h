@@ -31,7 +31,21 @@ struct Frag {
 // sub + LPR, ... with LPR a multiple of 8): the meta is loaded as one dword
 // per lane and assembled with four shuffles in finish_group, so a wavefront
 // moves 4 instead of 16 meta bytes per lane.
-template <uint32_t T, bool WAVE>
+typedef unsigned ntv4 __attribute__((ext_vector_type(4)));
+
+// A 16-byte weight load, non-temporal (streamed past the caches' retention) when NT.
+template <bool NT>
+__device__ __forceinline__ uint4 load16(const uint8_t* p) {
+    if constexpr (NT) {
+        const ntv4 v = __builtin_nontemporal_load(reinterpret_cast<const ntv4*>(p));
+        return make_uint4(v.x, v.y, v.z, v.w);
+    } else {
+        return *reinterpret_cast<const uint4*>(p);
+    }
+}
+
+// NT: non-temporal code loads (Q4_0 only; measured per kernel shape).
+template <uint32_t T, bool WAVE, bool NT = false>
 __device__ __forceinline__ Frag load_group_raw(const WeightPtrs& W, int row, int c, int n_in, int lane) {
     Frag f{};
     const size_t gi = size_t(row) * (n_in / 32) + c;
@@ -41,7 +55,7 @@ __device__ __forceinline__ Frag load_group_raw(const WeightPtrs& W, int row, int
         f.w1 = p[1];
         f.raw = W.d[gi];
     } else if constexpr (T == kQ4_0) {
-        f.w0 = *reinterpret_cast<const uint4*>(W.codes + gi * 16);
+        f.w0 = load16<NT>(W.codes + gi * 16);
         f.raw = W.d[gi];
     } else if constexpr (has_mins(T)) {
         f.w0 = *reinterpret_cast<const uint4*>(W.codes + gi * 16);
