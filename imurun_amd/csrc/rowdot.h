@@ -44,15 +44,15 @@ __device__ __forceinline__ uint4 load16(const uint8_t* p) {
     }
 }
 
-// NT: non-temporal code loads (Q4_0 only; measured per kernel shape).
+// NT: non-temporal code loads (Q8_0 / Q4_0; measured per kernel shape).
 template <uint32_t T, bool WAVE, bool NT = false>
 __device__ __forceinline__ Frag load_group_raw(const WeightPtrs& W, int row, int c, int n_in, int lane) {
     Frag f{};
     const size_t gi = size_t(row) * (n_in / 32) + c;
     if constexpr (T == kQ8_0) {
         const uint4* p = reinterpret_cast<const uint4*>(W.codes + size_t(row) * n_in + size_t(c) * 32);
-        f.w0 = p[0];
-        f.w1 = p[1];
+        f.w0 = load16<NT>(reinterpret_cast<const uint8_t*>(p));
+        f.w1 = load16<NT>(reinterpret_cast<const uint8_t*>(p + 1));
         f.raw = W.d[gi];
     } else if constexpr (T == kQ4_0) {
         f.w0 = load16<NT>(W.codes + gi * 16);
