@@ -18,6 +18,7 @@
  *   or_block_dots         brute force from dequantised integer codes.
  *   or_quantize_row       golden packed blocks from the reference's quantize_row.
  *   or_vec_dot_q8 / or_matmul_batch  golden per-row dots and matmul outputs.
+ *   or_silu_mul           a float64 restatement within 4 ulps (tests/test_oracle.py).
  *   or_moe_ffn            golden output of a tiny MoE layer composed from the
  *       reference's own primitives in the order of model.cpp:1523-1580.
  *   or_dequant_row / or_matmul_f32path (Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, IQ4_NL,
@@ -869,6 +870,16 @@ void or_softmax(float* x, int n) {
 }
 
 float or_silu(float v) { return v / (1.0f + expf(-v)); }
+
+/* h = silu(g) * u element by element, as ffn_block does it: silu_inplace
+ * (ops.cpp:25-30), then g[i] *= u[i] (model.cpp:1504-1508), each step one f32
+ * rounding. Pinned by tests/test_oracle.py against a float64 restatement. */
+void or_silu_mul(const float* g, const float* u, uint64_t n, float* h) {
+    for (uint64_t i = 0; i < n; ++i) {
+        const float s = or_silu(g[i]);
+        h[i] = s * u[i];
+    }
+}
 
 /* Top-k of p[0..ne) by value, descending (ties: lower index first). */
 void or_route(const float* logits, int n_tok, int ne, int k, int norm, int* sel, float* wsel) {

@@ -80,6 +80,7 @@ class Oracle:
         L.or_route.argtypes = [_P, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, _P, _P]
         L.or_silu.argtypes = [ctypes.c_float]
         L.or_silu.restype = ctypes.c_float
+        L.or_silu_mul.argtypes = [_P, _P, ctypes.c_uint64, _P]
         L.or_moe_ffn.argtypes = [_P, _P, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                  ctypes.c_int, ctypes.c_uint32, _P, ctypes.c_uint32, _P, ctypes.c_uint32, _P, _P,
                                  ctypes.c_int]
@@ -180,6 +181,15 @@ class Oracle:
 
     def silu(self, v: float) -> float:
         return self.L.or_silu(v)
+
+    def silu_mul(self, g: np.ndarray, u: np.ndarray) -> np.ndarray:
+        """h = silu(g) * u in FISH's f32 steps (ops.cpp:25-30, model.cpp:1504-1508)."""
+        g = np.ascontiguousarray(g, np.float32)
+        u = np.ascontiguousarray(u, np.float32)
+        assert g.shape == u.shape
+        h = np.empty_like(g)
+        self.L.or_silu_mul(_ptr(g), _ptr(u), g.size, _ptr(h))
+        return h
 
     def moe_ffn(self, x, logits, E, F, NE, K, norm, tg, wg, tu, wu, td, wd) -> np.ndarray:
         x = np.ascontiguousarray(x, np.float32)

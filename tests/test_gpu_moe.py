@@ -7,11 +7,18 @@ silu*up requantization bit-exact on the GPU's own f32 hidden values, the
 down product within 1e-4 * max|ref| on those codes, and the combine
 bit-exact (ascending expert order, separately rounded multiply and add).
 
-The end-to-end comparison with FISH's composed layer uses LAYER_TOL: the
-hidden state is requantized to int8 between the products, so f32 rounding
-differences of 1e-7 in gate/up may move one code by one step where
-silu(g)*u/d sits at a rounding midpoint, which shifts the layer output by
-about d_h * |w_down| (~1e-4 of max|out| for these weights).
+The end-to-end comparison with FISH's composed layer (model.cpp:1523-1599)
+is held to 1e-4 * max|out| plus a bound computed from the data: the hidden
+state is requantized to int8 between the products, so an f32 rounding
+difference in gate/up can move a hidden value across a rounding midpoint of
+its code (or move its block's scale). The test requantizes FISH's own hidden
+values (oracle gate/up on the same x, FISH's silu * up) and the GPU's, and
+for each slot takes delta_k = |d' q'_k - d q_k|, the difference of the two
+dequantized hidden values: nonzero where a code flipped or where the block's
+scale differs (its absmax differs in the last bit). A down row i then moves by at most
+sum_k delta_k |W_down[i][k]| <= sum_k delta_k colmax_k, colmax_k = max_i
+|W_down[i][k]|; the combine weights it by the slot's routing weight. The
+test prints the flipped codes, the observed error and the bound.
 """
 import numpy as np
 import pytest
@@ -22,7 +29,6 @@ from imurun_amd.synth import normal
 pytestmark = pytest.mark.gpu
 
 TOL = 1e-4
-LAYER_TOL = 2e-3
 
 
 @pytest.fixture(scope="module")
@@ -177,6 +183,38 @@ def check_stages(torch_dev, oracle, x, logits, parts, out, n_ff, k, types, packe
             acc = acc + p["wsel"][t, i] * p["down"][tok_slot[t, i]]
         want[t] = acc
     assert np.array_equal(out, want)
+    # what the hidden requantization may move: FISH's own hidden values (oracle gate/up on
+    # the same x, FISH's silu * up) against the GPU's, code by code
+    k_layout = fh.BLOCK_ELEMS[td] == 256
+    h_fish = oracle.silu_mul(g_ref, u_ref)
+    a_gpu = oracle.act_batch(h)[1 if k_layout else 0]
+    a_fish = oracle.act_batch(h_fish)[1 if k_layout else 0]
+    delta = np.abs(act_values(a_gpu, k_layout) - act_values(a_fish, k_layout)).reshape(n_tok * k, n_ff)
+    size, qoff = (276, 20) if k_layout else (40, 8)
+    b_gpu, b_fish = a_gpu.reshape(-1, size), a_fish.reshape(-1, size)
+    n_codes = int(np.count_nonzero(b_gpu[:, qoff:] != b_fish[:, qoff:]))
+    n_scales = int(np.count_nonzero(np.any(b_gpu[:, :4] != b_fish[:, :4], axis=1)))
+    slot_bound = np.zeros(n_tok * k)
+    for e in experts:
+        sl = np.nonzero(exp_of == e)[0]
+        sl = sl[np.any(delta[sl] > 0, axis=1)]
+        if sl.size == 0:
+            continue
+        w_e = oracle.dequant_row(td, pd[e * bd:(e + 1) * bd], n_embd * n_ff).reshape(n_embd, n_ff)
+        colmax = np.max(np.abs(w_e.astype(np.float64)), axis=0)
+        slot_bound[sl] = delta[sl] @ colmax
+    tok_bound = np.array([sum(abs(float(p["wsel"][t, i])) * slot_bound[tok_slot[t, i]] for i in range(k))
+                          for t in range(n_tok)])
+    return tok_bound, (n_codes, n_scales, b_gpu.shape[0], int(np.count_nonzero(delta)))
+
+
+def act_values(buf, k_layout):
+    """Dequantized values d * q of FISH's Q8ActK (276-byte) or Q8Act (40-byte) blocks, float64."""
+    size, qoff = (276, 20) if k_layout else (40, 8)
+    blk = buf.reshape(-1, size)
+    d = blk[:, :4].copy().view(np.float32).astype(np.float64)
+    q = blk[:, qoff:].view(np.int8).astype(np.float64)
+    return (d * q).reshape(-1)
 
 
 def run_case(torch_dev, oracle, n_tok, n_embd, n_ff, n_expert, k, types, seed, distinct=None, favour=None):
@@ -193,9 +231,20 @@ def run_case(torch_dev, oracle, n_tok, n_embd, n_ff, n_expert, k, types, seed, d
     out = fh.moe_ffn(dev(torch_dev, x), dev(torch_dev, logits), n_ff, n_expert, k, True, tg, wg, tu, wu, td, wd,
                      workspace=ws).cpu().numpy()
     parts = fh.moe_parts(ws, n_tok, n_embd, n_ff, n_expert, k)
-    check_stages(torch_dev, oracle, x, logits, parts, out, n_ff, k, types, (pg, pu, pd))
+    tok_bound, (codes, scales, blocks, moved) = check_stages(torch_dev, oracle, x, logits, parts, out, n_ff, k, types,
+                                                             (pg, pu, pd))
     want = oracle.moe_ffn(x, logits, n_embd, n_ff, n_expert, k, True, tg, pg, tu, pu, td, pd)
-    check_close(out, want, f"moe M={n_tok} E={n_embd} F={n_ff} NE={n_expert} k={k}", LAYER_TOL)
+    err = np.abs(out.astype(np.float64) - want)
+    scale = float(np.max(np.abs(want)))
+    allowed = TOL * scale + np.broadcast_to(tok_bound[:, None], err.shape)
+    worst = np.unravel_index(int(np.argmax(err / allowed)), err.shape)
+    print(f"moe M={n_tok} E={n_embd} F={n_ff} NE={n_expert} k={k}: against FISH's requantization {codes} of "
+          f"{n_tok * k * n_ff} hidden codes flipped, {scales} of {blocks} block scales differ; max err "
+          f"{float(err.max()):.3e} = {float(err.max()) / scale:.2e} of max|out|; at the tightest element err "
+          f"{float(err[worst]):.3e} vs allowed {float(allowed[worst]):.3e}")
+    assert np.all(err <= allowed), f"moe M={n_tok}: err {float(err[worst]):.3e} > {float(allowed[worst]):.3e}"
+    if moved == 0:  # nothing to excuse: the plain bar
+        check_close(out, want, f"moe M={n_tok} E={n_embd} F={n_ff} NE={n_expert} k={k}")
 
 
 def test_moe_matches_reference_golden(torch_dev, golden):
@@ -257,3 +306,21 @@ def test_moe_mixtral_full_size_decode(torch_dev, oracle):
 def test_moe_qwen3_full_size(torch_dev, oracle):
     """Qwen3-30B-A3B expert shapes, 128 experts (8 distinct, repeated), M=24."""
     run_case(torch_dev, oracle, 24, 2048, 768, 128, 8, (fh.Q4_K, fh.Q4_K, fh.Q6_K), 5000, distinct=8)
+
+
+def test_moe_mixtral_full_size_batched(torch_dev, oracle):
+    """Mixtral-8x7B expert shapes at M=64 (E=4096, F=14336, 8 experts, top-2; two distinct
+    experts, repeated): the grouped MFMA batch kernel in work-list mode at K=4096 and K=14336."""
+    run_case(torch_dev, oracle, 64, 4096, 14336, 8, 2, (fh.Q4_K, fh.Q4_K, fh.Q4_K), 4100, distinct=2)
+
+
+def test_moe_qwen3_full_size_decode(torch_dev, oracle):
+    """Qwen3-30B-A3B expert shapes at M=1 (E=2048, F=768, 128 experts, top-8): the one-token
+    expert kernels."""
+    run_case(torch_dev, oracle, 1, 2048, 768, 128, 8, (fh.Q4_K, fh.Q4_K, fh.Q6_K), 5100, distinct=16)
+
+
+def test_moe_qwen3_full_size_prefill(torch_dev, oracle):
+    """Qwen3-30B-A3B expert shapes at M=256 (128 experts, top-8, skewed per-expert counts from
+    N(0, 1) logits): grouped batch-kernel items over all 128 experts."""
+    run_case(torch_dev, oracle, 256, 2048, 768, 128, 8, (fh.Q4_K, fh.Q4_K, fh.Q6_K), 5200, distinct=16)

@@ -149,6 +149,24 @@ def test_moe_golden(oracle, golden):
     assert np.max(np.abs(out - want)) <= 1e-5 * np.max(np.abs(want))
 
 
+def test_silu_mul_float64(oracle):
+    """silu(g) * u in f32 steps (ops.cpp:25-30, model.cpp:1504-1508) against a float64
+    restatement: exp, add, divide and multiply are four f32 roundings (each at most half
+    an ulp, exp within one), so the result is within 4 ulps; a dropped factor of u, or
+    sigmoid in place of silu, is off by orders of magnitude more."""
+    g = normal(91, (4, 4096)) * np.float32(4.0)
+    u = normal(92, (4, 4096))
+    g[0, :6] = [0.0, -0.0, 80.0, -80.0, 1e-30, -1e-30]
+    h = oracle.silu_mul(g, u)
+    g64, u64 = g.astype(np.float64), u.astype(np.float64)
+    h64 = g64 / (1.0 + np.exp(-g64)) * u64
+    ulp = np.spacing(np.abs(h64).astype(np.float32)).astype(np.float64)
+    assert np.all(np.abs(h - h64) <= 4 * ulp + 1e-45)
+    assert oracle.silu(np.float32(2.0)) == np.float32(2.0) / (np.float32(1.0) + np.exp(np.float32(-2.0)))
+    wrong = (g64 / (1.0 + np.exp(-g64)))
+    assert np.max(np.abs(h - wrong)) > 1e-2
+
+
 def _abs_bound(x, w):
     """sum_k |x_k w_k| per (token, row): the scale of f32 rounding in a dot."""
     return np.abs(x.astype(np.float64)) @ np.abs(w.astype(np.float64)).T
