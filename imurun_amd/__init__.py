@@ -67,6 +67,9 @@ def load() -> ctypes.CDLL:
                                   ctypes.c_int),
         "fish_hip_matmul_tensors": ([ctypes.c_uint32, ctypes.c_int, _P, _P, ctypes.c_int, ctypes.c_int, _P, _P, _P,
                                      ctypes.c_uint64, _P], ctypes.c_int),
+        "fish_hip_matmul_tensors_noalloc": ([ctypes.c_uint32, ctypes.c_int, _P, _P, ctypes.c_int, ctypes.c_int, _P,
+                                             _P, _P], ctypes.c_int),
+        "fish_hip_noalloc_scratch_bytes": ([], ctypes.c_uint64),
         "fish_hip_block_ints": ([ctypes.c_uint32, _P, _P, ctypes.c_int, ctypes.c_int, _P, _P], ctypes.c_int),
         "fish_hip_quantize_rows": ([ctypes.c_uint32, _P, _P, ctypes.c_int, ctypes.c_int, ctypes.c_int], ctypes.c_int),
         "fish_hip_moe_workspace_bytes": ([ctypes.c_int] * 5, ctypes.c_uint64),
@@ -239,6 +242,31 @@ def matmul_tensors(t: int, ws, x, n_outs, ys=None, act=None, stream=None):
     _check(load().fish_hip_matmul_tensors(t, n, wp, x.data_ptr(), n_tok, n_in, no, yp, _ptr(act),
                                           act.numel() if act is not None else 0, _stream(stream)), "matmul_tensors")
     return ys
+
+
+def matmul_tensors_noalloc(t: int, ws, x, n_outs, ys, stream=None):
+    """matmul_tensors with the activation workspace in the library's fixed device array
+    (fish_hip_matmul_tensors_noalloc): the call allocates nothing; ys must be given."""
+    import torch
+    assert x.is_cuda and x.dtype == torch.float32 and x.dim() == 2 and x.is_contiguous()
+    n_tok, n_in = x.shape
+    n = len(ws)
+    if n != len(n_outs) or n != len(ys) or not 1 <= n <= 4:
+        raise FishHipError("matmul_tensors_noalloc: 1..4 tensors with one n_out and one y each")
+    for w, y, n_out in zip(ws, ys, n_outs):
+        if w.numel() < weight_bytes(t, n_in, n_out):
+            raise FishHipError("matmul_tensors_noalloc: weight buffer smaller than its layout")
+        assert y.numel() >= n_tok * n_out and y.is_contiguous()
+    wp = (ctypes.c_void_p * n)(*[w.data_ptr() for w in ws])
+    yp = (ctypes.c_void_p * n)(*[y.data_ptr() for y in ys])
+    no = (ctypes.c_int * n)(*n_outs)
+    _check(load().fish_hip_matmul_tensors_noalloc(t, n, wp, x.data_ptr(), n_tok, n_in, no, yp, _stream(stream)),
+           "matmul_tensors_noalloc")
+    return ys
+
+
+def noalloc_scratch_bytes() -> int:
+    return int(load().fish_hip_noalloc_scratch_bytes())
 
 
 def matmul_batch(t: int, w, x, n_out: int, stream=None):

@@ -11,7 +11,7 @@ CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "libfish_hip.so")
 BUILD = os.path.join(HERE, "_build")
 SOURCES = ["quantize.hip", "repack.hip", "gemv.hip", "batch.hip", "gemm.hip", "moe.hip", "dqmm.hip", "span.hip",
-           "capi.cpp", "pack.cpp"]
+           "noalloc.hip", "capi.cpp", "pack.cpp"]
 # code whose float rounding must follow FISH's baseline x86-64 build step by
 # step (no fused multiply-add): the host weight packer, the expert routing
 # softmax / combine, the f32-path dequantisers and the layer-span steps

@@ -698,6 +698,10 @@ private:
 
 }  // namespace
 
+namespace fishhip {
+void set_last_error(const std::string& msg) { g_err = msg; }
+}  // namespace fishhip
+
 extern "C" {
 
 int fish_hip_abi_version(void) { return FISH_HIP_ABI_VERSION; }

@@ -4,9 +4,14 @@
 
 #include <hip/hip_runtime.h>
 
+#include <string>
+
 #include "common.h"
 
 namespace fishhip {
+
+// The calling thread's fish_hip_last_error() message (capi.cpp).
+void set_last_error(const std::string& msg);
 
 // Planes of an activation buffer a quantization writes (common.h layout):
 // each matmul kernel reads its own, so a batch writes only what its

@@ -116,6 +116,22 @@ FISH_HIP_API int fish_hip_matmul_tensors(uint32_t type, int n, const void* const
                                          int n_in, const int* n_outs, float* const* ys, void* act_workspace,
                                          uint64_t act_workspace_bytes, void* stream);
 
+/* fish_hip_matmul_tensors for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, hosts that forbid
+ * hipMalloc). No counterpart in the reference: FISH's CPU path allocates its
+ * ActBatch per call. The activation workspace is a fixed device array of
+ * this library, FISH_HIP_NOALLOC_SCRATCH_MB MiB per GPU, held until the process
+ * ends; the call allocates and frees nothing. Sizes whose quantized
+ * activations (fish_hip_act_bytes(n_tok, n_in)) exceed it are refused with
+ * FISH_HIP_ERR_ARG. Calls on one GPU share the array: two calls that overlap
+ * on a GPU (different streams, or threads without ordering) race. */
+#define FISH_HIP_NOALLOC_SCRATCH_MB 32
+FISH_HIP_API int fish_hip_matmul_tensors_noalloc(uint32_t type, int n, const void* const* ws, const float* x,
+                                                 int n_tok, int n_in, const int* n_outs, float* const* ys,
+                                                 void* stream);
+/* Bytes of that array (FISH_HIP_NOALLOC_SCRATCH_MB << 20). */
+FISH_HIP_API uint64_t fish_hip_noalloc_scratch_bytes(void);
+
 /* The per-block integers of FISH's AVX2 kernels (quant_x86.cpp:280-495) for
  * every row of w against token 0 of act: Q8_0/Q4_0 one int32 per 32-block,
  * Q4_K / Q5_K two per super-block (sum sc*dot, sum m*bsum), Q6_K one per super-block. */
