@@ -94,9 +94,13 @@ def load() -> ctypes.CDLL:
         "fish_hip_backend_served": ([], ctypes.c_uint64),
         "fish_hip_backend_matmul": ([_P, _P, ctypes.c_int, ctypes.c_int, ctypes.c_int, _P], ctypes.c_int),
         "fish_hip_backend_matmul_group": ([_P, ctypes.c_int, _P, ctypes.c_int, ctypes.c_int, _P, _P], ctypes.c_int),
+        "fish_hip_backend_moe_ffn": ([_P, _P, _P, _P, _P, _P] + [ctypes.c_int] * 6 + [_P], ctypes.c_int),
         "fish_hip_span_prepare": ([_P], ctypes.c_int),
         "fish_hip_span_forward": ([_P, ctypes.c_int, ctypes.c_int], ctypes.c_int),
         "fish_hip_span_kv_truncate": ([ctypes.c_int], None),
+        "fish_hip_span_inspect": ([ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, _P, ctypes.c_uint64],
+                                  ctypes.c_int),
+        "fish_hip_span_last_tokens": ([], ctypes.c_int),
         "fish_hip_span_release": ([], None),
     }
     for name, (args, res) in sig.items():
@@ -374,10 +378,14 @@ def silu_mul_quantize(g, u, stream=None):
 
 # ------------------------------------------------------------------ backend (host buffers)
 
+SPAN_VECS = ("q_norm", "k_norm", "bias_q", "bias_k", "bias_v", "bias_o")
+
+
 class SpanLayer(ctypes.Structure):
     """fish_hip_span_layer (include/fish_hip.h)."""
     _fields_ = [(n, ctypes.c_void_p) for n in ("wq", "wk", "wv", "wo", "wg", "wu", "wd")] + \
-               [("attn_norm", ctypes.c_void_p), ("ffn_norm", ctypes.c_void_p)]
+               [("attn_norm", ctypes.c_void_p), ("ffn_norm", ctypes.c_void_p)] + \
+               [(n, ctypes.c_void_p) for n in SPAN_VECS]
 
 
 class SpanParams(ctypes.Structure):
@@ -386,16 +394,21 @@ class SpanParams(ctypes.Structure):
                 ("n_head_kv", ctypes.c_int), ("head_dim", ctypes.c_int), ("n_ff", ctypes.c_int),
                 ("n_ctx", ctypes.c_int), ("eps", ctypes.c_float), ("attn_scale", ctypes.c_float),
                 ("rope_cos", ctypes.c_void_p), ("rope_sin", ctypes.c_void_p), ("rot_dim", ctypes.c_int),
-                ("rope_neox", ctypes.c_int), ("layers", ctypes.c_void_p)]
+                ("rope_neox", ctypes.c_int), ("layers", ctypes.c_void_p), ("kv_q8", ctypes.c_int)]
 
 
 class HipBackend:
-    """ComputeBackend over host numpy buffers (backend.h:26-163)."""
+    """ComputeBackend over host numpy buffers (backend.h:26-163).
+
+    Tensors are named by strings; each name maps to one key pointer for the life of
+    the process (shared by every instance), so a name always addresses the same
+    resident tensor and no key address is ever reused for another name."""
+
+    _keys: dict[str, ctypes.c_void_p] = {}
+    _anchors: list = []
 
     def __init__(self):
         self.L = load()
-        self._keys: dict[str, ctypes.c_void_p] = {}
-        self._anchors = []
 
     def available(self) -> bool:
         return bool(self.L.fish_hip_backend_available())
@@ -447,22 +460,70 @@ class HipBackend:
         return y if ok else None
 
     def span_prepare(self, layers, n_embd, n_head, n_head_kv, head_dim, n_ff, n_ctx, rope_cos, rope_sin,
-                     rope_neox=False, eps=1e-5, attn_scale=0.0) -> bool:
+                     rope_neox=False, eps=1e-5, attn_scale=0.0, kv_q8=False) -> bool:
         """ComputeBackend::span_prepare over uploaded tensors: layers = [(names of
-        wq, wk, wv, wo, wg, wu, wd), attn_norm, ffn_norm]; RoPE tables [n_ctx][rot_dim / 2]."""
+        wq, wk, wv, wo, wg, wu, wd), attn_norm, ffn_norm] or [(names, attn_norm, ffn_norm,
+        extras)] with extras a dict of the optional SPAN_VECS (Qwen-3 q/k norms, biases);
+        RoPE tables [n_ctx][rot_dim / 2]."""
         arr = (SpanLayer * len(layers))()
         keep = []
-        for i, (names, an, fn) in enumerate(layers):
+        for i, layer in enumerate(layers):
+            names, an, fn = layer[:3]
+            extras = layer[3] if len(layer) > 3 else {}
             an = np.ascontiguousarray(an, np.float32)
             fn = np.ascontiguousarray(fn, np.float32)
             keep += [an, fn]
-            arr[i] = SpanLayer(*[self._key(n).value for n in names], an.ctypes.data, fn.ctypes.data)
+            vecs = []
+            for n in SPAN_VECS:
+                v = extras.get(n)
+                if v is None:
+                    vecs.append(None)
+                else:
+                    v = np.ascontiguousarray(v, np.float32)
+                    keep.append(v)
+                    vecs.append(v.ctypes.data)
+            arr[i] = SpanLayer(*[self._key(n).value for n in names], an.ctypes.data, fn.ctypes.data, *vecs)
         rc = np.ascontiguousarray(rope_cos, np.float32)
         rs = np.ascontiguousarray(rope_sin, np.float32)
         p = SpanParams(len(layers), n_embd, n_head, n_head_kv, head_dim, n_ff, n_ctx, eps, attn_scale,
                        rc.ctypes.data, rs.ctypes.data, 2 * rc.shape[1], 1 if rope_neox else 0,
-                       ctypes.cast(arr, ctypes.c_void_p))
+                       ctypes.cast(arr, ctypes.c_void_p), 1 if kv_q8 else 0)
         return bool(self.L.fish_hip_span_prepare(ctypes.byref(p)))
+
+    def span_kv_truncate(self, n_past: int) -> None:
+        self.L.fish_hip_span_kv_truncate(n_past)
+
+    SPAN_PARTS = ("x", "xb", "q", "k", "v", "qr", "att", "proj", "xb2", "h", "u", "dn")
+
+    def span_inspect(self, part: str, width: int, layer: int = 0, pos0: int = 0, n: int = 0):
+        """An intermediate buffer of the last span_forward call, [tokens][width] f32; part "kc" /
+        "vc" returns cache rows pos0 .. pos0 + n - 1 of `layer` ([n][width], width = kv_dim)."""
+        if part in ("kc", "vc"):
+            out = np.empty((n, width), np.float32)
+            ok = self.L.fish_hip_span_inspect(100 if part == "kc" else 101, layer, pos0, n, out.ctypes.data, out.size)
+        else:
+            t = int(self.L.fish_hip_span_last_tokens())
+            out = np.empty((t, width), np.float32)
+            ok = t > 0 and self.L.fish_hip_span_inspect(self.SPAN_PARTS.index(part), 0, 0, 0, out.ctypes.data,
+                                                        out.size)
+        if not ok:
+            raise FishHipError(f"span_inspect({part}) refused")
+        return out
+
+    def moe_ffn(self, names, x: np.ndarray, logits, n_ff: int, n_expert: int, k: int, norm: bool = True,
+                router: str | None = None):
+        """fish_hip_backend_moe_ffn over uploaded 3-D expert tensors (gate, up, down names) on host
+        buffers; `logits` [n_tok][n_expert] or None with a resident router tensor. out or None."""
+        x = np.ascontiguousarray(x, np.float32)
+        n_tok, n_embd = x.shape
+        lg = None if logits is None else np.ascontiguousarray(logits, np.float32)
+        out = np.empty((n_tok, n_embd), np.float32)
+        keys = [self._key(n).value for n in names]
+        kr = self._key(router).value if router else None
+        ok = self.L.fish_hip_backend_moe_ffn(keys[0], keys[1], keys[2], kr, x.ctypes.data,
+                                             None if lg is None else lg.ctypes.data, n_tok, n_embd, n_ff, n_expert, k,
+                                             int(norm), out.ctypes.data)
+        return out if ok else None
 
     def span_forward(self, x: np.ndarray, pos0: int) -> bool:
         """ComputeBackend::span_forward: x [n_tok, n_embd] float32, updated in place."""

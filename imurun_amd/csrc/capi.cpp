@@ -11,8 +11,10 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cstdint>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -39,6 +41,24 @@ int hip_fail(hipError_t e, const char* what) {
 }
 
 hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
+
+// VRAM the backend leaves free for other programs, applied to each of its
+// allocations (the rule of vram_headroom_bytes, backend.h:171-187, which FISH's
+// planner applies to its budget too): max(256 MB, 5 % of the heap); with
+// FISH_VRAM_HEADROOM_PCT = p (0..90) p % of the heap instead; with
+// FISH_VRAM_HEADROOM_MB = m (wins when both are set) m MB.
+uint64_t vram_headroom_bytes(uint64_t heap) {
+    uint64_t h = std::max<uint64_t>(heap / 20, uint64_t(256) << 20);
+    if (const char* e = std::getenv("FISH_VRAM_HEADROOM_PCT"); e && *e) {
+        const double pct = std::atof(e);
+        if (pct >= 0.0 && pct <= 90.0) h = uint64_t(double(heap) * pct / 100.0);
+    }
+    if (const char* e = std::getenv("FISH_VRAM_HEADROOM_MB"); e && *e) {
+        const long long mb = std::atoll(e);
+        if (mb >= 0) h = uint64_t(mb) << 20;
+    }
+    return h;
+}
 
 // Types with an int8 path (repacked device planes, quantized activations).
 bool int8_type(uint32_t type) {
@@ -209,33 +229,44 @@ public:
 
     bool upload(const void* key, uint32_t type, const void* data, int n_in, int n_out, int n_expert) {
         std::lock_guard<std::mutex> lk(mu_);
-        if (!ensure_init() || !key || !data || !type_ok(type) || n_expert < 1) return false;
+        if (!ensure_init() || broken_ || !key || !data || !type_ok(type) || n_in <= 0 || n_out <= 0 || n_expert < 1)
+            return false;
         if (map_.count(key)) return true;
-        WeightLayout L = weight_layout(type, n_in, n_out * n_expert);
+        if (int64_t(n_out) * n_expert > (int64_t(1) << 30)) return false;
+        const int rows = n_out * n_expert;
+        WeightLayout L = weight_layout(type, n_in, rows);
         if (f32path_type(type)) {
             // f32-path types stay in their GGUF bytes
             L = WeightLayout{};
             L.type = type;
             L.n_in = n_in;
-            L.n_out = n_out * n_expert;
-            L.total = f32path_bytes(type, n_in, n_out * n_expert);
+            L.n_out = rows;
+            L.total = f32path_bytes(type, n_in, rows);
         }
         if (!L.total) return false;
-        const size_t src_bytes = gguf_row_bytes(type, n_in) * size_t(n_out) * size_t(n_expert);
+        const size_t row_b = gguf_row_bytes(type, n_in);
+        // whole rows through one bounded staging buffer, so a large (3-D expert)
+        // tensor never needs a second device copy of its own size
+        const int chunk = int(std::max<size_t>(1, std::min<size_t>(kStageBytes / row_b, size_t(rows))));
         Resident r;
         r.layout = L;
         r.n_expert = n_expert;
         r.bytes = L.total;
-        void* staging = nullptr;
-        if (hipMalloc(&r.dev, L.total) != hipSuccess) { r.dev = nullptr; return false; }
-        if (hipMalloc(&staging, src_bytes) != hipSuccess) { (void)hipFree(r.dev); return false; }
-        hipError_t e = hipMemcpyAsync(staging, data, src_bytes, hipMemcpyHostToDevice, stream_);
-        if (e == hipSuccess && f32path_type(type))
-            e = hipMemcpyAsync(r.dev, staging, src_bytes, hipMemcpyDeviceToDevice, stream_);
-        else if (e == hipSuccess)
-            e = launch_repack(type, staging, n_in, n_out * n_expert, r.dev, stream_);
+        if (!grow_buffer(d_stage_, cap_stage_, size_t(chunk) * row_b)) return false;
+        if (dev_alloc(&r.dev, L.total) != hipSuccess) return false;
+        hipError_t e = hipSuccess;
+        for (int r0 = 0; r0 < rows && e == hipSuccess; r0 += chunk) {
+            const int nr = std::min(chunk, rows - r0);
+            e = hipMemcpyAsync(d_stage_, static_cast<const uint8_t*>(data) + size_t(r0) * row_b, size_t(nr) * row_b,
+                               hipMemcpyHostToDevice, stream_);
+            if (e != hipSuccess) break;
+            if (f32path_type(type))
+                e = hipMemcpyAsync(static_cast<uint8_t*>(r.dev) + size_t(r0) * row_b, d_stage_, size_t(nr) * row_b,
+                                   hipMemcpyDeviceToDevice, stream_);
+            else
+                e = launch_repack_rows(type, d_stage_, n_in, rows, r0, nr, r.dev, stream_);
+        }
         if (e == hipSuccess) e = hipStreamSynchronize(stream_);
-        (void)hipFree(staging);
         if (e != hipSuccess) {
             (void)hipFree(r.dev);
             mark_broken(e, "upload");
@@ -304,15 +335,68 @@ public:
             mark_broken(e, "matmul");
             return false;
         }
+        // every output comes back into one host staging buffer before any y_i is
+        // written, so a failed readback leaves all of them untouched
+        if (!grow_host(y_total * 4)) return false;
+        e = hipMemcpy(h_y_, d_y_, y_total * 4, hipMemcpyDeviceToHost);
+        if (e != hipSuccess) {
+            mark_broken(e, "readback");
+            return false;
+        }
         off = 0;
         for (int i = 0; i < n; ++i) {
             const size_t cnt = size_t(n_tok) * size_t(n_outs[i]);
-            e = hipMemcpy(ys[i], static_cast<float*>(d_y_) + off, cnt * 4, hipMemcpyDeviceToHost);
-            if (e != hipSuccess) {
-                mark_broken(e, "readback");
-                return false;
-            }
+            std::memcpy(ys[i], static_cast<const float*>(h_y_) + off, cnt * 4);
             off += cnt;
+        }
+        ++served_;
+        return true;
+    }
+
+    // The expert FFN on host buffers over 3-D resident expert tensors (uploaded
+    // with n_expert = ne[2]); router logits from the host, or computed here from
+    // a resident f32 / f16 router tensor. out written only on success.
+    bool moe_ffn_host(const void* kg, const void* ku, const void* kd, const void* kr, const float* x,
+                      const float* logits, int n_tok, int n_embd, int n_ff, int n_expert, int k, int norm, float* out) {
+        std::lock_guard<std::mutex> lk(mu_);
+        if (!ensure_init() || broken_ || !x || !out || (!logits && !kr)) return false;
+        const MoeWork w = moe_work(n_tok, n_embd, n_ff, n_expert, k);
+        if (!w.total) return false;
+        auto find = [&](const void* key, int n_in, int n_rows, int n_exp) -> const Resident* {
+            auto it = map_.find(key);
+            if (it == map_.end()) return nullptr;
+            const Resident& r = it->second;
+            return (r.n_expert == n_exp && r.layout.n_in == n_in && r.layout.n_out == n_rows * n_exp) ? &r : nullptr;
+        };
+        const Resident* rg = find(kg, n_embd, n_ff, n_expert);
+        const Resident* ru = find(ku, n_embd, n_ff, n_expert);
+        const Resident* rd = find(kd, n_ff, n_embd, n_expert);
+        const Resident* rr = kr ? find(kr, n_embd, n_expert, 1) : nullptr;
+        if (!rg || !ru || !rd || (kr && !rr)) return false;
+        const uint32_t tg = rg->layout.type, tu = ru->layout.type, td = rd->layout.type;
+        if (!int8_type(tg) || !int8_type(tu) || !int8_type(td) || ((is_kquant(tg) || is_kquant(tu)) && n_embd % 256) ||
+            (is_kquant(td) && n_ff % 256))
+            return false;
+        if (rr && ((rr->layout.type != kF32 && rr->layout.type != kF16) || n_embd % 4)) return false;
+        const size_t xb = align256(size_t(n_tok) * n_embd * 4), lb = align256(size_t(n_tok) * n_expert * 4);
+        if (!grow_buffer(d_moe_, cap_moe_, w.total + 2 * xb + lb)) return false;
+        uint8_t* base = static_cast<uint8_t*>(d_moe_);
+        float* dx = reinterpret_cast<float*>(base + w.total);
+        float* dout = reinterpret_cast<float*>(base + w.total + xb);
+        float* dl = reinterpret_cast<float*>(base + w.total + 2 * xb);
+        hipError_t e = hipMemcpyAsync(dx, x, size_t(n_tok) * n_embd * 4, hipMemcpyHostToDevice, stream_);
+        if (e == hipSuccess && rr)
+            e = launch_router(dx, n_tok, n_embd, rr->layout.type, rr->dev, n_expert, dl, stream_);
+        else if (e == hipSuccess)
+            e = hipMemcpyAsync(dl, logits, size_t(n_tok) * n_expert * 4, hipMemcpyHostToDevice, stream_);
+        if (e == hipSuccess)
+            e = moe_ffn(dx, dl, n_tok, n_embd, n_ff, n_expert, k, norm, tg, rg->dev, tu, ru->dev, td, rd->dev, base, w,
+                        dout, stream_);
+        if (e == hipSuccess) e = hipStreamSynchronize(stream_);
+        if (e == hipSuccess) e = hipMemcpy(out, dout, size_t(n_tok) * n_embd * 4, hipMemcpyDeviceToHost);
+        if (e != hipSuccess) {
+            mark_broken(e, "moe_ffn");
+            return false;
         }
         ++served_;
         return true;
@@ -332,6 +416,7 @@ public:
             p.n_head_kv <= 0 || p.n_head % p.n_head_kv || p.head_dim <= 0 || p.head_dim > 256 || p.n_ff <= 0 ||
             p.n_ctx <= 0 || p.rot_dim < 0 || p.rot_dim > p.head_dim || p.rot_dim % 2 || !p.rope_cos || !p.rope_sin)
             return false;
+        if (p.kv_q8) return false;  // int8 KV cache: not kept here, FISH keeps per-matmul routing
         const int E = p.n_embd, Q = p.n_head * p.head_dim, KV = p.n_head_kv * p.head_dim, F = p.n_ff;
         // every weight resident, unsplit, with the shapes of a dense layer
         for (int l = 0; l < p.n_layers; ++l) {
@@ -341,37 +426,68 @@ public:
             for (int i = 0; i < 7; ++i) {
                 auto it = map_.find(keys[i]);
                 if (it == map_.end() || it->second.n_expert != 1 || it->second.layout.n_in != n_in[i] ||
-                    it->second.layout.n_out != n_out[i])
+                    it->second.layout.n_out != n_out[i]) {
+                    span_keys_.clear();
                     return false;
+                }
                 span_keys_.push_back(keys[i]);
             }
-            if (!L.attn_norm || !L.ffn_norm) return false;
+            if (!L.attn_norm || !L.ffn_norm || (!L.q_norm) != (!L.k_norm)) {
+                span_keys_.clear();
+                return false;
+            }
         }
         sp_ = p;
         sp_.layers = nullptr;
+        // per-layer vectors: attn_norm, ffn_norm, q_norm, k_norm, bias_q, bias_k, bias_v, bias_o
+        const int D = p.head_dim;
+        const size_t vlen[kSpanVecs] = {size_t(E), size_t(E), size_t(D), size_t(D), size_t(Q), size_t(KV), size_t(KV),
+                                        size_t(E)};
+        size_t voff[kSpanVecs], per_layer = 0;
+        for (int i = 0; i < kSpanVecs; ++i) {
+            voff[i] = per_layer;
+            per_layer += align256(vlen[i] * 4);
+        }
         const size_t half = size_t(p.rot_dim / 2), ctx = size_t(p.n_ctx);
-        const size_t norm_b = size_t(p.n_layers) * 2 * E * 4, rope_b = ctx * half * 4,
-                     kv_b = size_t(p.n_layers) * ctx * KV * 4;
-        hipError_t e = hipMalloc(&d_span_fixed_, norm_b + 2 * rope_b + 2 * kv_b + 256);
-        if (e != hipSuccess) {
-            d_span_fixed_ = nullptr;
-            span_keys_.clear();
+        const size_t vec_b = size_t(p.n_layers) * per_layer, rope_b = align256(ctx * half * 4),
+                     kv_b = align256(size_t(p.n_layers) * ctx * KV * 2);
+        // buffers of later calls, sized once here so that no call grows them: a
+        // prefill chunk of up to kSpanChunk tokens, the decode graph's one token
+        // (attention partials over the whole context), the activation buffer
+        size_t act = 0;
+        for (int n_in : {E, Q, F}) act = std::max(act, act_layout(kSpanChunk, n_in).total);
+        const size_t ws_b = span_ws_bytes(kSpanChunk, p.n_ctx), dec_b = span_ws_bytes(1, p.n_ctx);
+        size_t dec_act = 0;
+        for (int n_in : {E, Q, F}) dec_act = std::max(dec_act, act_layout(1, n_in).total);
+        const size_t total = vec_b + 2 * rope_b + 2 * kv_b + ws_b + align256(dec_b) + dec_act + 256;
+        if (!act || !reserve(0, act, 0) || dev_alloc(&d_span_fixed_, total) != hipSuccess) {
+            span_free();
             return false;
         }
         char* b = static_cast<char*>(d_span_fixed_);
-        d_norms_ = reinterpret_cast<float*>(b);
-        d_cos_ = reinterpret_cast<float*>(b + norm_b);
-        d_sin_ = reinterpret_cast<float*>(b + norm_b + rope_b);
-        d_kc_ = reinterpret_cast<float*>(b + norm_b + 2 * rope_b);
-        d_vc_ = reinterpret_cast<float*>(b + norm_b + 2 * rope_b + kv_b);
+        d_vecs_ = reinterpret_cast<float*>(b);
+        d_cos_ = reinterpret_cast<float*>(b + vec_b);
+        d_sin_ = reinterpret_cast<float*>(b + vec_b + rope_b);
+        d_kc_ = reinterpret_cast<_Float16*>(b + vec_b + 2 * rope_b);
+        d_vc_ = reinterpret_cast<_Float16*>(b + vec_b + 2 * rope_b + kv_b);
+        d_span_ws_ = b + vec_b + 2 * rope_b + 2 * kv_b;
+        d_dec_ = b + vec_b + 2 * rope_b + 2 * kv_b + ws_b;
+        d_dec_act_ = b + vec_b + 2 * rope_b + 2 * kv_b + ws_b + align256(dec_b);
+        span_vec_off_.assign(size_t(p.n_layers) * kSpanVecs, SIZE_MAX);
+        hipError_t e = hipSuccess;
         for (int l = 0; l < p.n_layers && e == hipSuccess; ++l) {
-            e = hipMemcpy(d_norms_ + size_t(2 * l) * E, p.layers[l].attn_norm, size_t(E) * 4, hipMemcpyHostToDevice);
-            if (e == hipSuccess)
-                e = hipMemcpy(d_norms_ + size_t(2 * l + 1) * E, p.layers[l].ffn_norm, size_t(E) * 4,
-                              hipMemcpyHostToDevice);
+            const fish_hip_span_layer& L = p.layers[l];
+            const float* src[kSpanVecs] = {L.attn_norm, L.ffn_norm, L.q_norm, L.k_norm,
+                                           L.bias_q,    L.bias_k,   L.bias_v, L.bias_o};
+            for (int i = 0; i < kSpanVecs && e == hipSuccess; ++i) {
+                if (!src[i]) continue;
+                const size_t at = size_t(l) * per_layer + voff[i];
+                e = hipMemcpy(reinterpret_cast<char*>(d_vecs_) + at, src[i], vlen[i] * 4, hipMemcpyHostToDevice);
+                span_vec_off_[size_t(l) * kSpanVecs + i] = at;
+            }
         }
-        if (e == hipSuccess && rope_b) e = hipMemcpy(d_cos_, p.rope_cos, rope_b, hipMemcpyHostToDevice);
-        if (e == hipSuccess && rope_b) e = hipMemcpy(d_sin_, p.rope_sin, rope_b, hipMemcpyHostToDevice);
+        if (e == hipSuccess && half) e = hipMemcpy(d_cos_, p.rope_cos, ctx * half * 4, hipMemcpyHostToDevice);
+        if (e == hipSuccess && half) e = hipMemcpy(d_sin_, p.rope_sin, ctx * half * 4, hipMemcpyHostToDevice);
         if (e != hipSuccess) {
             span_free();
             mark_broken(e, "span_prepare");
@@ -390,7 +506,7 @@ public:
     bool span_forward(float* x, int n_tok, int pos0) {
         std::lock_guard<std::mutex> lk(mu_);
         if (!span_on_ || broken_ || !x || n_tok <= 0 || pos0 < 0 || pos0 + n_tok > sp_.n_ctx) return false;
-        const int E = sp_.n_embd, Q = sp_.n_head * sp_.head_dim, F = sp_.n_ff;
+        const size_t E = size_t(sp_.n_embd);
         std::vector<const Resident*> rs(span_keys_.size());
         for (size_t i = 0; i < rs.size(); ++i) {
             auto it = map_.find(span_keys_[i]);
@@ -398,55 +514,121 @@ public:
             rs[i] = &it->second;
         }
         if (n_tok == 1) return span_decode(x, pos0, rs);
-        size_t act = 0;
-        for (int n_in : {E, Q, F}) act = std::max(act, act_layout(n_tok, n_in).total);
-        if (!act || !reserve(0, act, 0) || !grow_span_ws(span_ws_bytes(n_tok, pos0 + n_tok))) return false;
-        SpanBufs B = span_bufs(d_span_ws_, n_tok, pos0 + n_tok);
-        hipError_t e = hipMemcpyAsync(B.x, x, size_t(n_tok) * E * 4, hipMemcpyHostToDevice, stream_);
-        if (e == hipSuccess) e = span_layers(rs, B, n_tok, pos0, nullptr, d_act_);
-        // x is written only once everything has run
+        // chunks of at most kSpanChunk tokens, in order (each attends over the
+        // cache rows the earlier ones wrote); the results gather in pinned host
+        // memory and reach x only once every chunk has run
+        if (!grow_host(size_t(n_tok) * E * 4)) return false;
+        const SpanBufs B = span_bufs(d_span_ws_, kSpanChunk, sp_.n_ctx);
+        last_bufs_ = B;
+        last_tok_ = std::min(kSpanChunk, n_tok - (n_tok - 1) / kSpanChunk * kSpanChunk);
+        last_pos0_ = pos0 + (n_tok - 1) / kSpanChunk * kSpanChunk;
+        hipError_t e = hipSuccess;
+        for (int c0 = 0; c0 < n_tok && e == hipSuccess; c0 += kSpanChunk) {
+            const int n = std::min(kSpanChunk, n_tok - c0);
+            e = hipMemcpyAsync(B.x, x + size_t(c0) * E, size_t(n) * E * 4, hipMemcpyHostToDevice, stream_);
+            if (e == hipSuccess) e = span_layers(rs, B, n, pos0 + c0, nullptr, d_act_);
+            if (e == hipSuccess)
+                e = hipMemcpyAsync(static_cast<float*>(h_y_) + size_t(c0) * E, B.x, size_t(n) * E * 4,
+                                   hipMemcpyDeviceToHost, stream_);
+        }
         if (e == hipSuccess) e = hipStreamSynchronize(stream_);
-        if (e == hipSuccess) e = hipMemcpy(x, B.x, size_t(n_tok) * E * 4, hipMemcpyDeviceToHost);
         if (e != hipSuccess) {
             mark_broken(e, "span_forward");
             return false;
         }
+        std::memcpy(x, h_y_, size_t(n_tok) * E * 4);
         ++served_;
         return true;
     }
 
+    // A buffer of the last span call's last chunk (part ids in span_sizes'
+    // order, 0..11), or rows [pos0, pos0 + n) of layer `layer`'s f16 K (part 100)
+    // or V (part 101) cache as f32, copied to host `out` of n_floats floats.
+    bool span_inspect(int part, int layer, int pos0, int n, float* out, uint64_t n_floats) {
+        std::lock_guard<std::mutex> lk(mu_);
+        if (!span_on_ || broken_ || !out) return false;
+        hipError_t e = hipSuccess;
+        if (part == 100 || part == 101) {
+            const size_t KV = size_t(sp_.n_head_kv) * sp_.head_dim;
+            if (layer < 0 || layer >= sp_.n_layers || pos0 < 0 || n <= 0 || pos0 + n > sp_.n_ctx ||
+                n_floats < size_t(n) * KV)
+                return false;
+            const _Float16* src = (part == 100 ? d_kc_ : d_vc_) + (size_t(layer) * sp_.n_ctx + pos0) * KV;
+            std::vector<_Float16> tmp(size_t(n) * KV);
+            e = hipMemcpy(tmp.data(), src, tmp.size() * 2, hipMemcpyDeviceToHost);
+            if (e == hipSuccess)
+                for (size_t i = 0; i < tmp.size(); ++i) out[i] = float(tmp[i]);
+        } else {
+            if (last_tok_ <= 0 || part < 0 || part >= kSpanBufs - 1) return false;
+            size_t z[kSpanBufs], cnt[kSpanBufs];
+            span_sizes(last_tok_, last_bufs_.ld, z, cnt);
+            float* const bufs[kSpanBufs - 1] = {last_bufs_.x,   last_bufs_.xb,  last_bufs_.q,    last_bufs_.k,
+                                                last_bufs_.v,   last_bufs_.qr,  last_bufs_.att,  last_bufs_.proj,
+                                                last_bufs_.xb2, last_bufs_.g,   last_bufs_.u,    last_bufs_.dn};
+            if (n_floats < cnt[part]) return false;
+            e = hipMemcpy(out, bufs[part], cnt[part] * 4, hipMemcpyDeviceToHost);
+        }
+        if (e != hipSuccess) {
+            mark_broken(e, "span_inspect");
+            return false;
+        }
+        return true;
+    }
+
+    int span_last_tokens() {
+        std::lock_guard<std::mutex> lk(mu_);
+        return span_on_ ? last_tok_ : 0;
+    }
+
 private:
-    // Device scratch of one span call: x, xb, q, k, v, q_rot, attn, proj, g, u,
-    // attention partials (positions < ld), each 256-byte aligned; then the position.
+    static constexpr int kSpanChunk = 256;  // FISH's largest forward batch (model.h:292)
+    static constexpr int kSpanVecs = 8;     // per-layer vectors kept on the device
+
+    // Device scratch of one span call, each buffer 256-byte aligned, in this
+    // order (the fish_hip_span_inspect part ids): x, xb (attention norm out),
+    // q, k, v (projections), qr (q after bias, norm and RoPE), att, proj (o
+    // projection), xb2 (FFN norm out), g (silu(g) * u after the FFN), u, dn
+    // (down projection), attention partials (positions < ld); then the position.
+    static constexpr int kSpanBufs = 13;
     struct SpanBufs {
-        float *x, *xb, *q, *k, *v, *qr, *att, *proj, *g, *u, *sc;
+        float *x, *xb, *q, *k, *v, *qr, *att, *proj, *xb2, *g, *u, *dn, *sc;
         int* pos;
         int ld;
     };
-    void span_sizes(int n_tok, int ld, size_t (&z)[11]) const {
+    void span_sizes(int n_tok, int ld, size_t (&z)[kSpanBufs], size_t (&cnt)[kSpanBufs]) const {
         const size_t T = size_t(n_tok), E = size_t(sp_.n_embd), Q = size_t(sp_.n_head) * sp_.head_dim,
                      KV = size_t(sp_.n_head_kv) * sp_.head_dim, F = size_t(sp_.n_ff);
-        const size_t v[11] = {T * E, T * E, T * Q, T * KV, T * KV, T * Q, T * Q, T * E, T * F, T * F,
-                              attention_scratch_floats(n_tok, sp_.n_head, sp_.head_dim, ld)};
-        for (int i = 0; i < 11; ++i) z[i] = (v[i] * 4 + 255) / 256 * 256;
+        // partials for the largest call that splits attention (at most kAttnSplitTok tokens)
+        const size_t part = attention_scratch_floats(std::min(n_tok, kAttnSplitTok), sp_.n_head, sp_.head_dim, ld);
+        const size_t v[kSpanBufs] = {T * E, T * E, T * Q, T * KV, T * KV, T * Q, T * Q,
+                                     T * E, T * E, T * F, T * F, T * E, part};
+        for (int i = 0; i < kSpanBufs; ++i) {
+            cnt[i] = v[i];
+            z[i] = (v[i] * 4 + 255) / 256 * 256;
+        }
     }
     size_t span_ws_bytes(int n_tok, int ld) const {
-        size_t z[11], total = 256;
-        span_sizes(n_tok, ld, z);
+        size_t z[kSpanBufs], cnt[kSpanBufs], total = 256;
+        span_sizes(n_tok, ld, z, cnt);
         for (size_t b : z) total += b;
         return total;
     }
     SpanBufs span_bufs(void* base, int n_tok, int ld) const {
-        size_t z[11];
-        span_sizes(n_tok, ld, z);
+        size_t z[kSpanBufs], cnt[kSpanBufs];
+        span_sizes(n_tok, ld, z, cnt);
         char* b = static_cast<char*>(base);
-        float* p[11];
-        for (int i = 0; i < 11; ++i) {
+        float* p[kSpanBufs];
+        for (int i = 0; i < kSpanBufs; ++i) {
             p[i] = reinterpret_cast<float*>(b);
             b += z[i];
         }
-        return SpanBufs{p[0], p[1], p[2], p[3], p[4], p[5], p[6], p[7], p[8], p[9], p[10],
+        return SpanBufs{p[0], p[1], p[2], p[3], p[4], p[5], p[6], p[7], p[8], p[9], p[10], p[11], p[12],
                         reinterpret_cast<int*>(b), ld};
+    }
+    // device copy of per-layer vector i of layer l, or nullptr when the layer has none
+    const float* span_vec(int l, int i) const {
+        const size_t at = span_vec_off_[size_t(l) * kSpanVecs + i];
+        return at == SIZE_MAX ? nullptr : reinterpret_cast<const float*>(reinterpret_cast<const char*>(d_vecs_) + at);
     }
 
     // The span's layers on B.x (model.cpp:1650-1801), asynchronous on stream_;
@@ -462,35 +644,37 @@ private:
         const float* pending = nullptr;
         for (int l = 0; l < sp_.n_layers && e == hipSuccess; ++l) {
             const Resident* const* W = rs.data() + size_t(7 * l);
-            float* kc = d_kc_ + size_t(l) * sp_.n_ctx * KV;
-            float* vc = d_vc_ + size_t(l) * sp_.n_ctx * KV;
+            _Float16* kc = d_kc_ + size_t(l) * sp_.n_ctx * KV;
+            _Float16* vc = d_vc_ + size_t(l) * sp_.n_ctx * KV;
+            const SpanVecs vecs{span_vec(l, 2), span_vec(l, 3), span_vec(l, 4), span_vec(l, 5), span_vec(l, 6)};
             const int n_qkv[3] = {Q, KV, KV}, n_e[1] = {E}, n_f[2] = {F, F};
             float* y_qkv[3] = {B.q, B.k, B.v};
             float* y_o[1] = {B.proj};
             float* y_gu[2] = {B.g, B.u};
-            e = launch_rmsnorm(B.x, pending, d_norms_ + size_t(2 * l) * E, B.xb, n_tok, E, sp_.eps, stream_);
+            float* y_d[1] = {B.dn};
+            e = launch_rmsnorm(B.x, pending, nullptr, span_vec(l, 0), B.xb, n_tok, E, sp_.eps, stream_);
             if (e == hipSuccess) e = run_group(W, 3, B.xb, n_tok, E, n_qkv, y_qkv, act);
             if (e == hipSuccess)
-                e = launch_rope_store(B.q, B.k, B.v, B.qr, kc, vc, n_tok, H, HKV, D, sp_.rot_dim, sp_.rope_neox != 0,
-                                      pos0, d_cos_, d_sin_, stream_, pos_dev);
+                e = launch_qkv_prep(B.q, B.k, B.v, vecs, B.qr, kc, vc, n_tok, H, HKV, D, sp_.rot_dim,
+                                    sp_.rope_neox != 0, sp_.eps, pos0, d_cos_, d_sin_, stream_, pos_dev);
             if (e == hipSuccess)
                 e = launch_attention(B.qr, kc, vc, B.att, B.sc, B.ld, n_tok, H, HKV, D, pos0, scale, stream_, pos_dev);
             if (e == hipSuccess) e = run_group(W + 3, 1, B.att, n_tok, Q, n_e, y_o, act);
             if (e == hipSuccess)
-                e = launch_rmsnorm(B.x, B.proj, d_norms_ + size_t(2 * l + 1) * E, B.xb, n_tok, E, sp_.eps, stream_);
-            if (e == hipSuccess) e = run_group(W + 4, 2, B.xb, n_tok, E, n_f, y_gu, act);
+                e = launch_rmsnorm(B.x, B.proj, span_vec(l, 7), span_vec(l, 1), B.xb2, n_tok, E, sp_.eps, stream_);
+            if (e == hipSuccess) e = run_group(W + 4, 2, B.xb2, n_tok, E, n_f, y_gu, act);
             if (e == hipSuccess) e = launch_silu_mul(B.g, B.u, T * F, stream_);
-            if (e == hipSuccess) e = run_group(W + 6, 1, B.g, n_tok, F, n_e, y_o, act);
-            pending = B.proj;
+            if (e == hipSuccess) e = run_group(W + 6, 1, B.g, n_tok, F, n_e, y_d, act);
+            pending = B.dn;
         }
         if (e == hipSuccess) e = launch_add(B.x, pending, T * E, stream_);
         return e;
     }
 
     // One decode token: the layer sequence is captured once into a HIP graph
-    // over fixed scratch (its own activation buffer, attention partials for n_ctx,
-    // the position in device memory) and replayed per token, so the launches of
-    // all layers cost one graph launch.
+    // over fixed scratch (allocated at span_prepare: attention partials for
+    // n_ctx, its own activation buffer, the position in device memory) and
+    // replayed per token, so the launches of all layers cost one graph launch.
     bool span_decode(float* x, int pos0, const std::vector<const Resident*>& rs) {
         const int E = sp_.n_embd;
         hipError_t e = hipSuccess;
@@ -500,23 +684,13 @@ private:
         if (dec_exec_ && devs != dec_devs_) {
             (void)hipGraphExecDestroy(dec_exec_);
             dec_exec_ = nullptr;
-            (void)hipFree(d_dec_);
-            d_dec_ = nullptr;
         }
         if (!dec_exec_) {
-            size_t act = 0;
-            for (int n_in : {E, sp_.n_head * sp_.head_dim, sp_.n_ff}) act = std::max(act, act_layout(1, n_in).total);
-            const size_t ws = span_ws_bytes(1, sp_.n_ctx);
-            if (!act || hipMalloc(&d_dec_, ws + act) != hipSuccess) {
-                d_dec_ = nullptr;
-                return false;
-            }
             dec_ = span_bufs(d_dec_, 1, sp_.n_ctx);
-            void* dact = static_cast<char*>(d_dec_) + ws;
             hipGraph_t g = nullptr;
             e = hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal);
             if (e == hipSuccess) {
-                const hipError_t le = span_layers(rs, dec_, 1, 0, dec_.pos, dact);
+                const hipError_t le = span_layers(rs, dec_, 1, 0, dec_.pos, d_dec_act_);
                 e = hipStreamEndCapture(stream_, &g);
                 if (e == hipSuccess) e = le;
             }
@@ -529,16 +703,22 @@ private:
             }
             dec_devs_ = devs;
         }
-        const int pos_host = pos0;
+        last_bufs_ = dec_;
+        last_tok_ = 1;
+        last_pos0_ = pos0;
+        if (!grow_host(size_t(E) * 4 + 256)) return false;
+        int* pos_host = reinterpret_cast<int*>(static_cast<char*>(h_y_) + size_t(E) * 4);
+        *pos_host = pos0;
         e = hipMemcpyAsync(dec_.x, x, size_t(E) * 4, hipMemcpyHostToDevice, stream_);
-        if (e == hipSuccess) e = hipMemcpyAsync(dec_.pos, &pos_host, sizeof(int), hipMemcpyHostToDevice, stream_);
+        if (e == hipSuccess) e = hipMemcpyAsync(dec_.pos, pos_host, sizeof(int), hipMemcpyHostToDevice, stream_);
         if (e == hipSuccess) e = hipGraphLaunch(dec_exec_, stream_);
+        if (e == hipSuccess) e = hipMemcpyAsync(h_y_, dec_.x, size_t(E) * 4, hipMemcpyDeviceToHost, stream_);
         if (e == hipSuccess) e = hipStreamSynchronize(stream_);
-        if (e == hipSuccess) e = hipMemcpy(x, dec_.x, size_t(E) * 4, hipMemcpyDeviceToHost);
         if (e != hipSuccess) {
             mark_broken(e, "span_forward");
             return false;
         }
+        std::memcpy(x, h_y_, size_t(E) * 4);
         ++served_;
         return true;
     }
@@ -616,25 +796,18 @@ private:
         return e;
     }
 
-    bool grow_span_ws(size_t need) {
-        if (need <= cap_span_ws_) return true;
-        if (d_span_ws_) (void)hipFree(d_span_ws_);
-        d_span_ws_ = nullptr;
-        cap_span_ws_ = 0;
-        if (hipMalloc(&d_span_ws_, need) != hipSuccess) return false;
-        cap_span_ws_ = need;
-        return true;
-    }
-
     void span_free() {
         if (dec_exec_) (void)hipGraphExecDestroy(dec_exec_);
         dec_exec_ = nullptr;
-        if (d_dec_) (void)hipFree(d_dec_);
-        d_dec_ = nullptr;
         if (d_span_fixed_) (void)hipFree(d_span_fixed_);
         d_span_fixed_ = nullptr;
+        d_vecs_ = d_cos_ = d_sin_ = nullptr;
+        d_kc_ = d_vc_ = nullptr;
+        d_span_ws_ = d_dec_ = d_dec_act_ = nullptr;
         span_keys_.clear();
+        span_vec_off_.clear();
         span_on_ = false;
+        last_tok_ = 0;
     }
 
     HipBackend() = default;
@@ -652,17 +825,43 @@ private:
         return ok_ = true;
     }
 
+    // hipMalloc within the headroom rule (vram_headroom_bytes): refused, not an
+    // error, when the allocation would leave less than the headroom free
+    hipError_t dev_alloc(void** p, size_t bytes) {
+        *p = nullptr;
+        size_t f = 0, t = 0;
+        if (hipMemGetInfo(&f, &t) != hipSuccess) return hipErrorOutOfMemory;
+        if (bytes > f || f - bytes < vram_headroom_bytes(t)) return hipErrorOutOfMemory;
+        const hipError_t e = hipMalloc(p, bytes);
+        if (e != hipSuccess) *p = nullptr;
+        return e;
+    }
+
+    bool grow_buffer(void*& p, size_t& cap, size_t need) {
+        if (need <= cap) return true;
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        cap = 0;
+        if (dev_alloc(&p, need) != hipSuccess) return false;
+        cap = need;
+        return true;
+    }
+
+    bool grow_host(size_t need) {
+        if (need <= cap_h_y_) return true;
+        if (h_y_) (void)hipHostFree(h_y_);
+        h_y_ = nullptr;
+        cap_h_y_ = 0;
+        if (hipHostMalloc(&h_y_, need, hipHostMallocDefault) != hipSuccess) {
+            h_y_ = nullptr;
+            return false;
+        }
+        cap_h_y_ = need;
+        return true;
+    }
+
     bool reserve(size_t xb, size_t ab, size_t yb) {
-        auto grow = [&](void*& p, size_t& cap, size_t need) {
-            if (need <= cap) return true;
-            if (p) (void)hipFree(p);
-            p = nullptr;
-            cap = 0;
-            if (hipMalloc(&p, need) != hipSuccess) return false;
-            cap = need;
-            return true;
-        };
-        return grow(d_x_, cap_x_, xb) && grow(d_act_, cap_act_, ab) && grow(d_y_, cap_y_, yb);
+        return grow_buffer(d_x_, cap_x_, xb) && grow_buffer(d_act_, cap_act_, ab) && grow_buffer(d_y_, cap_y_, yb);
     }
 
     void mark_broken(hipError_t e, const char* what) {
@@ -680,18 +879,30 @@ private:
     uint64_t bytes_ = 0;
     void *d_x_ = nullptr, *d_act_ = nullptr, *d_y_ = nullptr;
     size_t cap_x_ = 0, cap_act_ = 0, cap_y_ = 0;
-    // layer span: parameters, weight keys (7 per layer), norms / RoPE tables /
-    // KV cache in one allocation, per-call scratch
+    // upload staging (whole rows, at most kStageBytes), expert-FFN workspace,
+    // pinned host staging of matmul outputs
+    static constexpr size_t kStageBytes = size_t(64) << 20;
+    void* d_stage_ = nullptr;
+    size_t cap_stage_ = 0;
+    void* d_moe_ = nullptr;
+    size_t cap_moe_ = 0;
+    void* h_y_ = nullptr;
+    size_t cap_h_y_ = 0;
+    // layer span: parameters, weight keys (7 per layer); one allocation holds the
+    // per-layer vectors, RoPE tables, f16 KV cache and every per-call buffer
     bool span_on_ = false;
     fish_hip_span_params sp_{};
     std::vector<const void*> span_keys_;
+    std::vector<size_t> span_vec_off_;  // [layer][kSpanVecs] byte offset in d_vecs_, SIZE_MAX = absent
     void* d_span_fixed_ = nullptr;
-    float *d_norms_ = nullptr, *d_cos_ = nullptr, *d_sin_ = nullptr, *d_kc_ = nullptr, *d_vc_ = nullptr;
-    void* d_span_ws_ = nullptr;
-    size_t cap_span_ws_ = 0;
-    // decode graph over fixed scratch (built at the first one-token call)
+    float *d_vecs_ = nullptr, *d_cos_ = nullptr, *d_sin_ = nullptr;
+    _Float16 *d_kc_ = nullptr, *d_vc_ = nullptr;
+    void *d_span_ws_ = nullptr, *d_dec_ = nullptr, *d_dec_act_ = nullptr;
+    // buffers of the last span call's last chunk (fish_hip_span_inspect)
+    SpanBufs last_bufs_{};
+    int last_tok_ = 0, last_pos0_ = 0;
+    // decode graph over the fixed decode buffers (built at the first one-token call)
     hipGraphExec_t dec_exec_ = nullptr;
-    void* d_dec_ = nullptr;
     SpanBufs dec_{};
     std::vector<const void*> dec_devs_;
 };
@@ -894,12 +1105,25 @@ int fish_hip_backend_matmul(const void* key, const float* x, int n_tok, int n_in
     return HipBackend::instance().matmul_group(keys, 1, x, n_tok, n_in, &n_out, ys) ? 1 : 0;
 }
 
+int fish_hip_backend_moe_ffn(const void* key_gate, const void* key_up, const void* key_down, const void* key_router,
+                             const float* x, const float* logits, int n_tok, int n_embd, int n_ff, int n_expert, int k,
+                             int norm, float* out) {
+    return HipBackend::instance().moe_ffn_host(key_gate, key_up, key_down, key_router, x, logits, n_tok, n_embd, n_ff,
+                                               n_expert, k, norm, out)
+               ? 1
+               : 0;
+}
+
 int fish_hip_span_prepare(const fish_hip_span_params* p) {
     return p && HipBackend::instance().span_prepare(*p) ? 1 : 0;
 }
 int fish_hip_span_forward(float* x, int n_tok, int pos0) {
     return HipBackend::instance().span_forward(x, n_tok, pos0) ? 1 : 0;
 }
+int fish_hip_span_inspect(int part, int layer, int pos0, int n, float* out, uint64_t n_floats) {
+    return HipBackend::instance().span_inspect(part, layer, pos0, n, out, n_floats) ? 1 : 0;
+}
+int fish_hip_span_last_tokens(void) { return HipBackend::instance().span_last_tokens(); }
 void fish_hip_span_kv_truncate(int n_past) { (void)n_past; }  // positions >= n_past are rewritten before use
 void fish_hip_span_release(void) { HipBackend::instance().span_release(); }
 

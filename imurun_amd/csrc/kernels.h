@@ -86,6 +86,10 @@ hipError_t launch_moe_combine(const float* down, const MoeRouting& r, int n_tok,
 
 // GGUF rows (device bytes) -> repacked device layout (weight_layout()).
 hipError_t launch_repack(uint32_t type, const void* gguf, int n_in, int n_out, void* dst, hipStream_t stream);
+// The same for rows row0 .. row0 + n_rows - 1 of an n_out-row tensor (gguf holds
+// just those rows): uploads stage a large tensor through a bounded buffer.
+hipError_t launch_repack_rows(uint32_t type, const void* gguf, int n_in, int n_out, int row0, int n_rows, void* dst,
+                              hipStream_t stream);
 
 // Token mapping of a few-token matmul launch. Plain launches (items ==
 // nullptr) take tokens 0..n_tok-1 of the activation buffer and write the same
@@ -144,20 +148,32 @@ struct GemmGroup {
 hipError_t launch_gemm_group(int n, const void* const* ws, const WeightLayout* WLs, const void* act, int n_tok,
                              float* const* ys, const int* ldys, hipStream_t stream);
 
-// Layer-span steps (span.hip): rmsnorm per token row; RoPE of q into q_out and
-// of k into the KV-cache rows pos0.. (with v); causal GQA attention per
-// (token, head), split over chunks of positions < ld (ld >= pos0 + n_tok); g = silu(g) * u; x += y. With pos_dev, RoPE and attention read the
-// first position from device memory instead of pos0 (a graph replayed for every
-// decode position; the caller keeps pos_dev[0] + n_tok <= the cache and ld).
-// rmsnorm with y != nullptr first adds y into x (x += y, written back).
-hipError_t launch_rmsnorm(float* x, const float* y, const float* w, float* out, int n_tok, int n, float eps,
-                          hipStream_t s);
-hipError_t launch_rope_store(const float* q, const float* k, const float* v, float* q_out, float* kc, float* vc,
-                             int n_tok, int H, int HKV, int D, int rot_dim, bool neox, int pos0, const float* cosv,
-                             const float* sinv, hipStream_t s, const int* pos_dev = nullptr);
-// `part` holds attention_scratch_floats(n_tok, H, D, ld) floats.
+// Layer-span steps (span.hip): rmsnorm per token row; q/k/v preparation (biases,
+// per-head q/k RMS norms, RoPE of q into q_out and of k into the f16 KV-cache
+// rows pos0.., v into its cache rows); causal GQA attention per (token, head)
+// over positions < ld (ld >= pos0 + n_tok): a few tokens split over position
+// chunks with partials in `part`, more tokens in one pass; g = silu(g) * u;
+// x += y. With pos_dev, the kernels read the first position from device memory
+// instead of pos0 (a graph replayed for every decode position; the caller
+// keeps pos_dev[0] + n_tok <= the cache and ld). rmsnorm with y != nullptr
+// first adds y (+ b when given) into x (written back).
+struct SpanVecs {
+    const float* q_norm;  // [head_dim] or null (Qwen-3)
+    const float* k_norm;
+    const float* bias_q;  // [q_dim] or null
+    const float* bias_k;  // [kv_dim]
+    const float* bias_v;
+};
+constexpr int kAttnSplitTok = 4;  // tokens per call that split attention over position chunks
+hipError_t launch_rmsnorm(float* x, const float* y, const float* b, const float* w, float* out, int n_tok, int n,
+                          float eps, hipStream_t s);
+hipError_t launch_qkv_prep(const float* q, const float* k, const float* v, const SpanVecs& vecs, float* q_out,
+                           _Float16* kc, _Float16* vc, int n_tok, int H, int HKV, int D, int rot_dim, bool neox,
+                           float eps, int pos0, const float* cosv, const float* sinv, hipStream_t s,
+                           const int* pos_dev = nullptr);
+// `part` holds attention_scratch_floats(n_tok, H, D, ld) floats (0 above kAttnSplitTok tokens).
 size_t attention_scratch_floats(int n_tok, int H, int D, int ld);
-hipError_t launch_attention(const float* q, const float* kc, const float* vc, float* out, float* part, int ld,
+hipError_t launch_attention(const float* q, const _Float16* kc, const _Float16* vc, float* out, float* part, int ld,
                             int n_tok, int H, int HKV, int D, int pos0, float scale, hipStream_t s,
                             const int* pos_dev = nullptr);
 hipError_t launch_silu_mul(float* g, const float* u, size_t n, hipStream_t s);

@@ -33,14 +33,15 @@ __device__ __forceinline__ int q6k_code(const uint8_t* sb, int e) {
     return lo | (hi << 4);
 }
 
-// One thread per (row, 32-element group).
-__global__ void repack_kernel(uint32_t type, const uint8_t* __restrict__ src, int n_in, int n_out, size_t src_row,
-                              uint8_t* __restrict__ dst, WeightLayout L) {
+// One thread per (row, 32-element group) of rows row0 .. row0 + n_rows - 1 of
+// the tensor whose layout is L; src holds those rows' GGUF bytes.
+__global__ void repack_kernel(uint32_t type, const uint8_t* __restrict__ src, int n_in, int row0, int n_rows,
+                              size_t src_row, uint8_t* __restrict__ dst, WeightLayout L) {
     const long gid = long(blockIdx.x) * blockDim.x + threadIdx.x;
     const int groups = n_in / 32;
-    if (gid >= long(n_out) * groups) return;
-    const int r = int(gid / groups), c = int(gid % groups);
-    const uint8_t* row = src + size_t(r) * src_row;
+    if (gid >= long(n_rows) * groups) return;
+    const int rr = int(gid / groups), c = int(gid % groups), r = row0 + rr;
+    const uint8_t* row = src + size_t(rr) * src_row;
     uint8_t* codes = dst + L.codes + (size_t(r) * groups + c) * 16;
     uint8_t q[32];
     switch (type) {
@@ -118,14 +119,19 @@ __global__ void repack_kernel(uint32_t type, const uint8_t* __restrict__ src, in
 
 }  // namespace
 
-hipError_t launch_repack(uint32_t type, const void* gguf, int n_in, int n_out, void* dst, hipStream_t stream) {
+hipError_t launch_repack_rows(uint32_t type, const void* gguf, int n_in, int n_out, int row0, int n_rows, void* dst,
+                              hipStream_t stream) {
     const WeightLayout L = weight_layout(type, n_in, n_out);
-    if (!L.total) return hipErrorInvalidValue;
-    const long threads = long(n_out) * (n_in / 32);
+    if (!L.total || row0 < 0 || n_rows <= 0 || row0 + n_rows > n_out) return hipErrorInvalidValue;
+    const long threads = long(n_rows) * (n_in / 32);
     const unsigned blocks = unsigned((threads + 255) / 256);
     hipLaunchKernelGGL(repack_kernel, dim3(blocks), dim3(256), 0, stream, type, static_cast<const uint8_t*>(gguf),
-                       n_in, n_out, gguf_row_bytes(type, n_in), static_cast<uint8_t*>(dst), L);
+                       n_in, row0, n_rows, gguf_row_bytes(type, n_in), static_cast<uint8_t*>(dst), L);
     return hipGetLastError();
+}
+
+hipError_t launch_repack(uint32_t type, const void* gguf, int n_in, int n_out, void* dst, hipStream_t stream) {
+    return launch_repack_rows(type, gguf, n_in, n_out, 0, n_out, dst, stream);
 }
 
 }  // namespace fishhip

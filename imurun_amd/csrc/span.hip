@@ -4,12 +4,19 @@
 //
 // Each kernel restates FISH's CPU step for one layer (model.cpp:1650-1790):
 //   rmsnorm      ops.cpp:18-23   (double sum of squares, f32 scale, x * scale * w)
-//   RoPE + KV    ops.cpp:126-152 (table rotation, neox or adjacent pairs) and the
-//                KV-cache store of model.cpp:1726-1734
+//   q/k/v prep   the projection biases (add_bias, model.cpp:1704-1706), the
+//                Qwen-3 per-head q/k RMS norms (model.cpp:1712-1719), RoPE
+//                (ops.cpp:126-152, neox or adjacent pairs) and the KV-cache
+//                store (model.cpp:1721-1729), in one kernel
 //   attention    ops.cpp:303-357 (causal, GQA head groups, max-subtracted exp,
-//                softmax-weighted sum of V; split over position chunks)
+//                softmax-weighted sum of V; a decode token split over position
+//                chunks, more tokens in one pass per (token, head))
 //   silu * up    ops.cpp:25-30, model.cpp:1504-1508
-//   residual add model.cpp:1772-1776, :1797-1801 (fused into the next rmsnorm)
+//   residual add model.cpp:1772-1776, :1797-1801, with the o bias
+//                (model.cpp:1749) (fused into the next rmsnorm)
+// The KV cache holds f16 K and V (4 bytes per position and K+V element), as
+// FISH's own device span does (vulkan_backend.cpp:1650) and as its planner
+// budgets (model.cpp:1318-1320); values round to nearest even when stored.
 // The file is compiled without floating-point contraction, so every
 // expression rounds as FISH's baseline x86-64 build does; exp is the device's
 // expf, within a few ulp of the C library's.
@@ -51,10 +58,11 @@ __device__ __forceinline__ float block_reduce_f(float v, float* red, bool is_max
 }
 
 // one workgroup of kNormTh threads per token; with y, first x += y (the
-// residual add, written back to x), then out = rmsnorm(x)
+// residual add, written back to x; with b, y + b is added: the projection's
+// bias, then the residual), then out = rmsnorm(x)
 __global__ __launch_bounds__(kNormTh) void rmsnorm_kernel(float* __restrict__ x, const float* __restrict__ y,
-                                                          const float* __restrict__ w, float* __restrict__ out, int n,
-                                                          float eps) {
+                                                          const float* __restrict__ b, const float* __restrict__ w,
+                                                          float* __restrict__ out, int n, float eps) {
     __shared__ double red[kNormTh];
     float* xr = x + size_t(blockIdx.x) * n;
     const float* yr = y ? y + size_t(blockIdx.x) * n : nullptr;
@@ -64,7 +72,7 @@ __global__ __launch_bounds__(kNormTh) void rmsnorm_kernel(float* __restrict__ x,
     for (int i = threadIdx.x; i < n; i += kNormTh) {
         float v = xr[i];
         if (yr) {
-            v = v + yr[i];
+            v = v + (b ? yr[i] + b[i] : yr[i]);
             xr[i] = v;
         }
         s += double(v) * double(v);
@@ -74,45 +82,70 @@ __global__ __launch_bounds__(kNormTh) void rmsnorm_kernel(float* __restrict__ x,
     for (int i = threadIdx.x; i < n; i += kNormTh) orow[i] = xr[i] * scale * w[i];
 }
 
-// The rotated value of element f of a row of heads of D values (ops.cpp:126-152).
-__device__ __forceinline__ float rope_elem(const float* __restrict__ src, int f, int D, int half, int neox,
+// RoPE of element d of one head of D values held in LDS (ops.cpp:126-152).
+__device__ __forceinline__ float rope_elem(const float* __restrict__ row, int d, int half, int neox,
                                            const float* __restrict__ c, const float* __restrict__ s) {
-    const int base = f - f % D, d = f % D;
-    if (d >= 2 * half) return src[f];  // past rot_dim: unchanged
+    if (d >= 2 * half) return row[d];  // past rot_dim: unchanged
     if (neox) {
         const int i = d < half ? d : d - half;
-        const float x0 = src[base + i], x1 = src[base + i + half];
+        const float x0 = row[i], x1 = row[i + half];
         return d < half ? x0 * c[i] - x1 * s[i] : x0 * s[i] + x1 * c[i];
     }
     const int i = d >> 1;
-    const float x0 = src[base + 2 * i], x1 = src[base + 2 * i + 1];
+    const float x0 = row[2 * i], x1 = row[2 * i + 1];
     return (d & 1) ? x0 * s[i] + x1 * c[i] : x0 * c[i] - x1 * s[i];
 }
 
-// one workgroup per (token t, head): q heads first, then k heads; q_out =
-// rope(q), the cache rows of position pos0 + t get rope(k) and v
-__global__ __launch_bounds__(kTh) void rope_store_kernel(const float* __restrict__ q, const float* __restrict__ k,
-                                                         const float* __restrict__ v, float* __restrict__ q_out,
-                                                         float* __restrict__ kc, float* __restrict__ vc, int Q,
-                                                         int KV, int D, int half, int neox, int pos0,
-                                                         const int* __restrict__ pos_dev,
-                                                         const float* __restrict__ cosv,
-                                                         const float* __restrict__ sinv) {
+// One workgroup per (token t, head): q heads first, then k heads (whose
+// workgroup also stores the v head of the same index). Thread d owns element d
+// of the head (D <= kTh): value + bias, the per-head RMS norm when given (the
+// rmsnorm of ops.cpp:18-23 over the head's D values), RoPE; q -> q_out, k and
+// v -> f16 cache rows of position pos0 + t.
+__global__ __launch_bounds__(kTh) void qkv_prep_kernel(const float* __restrict__ q, const float* __restrict__ k,
+                                                       const float* __restrict__ v, SpanVecs vecs,
+                                                       float* __restrict__ q_out, _Float16* __restrict__ kc,
+                                                       _Float16* __restrict__ vc, int Q, int KV, int D, int half,
+                                                       int neox, float eps, int pos0, const int* __restrict__ pos_dev,
+                                                       const float* __restrict__ cosv,
+                                                       const float* __restrict__ sinv) {
+    __shared__ float row[kTh];
+    __shared__ double red[kTh];
     if (pos_dev) pos0 = *pos_dev;
-    const int t = blockIdx.x, hh = blockIdx.y, pos = pos0 + t, H = Q / D;
+    const int t = blockIdx.x, hh = blockIdx.y, pos = pos0 + t, H = Q / D, d = threadIdx.x;
+    const bool is_q = hh < H;
+    const int head = is_q ? hh : hh - H;
+    const float* src = is_q ? q + size_t(t) * Q : k + size_t(t) * KV;
+    const float* bias = is_q ? vecs.bias_q : vecs.bias_k;
+    const float* nw = is_q ? vecs.q_norm : vecs.k_norm;
+    float val = 0.0f;
+    if (d < D) {
+        val = src[head * D + d];
+        if (bias) val = val + bias[head * D + d];
+    }
+    if (nw) {  // uniform over the workgroup
+        red[d] = d < D ? double(val) * double(val) : 0.0;
+        __syncthreads();
+        for (int st = kTh / 2; st > 0; st >>= 1) {
+            if (d < st) red[d] += red[d + st];
+            __syncthreads();
+        }
+        const float scale = 1.0f / sqrtf(float(red[0] / D) + eps);
+        if (d < D) val = val * scale * nw[d];
+    }
+    row[d] = val;
+    __syncthreads();
+    if (d >= D) return;
     const float* c = cosv + size_t(pos) * half;
     const float* s = sinv + size_t(pos) * half;
-    if (hh < H) {
-        const float* qr = q + size_t(t) * Q;
-        for (int f = hh * D + threadIdx.x; f < (hh + 1) * D; f += kTh)
-            q_out[size_t(t) * Q + f] = rope_elem(qr, f, D, half, neox, c, s);
+    const float r = rope_elem(row, d, half, neox, c, s);
+    if (is_q) {
+        q_out[size_t(t) * Q + head * D + d] = r;
     } else {
-        const float* kr = k + size_t(t) * KV;
-        const float* vr = v + size_t(t) * KV;
-        for (int f = (hh - H) * D + threadIdx.x; f < (hh - H + 1) * D; f += kTh) {
-            kc[size_t(pos) * KV + f] = rope_elem(kr, f, D, half, neox, c, s);
-            vc[size_t(pos) * KV + f] = vr[f];
-        }
+        const size_t at = size_t(pos) * KV + head * D + d;
+        kc[at] = _Float16(r);
+        float vv = v[size_t(t) * KV + head * D + d];
+        if (vecs.bias_v) vv = vv + vecs.bias_v[head * D + d];
+        vc[at] = _Float16(vv);
     }
 }
 
@@ -131,8 +164,8 @@ __global__ __launch_bounds__(kTh) void rope_store_kernel(const float* __restrict
 constexpr int kCh = 64;
 
 template <int DL>
-__global__ __launch_bounds__(kTh) void attn_part_kernel(const float* __restrict__ q, const float* __restrict__ kc,
-                                                        const float* __restrict__ vc, float* __restrict__ part,
+__global__ __launch_bounds__(kTh) void attn_part_kernel(const float* __restrict__ q, const _Float16* __restrict__ kc,
+                                                        const _Float16* __restrict__ vc, float* __restrict__ part,
                                                         int S, int H, int HKV, int D, int pos0,
                                                         const int* __restrict__ pos_dev, float scale) {
     constexpr int PB = kCh / 4;
@@ -157,16 +190,16 @@ __global__ __launch_bounds__(kTh) void attn_part_kernel(const float* __restrict_
     float qv[DL];
 #pragma unroll
     for (int i = 0; i < DL; ++i) qv[i] = lane + 64 * i < D ? q[size_t(t) * Q + size_t(h) * D + lane + 64 * i] : 0.0f;
-    const float* kb = kc + size_t(kvh) * D;
-    const float* vb = vc + size_t(kvh) * D;
+    const _Float16* kb = kc + size_t(kvh) * D;
+    const _Float16* vb = vc + size_t(kvh) * D;
 
     // scores of positions j0 + w + 4 b
     float kv[PB][DL];
 #pragma unroll
     for (int b = 0; b < PB; ++b) {
-        const float* kr = kb + size_t(min(j0 + w + 4 * b, jn)) * KV;
+        const _Float16* kr = kb + size_t(min(j0 + w + 4 * b, jn)) * KV;
 #pragma unroll
-        for (int i = 0; i < DL; ++i) kv[b][i] = lane + 64 * i < D ? kr[lane + 64 * i] : 0.0f;
+        for (int i = 0; i < DL; ++i) kv[b][i] = lane + 64 * i < D ? float(kr[lane + 64 * i]) : 0.0f;
     }
 #pragma unroll
     for (int b = 0; b < PB; ++b) {
@@ -196,9 +229,9 @@ __global__ __launch_bounds__(kTh) void attn_part_kernel(const float* __restrict_
     float vv[PB][DL];
 #pragma unroll
     for (int b = 0; b < PB; ++b) {
-        const float* vr = vb + size_t(min(j0 + w + 4 * b, jn)) * KV;
+        const _Float16* vr = vb + size_t(min(j0 + w + 4 * b, jn)) * KV;
 #pragma unroll
-        for (int i = 0; i < DL; ++i) vv[b][i] = lane + 64 * i < D ? vr[lane + 64 * i] : 0.0f;
+        for (int i = 0; i < DL; ++i) vv[b][i] = lane + 64 * i < D ? float(vr[lane + 64 * i]) : 0.0f;
     }
     float acc[DL];
 #pragma unroll
@@ -253,6 +286,96 @@ __global__ __launch_bounds__(kTh) void attn_combine_kernel(const float* __restri
     if (tid < D) out[size_t(t) * H * D + size_t(h) * D + tid] = o * inv;
 }
 
+// Attention of more tokens (prefill): one workgroup per (token, head) walks
+// the chunks of kCh positions up to the token's own, each chunk as in
+// attn_part_kernel, and merges them into a running (max, sum, output) --
+// no partials in memory, so the scratch does not grow with tokens x context.
+template <int DL>
+__global__ __launch_bounds__(kTh) void attn_full_kernel(const float* __restrict__ q, const _Float16* __restrict__ kc,
+                                                        const _Float16* __restrict__ vc, float* __restrict__ out,
+                                                        int H, int HKV, int D, int pos0,
+                                                        const int* __restrict__ pos_dev, float scale) {
+    constexpr int PB = kCh / 4;
+    __shared__ float s_e[kCh];
+    __shared__ float s_o[4][64 * DL];
+    __shared__ float s_ml[2];
+    if (pos_dev) pos0 = *pos_dev;
+    const int item = blockIdx.x, t = item / H, h = item % H;
+    const int pos = pos0 + t, kvh = h / (H / HKV), KV = HKV * D, Q = H * D;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    float qv[DL];
+#pragma unroll
+    for (int i = 0; i < DL; ++i) qv[i] = lane + 64 * i < D ? q[size_t(t) * Q + size_t(h) * D + lane + 64 * i] : 0.0f;
+    const _Float16* kb = kc + size_t(kvh) * D;
+    const _Float16* vb = vc + size_t(kvh) * D;
+    float o_run = 0.0f, m_run = -INFINITY, l_run = 0.0f;
+    for (int j0 = 0; j0 <= pos; j0 += kCh) {
+        const int jn = min(pos, j0 + kCh - 1);
+        float kv[PB][DL];
+#pragma unroll
+        for (int b = 0; b < PB; ++b) {
+            const _Float16* kr = kb + size_t(min(j0 + w + 4 * b, jn)) * KV;
+#pragma unroll
+            for (int i = 0; i < DL; ++i) kv[b][i] = lane + 64 * i < D ? float(kr[lane + 64 * i]) : 0.0f;
+        }
+#pragma unroll
+        for (int b = 0; b < PB; ++b) {
+            float sum = 0.0f;
+#pragma unroll
+            for (int i = 0; i < DL; ++i) sum += qv[i] * kv[b][i];
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+            if (lane == 0) s_e[w + 4 * b] = j0 + w + 4 * b <= jn ? sum * scale : -INFINITY;
+        }
+        __syncthreads();
+        if (w == 0) {
+            float m = s_e[lane];
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+            const float e = lane <= jn - j0 ? expf(s_e[lane] - m) : 0.0f;
+            float l = e;
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) l += __shfl_xor(l, off);
+            s_e[lane] = e;
+            if (lane == 0) {
+                s_ml[0] = m;
+                s_ml[1] = l;
+            }
+        }
+        __syncthreads();
+        float vv[PB][DL];
+#pragma unroll
+        for (int b = 0; b < PB; ++b) {
+            const _Float16* vr = vb + size_t(min(j0 + w + 4 * b, jn)) * KV;
+#pragma unroll
+            for (int i = 0; i < DL; ++i) vv[b][i] = lane + 64 * i < D ? float(vr[lane + 64 * i]) : 0.0f;
+        }
+        float acc[DL];
+#pragma unroll
+        for (int i = 0; i < DL; ++i) acc[i] = 0.0f;
+#pragma unroll
+        for (int b = 0; b < PB; ++b) {
+            const float e = s_e[w + 4 * b];  // 0 past jn
+#pragma unroll
+            for (int i = 0; i < DL; ++i) acc[i] += e * vv[b][i];
+        }
+#pragma unroll
+        for (int i = 0; i < DL; ++i) s_o[w][lane + 64 * i] = acc[i];
+        __syncthreads();
+        // merge the chunk (mc, lc, oc) into the running softmax
+        const float mc = s_ml[0], lc = s_ml[1], mn = fmaxf(m_run, mc);
+        const float a = m_run == -INFINITY ? 0.0f : expf(m_run - mn), bc = expf(mc - mn);
+        if (tid < D) {
+            const float oc = (s_o[0][tid] + s_o[1][tid]) + (s_o[2][tid] + s_o[3][tid]);
+            o_run = o_run * a + oc * bc;
+        }
+        l_run = l_run * a + lc * bc;
+        m_run = mn;
+        __syncthreads();  // the next chunk overwrites s_e, s_o, s_ml
+    }
+    if (tid < D) out[size_t(t) * Q + size_t(h) * D + tid] = o_run * (1.0f / l_run);
+}
+
 // g = silu(g) * u
 __global__ __launch_bounds__(kTh) void silu_mul_kernel(float* __restrict__ g, const float* __restrict__ u, size_t n) {
     const size_t i = size_t(blockIdx.x) * kTh + threadIdx.x;
@@ -272,28 +395,41 @@ unsigned blocks_for(size_t n) { return unsigned((n + kTh - 1) / kTh); }
 
 }  // namespace
 
-hipError_t launch_rmsnorm(float* x, const float* y, const float* w, float* out, int n_tok, int n, float eps,
-                          hipStream_t s) {
+hipError_t launch_rmsnorm(float* x, const float* y, const float* b, const float* w, float* out, int n_tok, int n,
+                          float eps, hipStream_t s) {
     if (n_tok <= 0 || n <= 0) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(rmsnorm_kernel, dim3(unsigned(n_tok)), dim3(kNormTh), 0, s, x, y, w, out, n, eps);
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(unsigned(n_tok)), dim3(kNormTh), 0, s, x, y, b, w, out, n, eps);
     return hipGetLastError();
 }
 
-hipError_t launch_rope_store(const float* q, const float* k, const float* v, float* q_out, float* kc, float* vc,
-                             int n_tok, int H, int HKV, int D, int rot_dim, bool neox, int pos0, const float* cosv,
-                             const float* sinv, hipStream_t s, const int* pos_dev) {
-    if (n_tok <= 0 || H <= 0 || HKV <= 0 || D <= 0 || rot_dim < 0 || rot_dim > D || rot_dim % 2) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(rope_store_kernel, dim3(unsigned(n_tok), unsigned(H + HKV)), dim3(kTh), 0, s, q, k, v, q_out, kc, vc, H * D,
-                       HKV * D, D, rot_dim / 2, neox ? 1 : 0, pos0, pos_dev, cosv, sinv);
+hipError_t launch_qkv_prep(const float* q, const float* k, const float* v, const SpanVecs& vecs, float* q_out,
+                           _Float16* kc, _Float16* vc, int n_tok, int H, int HKV, int D, int rot_dim, bool neox,
+                           float eps, int pos0, const float* cosv, const float* sinv, hipStream_t s,
+                           const int* pos_dev) {
+    if (n_tok <= 0 || H <= 0 || HKV <= 0 || D <= 0 || D > kTh || rot_dim < 0 || rot_dim > D || rot_dim % 2)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(qkv_prep_kernel, dim3(unsigned(n_tok), unsigned(H + HKV)), dim3(kTh), 0, s, q, k, v, vecs,
+                       q_out, kc, vc, H * D, HKV * D, D, rot_dim / 2, neox ? 1 : 0, eps, pos0, pos_dev, cosv, sinv);
     return hipGetLastError();
 }
 
-hipError_t launch_attention(const float* q, const float* kc, const float* vc, float* out, float* part, int ld,
+hipError_t launch_attention(const float* q, const _Float16* kc, const _Float16* vc, float* out, float* part, int ld,
                             int n_tok, int H, int HKV, int D, int pos0, float scale, hipStream_t s,
                             const int* pos_dev) {
     if (n_tok <= 0 || D <= 0 || D > kTh || HKV <= 0 || H % HKV || ld < pos0 + n_tok) return hipErrorInvalidValue;
+    const dim3 block(kTh);
+    if (n_tok > kAttnSplitTok) {
+        const dim3 grid(unsigned(n_tok * H));
+        if (D <= 64)
+            hipLaunchKernelGGL(attn_full_kernel<1>, grid, block, 0, s, q, kc, vc, out, H, HKV, D, pos0, pos_dev, scale);
+        else if (D <= 128)
+            hipLaunchKernelGGL(attn_full_kernel<2>, grid, block, 0, s, q, kc, vc, out, H, HKV, D, pos0, pos_dev, scale);
+        else
+            hipLaunchKernelGGL(attn_full_kernel<4>, grid, block, 0, s, q, kc, vc, out, H, HKV, D, pos0, pos_dev, scale);
+        return hipGetLastError();
+    }
     const int S = (ld + kCh - 1) / kCh;
-    const dim3 grid(unsigned(n_tok * H), unsigned(S)), block(kTh);
+    const dim3 grid(unsigned(n_tok * H), unsigned(S));
     if (D <= 64)
         hipLaunchKernelGGL(attn_part_kernel<1>, grid, block, 0, s, q, kc, vc, part, S, H, HKV, D, pos0, pos_dev, scale);
     else if (D <= 128)
@@ -305,6 +441,7 @@ hipError_t launch_attention(const float* q, const float* kc, const float* vc, fl
 }
 
 size_t attention_scratch_floats(int n_tok, int H, int D, int ld) {
+    if (n_tok > kAttnSplitTok) return 0;
     return size_t(n_tok) * H * size_t((ld + kCh - 1) / kCh) * size_t(D + 2);
 }
 

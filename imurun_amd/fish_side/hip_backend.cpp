@@ -49,22 +49,23 @@ public:
                                              ys) != 0;
     }
 
-    // Layer spans (backend.h:89-162) for dense llama-style layers: separate
-    // q/k/v and gate/up projections, RMS norms, RoPE, f32 KV cache, SiLU.
-    // Everything else a span can carry (fused qkv or gate|up, biases, q/k or
-    // post norms, soft-caps, sliding windows, GELU) is refused, and FISH then
-    // keeps routing per matmul.
+    // Layer spans (backend.h:89-162) for dense layers with separate q/k/v and
+    // gate/up projections, RMS norms, RoPE, an f16 KV cache and SiLU: llama, and
+    // the Qwen-2 projection biases and Qwen-3 per-head q/k norms. Everything
+    // else a span can carry (fused qkv or gate|up, post norms, soft-caps,
+    // sliding windows, GELU, the int8 KV cache) is refused, and FISH then keeps
+    // routing per matmul.
     bool span_prepare(const SpanParams& p) override {
         const int n = p.layer_end - p.layer_begin;
-        if (n <= 0 || !p.layers || p.attn_softcap > 0.0f || p.window > 0 || p.gelu) return false;
+        if (n <= 0 || !p.layers || p.attn_softcap > 0.0f || p.window > 0 || p.gelu || p.kv_q8) return false;
         std::vector<fish_hip_span_layer> ls(static_cast<size_t>(n));
         for (int i = 0; i < n; ++i) {
             const SpanLayer& L = p.layers[i];
             if (L.wqkv || !L.wq || !L.wk || !L.wv || !L.wo || !L.wg || !L.wu || !L.wd || !L.attn_norm ||
-                !L.ffn_norm || L.post_attn_norm || L.post_ffn_norm || L.q_norm || L.k_norm || L.bias_q || L.bias_k ||
-                L.bias_v || L.bias_o || L.bias_qkv || L.sliding_window)
+                !L.ffn_norm || L.post_attn_norm || L.post_ffn_norm || L.bias_qkv || L.sliding_window)
                 return false;
-            ls[size_t(i)] = {L.wq, L.wk, L.wv, L.wo, L.wg, L.wu, L.wd, L.attn_norm, L.ffn_norm};
+            ls[size_t(i)] = {L.wq,     L.wk,     L.wv,     L.wo,     L.wg,     L.wu,     L.wd,     L.attn_norm,
+                             L.ffn_norm, L.q_norm, L.k_norm, L.bias_q, L.bias_k, L.bias_v, L.bias_o};
         }
         fish_hip_span_params hp{};
         hp.n_layers = n;
@@ -81,6 +82,7 @@ public:
         hp.rot_dim = p.rot_dim;
         hp.rope_neox = p.rope_neox ? 1 : 0;
         hp.layers = ls.data();
+        hp.kv_q8 = p.kv_q8 ? 1 : 0;
         return fish_hip_span_prepare(&hp) != 0;
     }
     bool span_forward(float* x, int n_tok, int pos0) override { return fish_hip_span_forward(x, n_tok, pos0) != 0; }

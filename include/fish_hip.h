@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define FISH_HIP_ABI_VERSION 1
+#define FISH_HIP_ABI_VERSION 2
 
 #define FISH_HIP_ERR_ARG (-1)     /* bad argument or unsupported type/shape */
 #define FISH_HIP_ERR_DEVICE (-2)  /* HIP runtime error; the backend is disabled */
@@ -229,12 +229,30 @@ FISH_HIP_API int fish_hip_backend_matmul(const void* key, const float* x, int n_
 /* ComputeBackend::matmul_group (backend.h:78-87): several tensors, one input. */
 FISH_HIP_API int fish_hip_backend_matmul_group(const void* const* keys, int n, const float* x, int n_tok, int n_in,
                                                const int* n_outs, float* const* ys);
+/* The expert FFN of LlamaModel::moe_ffn (model.cpp:1523-1580) on host buffers:
+ * the hook FISH lacks, since mm(expert >= 0) calls matmul_batch directly
+ * (model.cpp:1466-1470). key_gate / key_up / key_down are the 3-D expert
+ * tensors uploaded with n_expert = ne[2] (gate, up [n_expert][n_ff][n_embd],
+ * down [n_expert][n_embd][n_ff]). Router logits come from `logits` (host,
+ * f32 [n_tok][n_expert], as matmul_batch(gate_inp) leaves them, model.cpp:1529)
+ * or, when key_router is given (a resident F32 / F16 [n_expert][n_embd]
+ * tensor), are computed on the device from x and `logits` may be NULL.
+ * x f32 [n_tok][n_embd], out f32 [n_tok][n_embd] (host). Softmax, top-k,
+ * renormalisation when norm, per-expert gate / up / silu * up / down and the
+ * weighted sum in ascending expert order, as fish_hip_moe_ffn. 1 ok, 0 refused
+ * or failed (out untouched; the caller runs its CPU loop). */
+FISH_HIP_API int fish_hip_backend_moe_ffn(const void* key_gate, const void* key_up, const void* key_down,
+                                          const void* key_router, const float* x, const float* logits, int n_tok,
+                                          int n_embd, int n_ff, int n_expert, int k, int norm, float* out);
 
 /* ---------------------------------------------------------------- layer spans (host pointers, synchronous) */
 
-/* One dense llama-style layer of a span (backend.h:114-134 SpanLayer, the
- * subset this backend runs): the weight keys given to fish_hip_upload (all
- * resident) and the two RMS-norm weight vectors [n_embd] (host, copied). */
+/* One dense layer of a span (backend.h:114-134 SpanLayer, the subset this
+ * backend runs): the weight keys given to fish_hip_upload (all resident), the
+ * two RMS-norm weight vectors [n_embd], and optionally the Qwen-3 per-head
+ * q / k RMS-norm weights [head_dim] and the q / k / v / o projection biases
+ * ([q_dim], [kv_dim], [kv_dim], [n_embd]); NULL = absent. Vectors are host
+ * memory, copied at fish_hip_span_prepare. */
 typedef struct fish_hip_span_layer {
     const void* wq;
     const void* wk;
@@ -245,6 +263,12 @@ typedef struct fish_hip_span_layer {
     const void* wd;
     const float* attn_norm;
     const float* ffn_norm;
+    const float* q_norm;
+    const float* k_norm;
+    const float* bias_q;
+    const float* bias_k;
+    const float* bias_v;
+    const float* bias_o;
 } fish_hip_span_layer;
 
 /* backend.h:136-154 SpanParams, same meaning: head_dim <= 256, n_head a
@@ -260,19 +284,44 @@ typedef struct fish_hip_span_params {
     int rot_dim;
     int rope_neox;
     const fish_hip_span_layer* layers;
+    /* SpanParams::kv_q8 (backend.h:150-153): an int8 KV cache requested by
+     * FISH's planner; this backend keeps f16 K and V only, so nonzero is refused */
+    int kv_q8;
 } fish_hip_span_params;
 
 /* ComputeBackend::span_prepare (backend.h:156): keeps the layers' weights,
- * copies the norms and RoPE tables and allocates an f32 KV cache of n_ctx
- * positions per layer. Replaces an earlier span. 1 ok, 0 refused (no span). */
+ * copies the norms, biases and RoPE tables, and allocates an f16 KV cache of
+ * n_ctx positions per layer (4 bytes per position and K+V element, FISH's
+ * planner budget, model.cpp:1318-1320) together with every buffer later
+ * calls use, each allocation leaving FISH's VRAM headroom free
+ * (vram_headroom_bytes, backend.h:171-187). Replaces an earlier span.
+ * 1 ok, 0 refused (no span). */
 FISH_HIP_API int fish_hip_span_prepare(const fish_hip_span_params* p);
 /* ComputeBackend::span_forward (backend.h:157): x [n_tok][n_embd] (host) is the
  * residual stream entering the span's first layer; on return it leaves the
  * last one, and positions pos0 .. pos0 + n_tok - 1 are in the KV cache.
- * 1 ok; 0 failed with x unmodified. */
+ * Batches of more than 256 tokens (FISH's largest, model.h:292) run in
+ * consecutive chunks. 1 ok; 0 failed with x unmodified. */
 FISH_HIP_API int fish_hip_span_forward(float* x, int n_tok, int pos0);
-/* ComputeBackend::span_kv_truncate / span_release (backend.h:158-159) */
+/* ComputeBackend::span_kv_truncate / span_release (backend.h:158-159). Positions
+ * >= n_past need no clearing: every forward writes the cache rows of its own
+ * positions before its attention reads them, and attends only over positions
+ * up to its own, so a rewind followed by new tokens never reads a stale row. */
 FISH_HIP_API void fish_hip_span_kv_truncate(int n_past);
+/* The intermediate values of the last fish_hip_span_forward call (its last
+ * chunk of up to 256 tokens; for a multi-layer span, those of the last layer),
+ * copied to host `out` (n_floats floats), for stage-by-stage verification; no
+ * counterpart in FISH, whose forward keeps them in local buffers
+ * (model.cpp:1654-1801). part: 0 x (the residual stream after the call),
+ * 1 attention RMS-norm output [n_tok][n_embd], 2 q, 3 k, 4 v (projection
+ * outputs, before bias) [n_tok][q_dim | kv_dim], 5 q after bias, q-norm and
+ * RoPE, 6 attention output [n_tok][q_dim], 7 o projection [n_tok][n_embd],
+ * 8 FFN RMS-norm output, 9 silu(gate) * up [n_tok][n_ff], 10 up, 11 down
+ * projection [n_tok][n_embd]; 100 / 101 rows pos0 .. pos0 + n - 1 of layer
+ * `layer`'s K / V cache (f16, returned as f32) [n][kv_dim]. 1 ok, 0 refused. */
+FISH_HIP_API int fish_hip_span_inspect(int part, int layer, int pos0, int n, float* out, uint64_t n_floats);
+/* Tokens in the last chunk fish_hip_span_inspect returns (0 without a span call). */
+FISH_HIP_API int fish_hip_span_last_tokens(void);
 FISH_HIP_API void fish_hip_span_release(void);
 
 #ifdef __cplusplus

@@ -303,6 +303,9 @@ class DropIn:
         L.drop_backend_name.restype = ctypes.c_char_p
         L.drop_tensor_new.restype = _P
         L.drop_tensor_new.argtypes = [ctypes.c_uint32, _P, ctypes.c_int, ctypes.c_int]
+        L.drop_tensor3_new.restype = _P
+        L.drop_tensor3_new.argtypes = [ctypes.c_uint32, _P, ctypes.c_int, ctypes.c_int, ctypes.c_int]
+        L.drop_moe_ffn.argtypes = [_P, _P, _P, _P, _P] + [ctypes.c_int] * 6 + [_P]
         for f in ("drop_tensor_free", "drop_upload", "drop_resident", "drop_release"):
             getattr(L, f).argtypes = [_P]
         L.drop_bytes_resident.restype = ctypes.c_uint64
@@ -320,6 +323,22 @@ class DropIn:
         h = self.L.drop_tensor_new(t, _ptr(packed), n_in, n_out)
         self._keep[h] = (packed, n_in, n_out)
         return h
+
+    def tensor3(self, t: int, packed: np.ndarray, n_in: int, n_out: int, n_expert: int):
+        """A 3-D expert TensorInfo [n_expert][n_out][n_in] over the packed bytes."""
+        packed = np.ascontiguousarray(packed)
+        h = self.L.drop_tensor3_new(t, _ptr(packed), n_in, n_out, n_expert)
+        self._keep[h] = (packed, n_in, n_out)
+        return h
+
+    def moe_ffn(self, hs, x, logits, n_ff: int, n_expert: int, k: int, norm: bool = True):
+        """The expert hook called with FISH's TensorInfo keys (out, or None when refused)."""
+        x = np.ascontiguousarray(x, np.float32)
+        logits = np.ascontiguousarray(logits, np.float32)
+        out = np.zeros_like(x)
+        ok = self.L.drop_moe_ffn(hs[0], hs[1], hs[2], _ptr(x), _ptr(logits), x.shape[0], x.shape[1], n_ff, n_expert,
+                                 k, int(norm), _ptr(out))
+        return out if ok else None
 
     def free(self, h) -> None:
         self.L.drop_tensor_free(h)

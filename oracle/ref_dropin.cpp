@@ -11,6 +11,8 @@
 #include <fish/gguf.h>
 #include <fish/ops.h>
 
+#include "fish_hip.h"
+
 #include <cstring>
 #include <vector>
 
@@ -32,6 +34,19 @@ void* drop_tensor_new(uint32_t type, const void* data, int n_in, int n_out) {
     return t;
 }
 void drop_tensor_free(void* t) { delete static_cast<TensorInfo*>(t); }
+
+// A 3-D expert tensor [n_expert][n_out][n_in] (ne = {n_in, n_out, n_expert},
+// FISH's ffn_*_exps layout, model.cpp:66-69) over caller-owned GGUF bytes.
+void* drop_tensor3_new(uint32_t type, const void* data, int n_in, int n_out, int n_expert) {
+    auto* t = new TensorInfo();
+    t->name = "experts";
+    t->type = static_cast<GgmlType>(type);
+    t->ne = {static_cast<uint64_t>(n_in), static_cast<uint64_t>(n_out), static_cast<uint64_t>(n_expert)};
+    t->data = static_cast<const uint8_t*>(data);
+    t->nbytes = ggml_row_size(t->type, static_cast<uint64_t>(n_in)) * static_cast<uint64_t>(n_out) *
+                static_cast<uint64_t>(n_expert);
+    return t;
+}
 
 // What FISH's placement does at load: supports() then upload().
 int drop_upload(void* t) {
@@ -63,6 +78,17 @@ void drop_matmul_tensors(void* const* ts, int n, const float* x, int n_tok, int 
     std::vector<const TensorInfo*> v(static_cast<size_t>(n));
     for (int i = 0; i < n; ++i) v[static_cast<size_t>(i)] = static_cast<const TensorInfo*>(ts[i]);
     matmul_tensors(v.data(), n, x, &acts, n_tok, n_in, n_outs, ys);
+}
+
+// The routed experts of LlamaModel::moe_ffn as the patched model.cpp runs them
+// (the expert hook of INTEGRATION.md, placed right after the router matmul,
+// model.cpp:1529): FISH's three 3-D expert TensorInfos, already uploaded
+// through FISH's backend, are the keys; x is xb_ and logits the router_ rows
+// the matmul left; out receives ffn_out_. 1 when the device ran it, 0 when the
+// CPU loop of model.cpp:1549-1580 would run instead.
+int drop_moe_ffn(void* gate, void* up, void* down, const float* x, const float* logits, int n_tok, int n_embd,
+                 int n_ff, int n_expert, int k, int norm, float* out) {
+    return fish_hip_backend_moe_ffn(gate, up, down, nullptr, x, logits, n_tok, n_embd, n_ff, n_expert, k, norm, out);
 }
 
 // FISH's CPU path for the same call (the backend hook bypassed).

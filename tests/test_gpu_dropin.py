@@ -119,3 +119,63 @@ def test_unsupported_type_stays_on_the_cpu(drop):
         assert served() == n0
     finally:
         drop.free(h)
+
+
+@pytest.mark.parametrize("n_tok,types", [(9, (fh.Q4_K, fh.Q4_K, fh.Q6_K)), (40, (fh.Q4_K, fh.Q5_K, fh.Q6_K)),
+                                         (1, (fh.Q4_K, fh.Q4_K, fh.Q4_K)), (5, (fh.Q8_0, fh.Q4_0, fh.Q6_K))])
+def test_moe_ffn_through_fish_expert_tensors(drop, oracle, n_tok, types):
+    """FISH's three 3-D expert TensorInfos uploaded through FISH's backend (upload() with
+    ne[2] experts), then the expert hook as the patched model.cpp calls it after the router
+    matmul: bit-identical to the device-pointer expert FFN, and against FISH's own CPU
+    moe_ffn composition (compiled from the reference, AVX2 matmul_batch) within 1e-4 of
+    max|out| plus the movement FISH's own hidden values explain (their int8 requantization
+    is discontinuous: FISH's scalar and AVX2 paths differ by 1e-3 on the 9-token case)."""
+    import torch
+    from oracle.oracle import Ref
+    from test_gpu_moe import hidden_bound
+    tg, tu, td = types
+    E, F, NE, K = 256, 512, 8, 2
+    d = torch.device("cuda:0")
+    pg = np.concatenate([fh.quantize_rows(tg, normal(9000 + e, (F, E), 0.02)) for e in range(NE)])
+    pu = np.concatenate([fh.quantize_rows(tu, normal(9100 + e, (F, E), 0.02)) for e in range(NE)])
+    pd = np.concatenate([fh.quantize_rows(td, normal(9200 + e, (E, F), 0.02)) for e in range(NE)])
+    hs = [drop.tensor3(tg, pg, E, F, NE), drop.tensor3(tu, pu, E, F, NE), drop.tensor3(td, pd, F, E, NE)]
+    try:
+        for h in hs:
+            assert drop.upload(h) and drop.resident(h)
+        x = normal(9300 + n_tok, (n_tok, E))
+        logits = normal(9400 + n_tok, (n_tok, NE))
+        before = served()
+        got = drop.moe_ffn(hs, x, logits, F, NE, K)
+        assert got is not None and served() == before + 1
+        # the device-pointer path on the same bytes, with its intermediate buffers
+        tx, tl = torch.from_numpy(x).to(d), torch.from_numpy(logits).to(d)
+        wg, wu, wd = (fh.repack(t, torch.from_numpy(p).to(d), n_in, NE * n_out)
+                      for t, p, n_in, n_out in ((tg, pg, E, F), (tu, pu, E, F), (td, pd, F, E)))
+        ws = torch.empty(fh.moe_workspace_bytes(n_tok, E, F, NE, K), dtype=torch.uint8, device=d)
+        dev_out = fh.moe_ffn(tx, tl, F, NE, K, True, tg, wg, tu, wu, td, wd, workspace=ws).cpu().numpy()
+        assert np.array_equal(got, dev_out)
+        # FISH's own CPU composition, and the bound from FISH's AVX2 gate / up products
+        ref = Ref()
+        want, _, _ = ref.moe_ffn(x, logits, E, F, NE, K, True, tg, pg, tu, pu, td, pd)
+        p = {n: v.cpu().numpy() for n, v in fh.moe_parts(ws, n_tok, E, F, NE, K).items()}
+        exp_of = np.empty(n_tok * K, np.int64)
+        exp_of[p["tok_slot"].reshape(-1)] = p["sel"].reshape(-1)
+        bg, bu = fh.gguf_row_bytes(tg, E) * F, fh.gguf_row_bytes(tu, E) * F
+        g_f, u_f = np.zeros_like(p["gate"]), np.zeros_like(p["up"])
+        for e in np.unique(exp_of):
+            sl = np.nonzero(exp_of == e)[0]
+            g_f[sl] = ref.matmul_f32(tg, pg[e * bg:(e + 1) * bg], x[p["slot_tok"][sl]], F)
+            u_f[sl] = ref.matmul_f32(tu, pu[e * bu:(e + 1) * bu], x[p["slot_tok"][sl]], F)
+        _, _, h_gpu = fh.silu_mul_quantize(torch.from_numpy(p["gate"]).to(d), torch.from_numpy(p["up"]).to(d))
+        bound, (codes, scales, blocks, _) = hidden_bound(oracle, g_f, u_f, h_gpu.cpu().numpy(), td, pd, exp_of,
+                                                         p["wsel"], p["tok_slot"], E, F, K)
+        err = np.abs(got.astype(np.float64) - want)
+        allowed = TOL * float(np.max(np.abs(want))) + np.broadcast_to(bound[:, None], err.shape)
+        print(f"drop-in moe M={n_tok}: {codes} codes / {scales} of {blocks} scales differ from FISH's AVX2 "
+              f"requantization; max err {float(err.max()):.3e}, max allowed {float(allowed.max()):.3e}")
+        assert np.all(err <= allowed)
+    finally:
+        for h in hs:
+            drop.release(h)
+            drop.free(h)

@@ -185,9 +185,19 @@ def check_stages(torch_dev, oracle, x, logits, parts, out, n_ff, k, types, packe
     assert np.array_equal(out, want)
     # what the hidden requantization may move: FISH's own hidden values (oracle gate/up on
     # the same x, FISH's silu * up) against the GPU's, code by code
+    return hidden_bound(oracle, g_ref, u_ref, h, td, pd, exp_of, p["wsel"], tok_slot, n_embd, n_ff, k)
+
+
+def hidden_bound(oracle, g_fish, u_fish, h_gpu, td, pd, exp_of, wsel, tok_slot, n_embd, n_ff, k):
+    """Per-token bound on how far the layer output may move because the hidden values that reach
+    the down projection differ: FISH's own (silu(g_fish) * u_fish, requantized) against the GPU's
+    (h_gpu, requantized), both [slot][n_ff]. Returns (bound [n_tok], (flipped codes, differing block
+    scales, blocks, differing dequantized values))."""
+    n_tok = tok_slot.shape[0]
     k_layout = fh.BLOCK_ELEMS[td] == 256
-    h_fish = oracle.silu_mul(g_ref, u_ref)
-    a_gpu = oracle.act_batch(h)[1 if k_layout else 0]
+    bd = fh.gguf_row_bytes(td, n_ff) * n_embd
+    h_fish = oracle.silu_mul(g_fish, u_fish)
+    a_gpu = oracle.act_batch(h_gpu)[1 if k_layout else 0]
     a_fish = oracle.act_batch(h_fish)[1 if k_layout else 0]
     delta = np.abs(act_values(a_gpu, k_layout) - act_values(a_fish, k_layout)).reshape(n_tok * k, n_ff)
     size, qoff = (276, 20) if k_layout else (40, 8)
@@ -195,7 +205,7 @@ def check_stages(torch_dev, oracle, x, logits, parts, out, n_ff, k, types, packe
     n_codes = int(np.count_nonzero(b_gpu[:, qoff:] != b_fish[:, qoff:]))
     n_scales = int(np.count_nonzero(np.any(b_gpu[:, :4] != b_fish[:, :4], axis=1)))
     slot_bound = np.zeros(n_tok * k)
-    for e in experts:
+    for e in np.unique(exp_of):
         sl = np.nonzero(exp_of == e)[0]
         sl = sl[np.any(delta[sl] > 0, axis=1)]
         if sl.size == 0:
@@ -203,7 +213,7 @@ def check_stages(torch_dev, oracle, x, logits, parts, out, n_ff, k, types, packe
         w_e = oracle.dequant_row(td, pd[e * bd:(e + 1) * bd], n_embd * n_ff).reshape(n_embd, n_ff)
         colmax = np.max(np.abs(w_e.astype(np.float64)), axis=0)
         slot_bound[sl] = delta[sl] @ colmax
-    tok_bound = np.array([sum(abs(float(p["wsel"][t, i])) * slot_bound[tok_slot[t, i]] for i in range(k))
+    tok_bound = np.array([sum(abs(float(wsel[t, i])) * slot_bound[tok_slot[t, i]] for i in range(k))
                           for t in range(n_tok)])
     return tok_bound, (n_codes, n_scales, b_gpu.shape[0], int(np.count_nonzero(delta)))
 
@@ -324,3 +334,47 @@ def test_moe_qwen3_full_size_prefill(torch_dev, oracle):
     """Qwen3-30B-A3B expert shapes at M=256 (128 experts, top-8, skewed per-expert counts from
     N(0, 1) logits): grouped batch-kernel items over all 128 experts."""
     run_case(torch_dev, oracle, 256, 2048, 768, 128, 8, (fh.Q4_K, fh.Q4_K, fh.Q6_K), 5200, distinct=16)
+
+
+@pytest.mark.parametrize("n_tok", [1, 20, 64])
+def test_backend_moe_ffn_on_host_buffers(torch_dev, oracle, n_tok):
+    """fish_hip_backend_moe_ffn: the expert tensors uploaded through the backend as 3-D tensors
+    (n_expert = ne[2]), x / logits / out in host memory. Bit-identical to fish_hip_moe_ffn on
+    device pointers; with a resident f32 router tensor the logits are computed on the device
+    (= router_logits then moe_ffn); refusals leave out untouched."""
+    torch, d = torch_dev
+    be = fh.HipBackend()
+    E, F, NE, K = 512, 1024, 8, 2
+    types = (fh.Q4_K, fh.Q4_K, fh.Q6_K)
+    tg, tu, td = types
+    pg, wg = repacked_experts(torch_dev, oracle, tg, NE, F, E, 8100)
+    pu, wu = repacked_experts(torch_dev, oracle, tu, NE, F, E, 8200)
+    pd, wd = repacked_experts(torch_dev, oracle, td, NE, E, F, 8300)
+    names = [f"bmoe{n_tok}.{n}" for n in ("gate", "up", "down")]
+    assert be.upload(names[0], tg, pg, E, F, NE) and be.upload(names[1], tu, pu, E, F, NE)
+    assert be.upload(names[2], td, pd, F, E, NE)
+    wr = normal(8400, (NE, E), 0.05)
+    assert be.upload(f"bmoe{n_tok}.router", fh.F32, wr.view(np.uint8), E, NE)
+    try:
+        x = normal(8500 + n_tok, (n_tok, E))
+        logits = normal(8600 + n_tok, (n_tok, NE))
+        served = int(fh.load().fish_hip_backend_served())
+        got = be.moe_ffn(names, x, logits, F, NE, K)
+        assert got is not None, fh.last_error()
+        assert int(fh.load().fish_hip_backend_served()) == served + 1
+        want = fh.moe_ffn(dev(torch_dev, x), dev(torch_dev, logits), F, NE, K, True, tg, wg, tu, wu, td, wd)
+        assert np.array_equal(got, want.cpu().numpy())
+        # router logits on the device from the resident router tensor
+        got_r = be.moe_ffn(names, x, None, F, NE, K, router=f"bmoe{n_tok}.router")
+        lg = fh.router_logits(dev(torch_dev, x), dev(torch_dev, wr))
+        want_r = fh.moe_ffn(dev(torch_dev, x), lg, F, NE, K, True, tg, wg, tu, wu, td, wd)
+        assert np.array_equal(got_r, want_r.cpu().numpy())
+        # refusals: expert count or widths that do not match the resident tensors
+        assert be.moe_ffn(names, x, logits[:, :4], F, 4, K) is None
+        assert be.moe_ffn(names, x, logits, F // 2, NE, K) is None
+        assert be.moe_ffn([names[0], names[1], "bmoe.absent"], x, logits, F, NE, K) is None
+        # a 2-D tensor is not an expert tensor: the router as gate is refused
+        assert be.moe_ffn([f"bmoe{n_tok}.router", names[1], names[2]], x, logits, F, NE, K) is None
+    finally:
+        for n in names + [f"bmoe{n_tok}.router"]:
+            be.release(n)

@@ -304,3 +304,32 @@ def test_backend_upload_matmul_group(torch_dev, oracle):
     assert be.matmul("q", normal(1, (1, n_in)), 255) is None
     be.release("q")
     assert not be.resident("q")
+
+
+def test_backend_upload_keeps_the_vram_headroom(torch_dev, oracle, monkeypatch):
+    """upload() leaves FISH's VRAM headroom free (vram_headroom_bytes, backend.h:171-187): with
+    FISH_VRAM_HEADROOM_MB above the free memory the upload is refused (earlier uploads intact),
+    also when FISH_VRAM_HEADROOM_PCT says 0 (the MB setting wins); with the percentage alone at 0,
+    or the default rule, it succeeds."""
+    be = fh.HipBackend()
+    n_in, n_out = 1024, 256
+    packed = packed_weights(oracle, fh.Q4_K, n_out, n_in, 1900)
+    try:
+        assert be.upload("headroom.a", fh.Q4_K, packed, n_in, n_out)
+        before = be.bytes_resident()
+        free_mb = be.memory_free() >> 20
+        monkeypatch.setenv("FISH_VRAM_HEADROOM_MB", str(free_mb + 1024))
+        assert not be.upload("headroom.b", fh.Q4_K, packed, n_in, n_out)
+        assert be.bytes_resident() == before and be.resident("headroom.a") and not be.resident("headroom.b")
+        monkeypatch.setenv("FISH_VRAM_HEADROOM_PCT", "0")
+        assert not be.upload("headroom.b", fh.Q4_K, packed, n_in, n_out)
+        monkeypatch.delenv("FISH_VRAM_HEADROOM_MB")
+        assert be.upload("headroom.b", fh.Q4_K, packed, n_in, n_out)
+        be.release("headroom.b")
+        monkeypatch.delenv("FISH_VRAM_HEADROOM_PCT")
+        assert be.upload("headroom.b", fh.Q4_K, packed, n_in, n_out)
+        x = normal(1901, (3, n_in))
+        assert np.array_equal(be.matmul("headroom.a", x, n_out), be.matmul("headroom.b", x, n_out))
+    finally:
+        be.release("headroom.a")
+        be.release("headroom.b")
