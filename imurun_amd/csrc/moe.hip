@@ -29,66 +29,107 @@ constexpr int kMoe1MaxGroups = 1024;  // k * n_ff <= 32768 hidden values in LDS
 // One token's routing by one wavefront (model.cpp:1528-1547): softmax over
 // the experts in FISH's order (max, then exp(x - max) summed left to right,
 // then times 1/sum), the k most probable by k wavefront argmax rounds (ties:
-// lower expert), renormalised by their sum when norm. Every lane ends with
-// chosen[j] / prob[j], j < k, in descending probability. s_p: LDS scratch
-// of kMaxExperts floats owned by this wavefront.
-__device__ void route_token(const float* __restrict__ lg, int n_expert, int k, int norm, float* s_p, int lane,
-                            int (&chosen)[kMaxK], float (&prob)[kMaxK]) {
-    float m = -INFINITY;
-    for (int e = lane; e < n_expert; e += 64) m = fmaxf(m, lg[e]);
-    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-    for (int e = lane; e < n_expert; e += 64) s_p[e] = expf(__fsub_rn(lg[e], m));
+// lower expert), renormalised by their sum when norm. The results land in
+// LDS: e_out[j] / w_out[j], j < k, in descending probability, readable by
+// every lane of the wavefront on return. s_p: LDS scratch of kMaxExperts
+// floats owned by this wavefront, 16-byte aligned.
+//
+// The logits come in registers (load_logits: lane l holds experts l + 64 q),
+// fetched in one batch at kernel entry. Fetching them inside the routing, one
+// load and wait per loop, put several dependent round trips -- each queued
+// behind the other workgroups' weight traffic -- in front of every
+// workgroup's weight loads (measured: 9 us of the 15.7 us Qwen3 gate+up).
+constexpr int kLgPerLane = kMaxExperts / 64;
+
+__device__ __forceinline__ void load_logits(const float* __restrict__ lg, int n_expert, int lane,
+                                            float (&v)[kLgPerLane]) {
+    // unconditional loads from clamped addresses: no branch, so no wait for other loads at a join
+#pragma unroll
+    for (int q = 0; q < kLgPerLane; ++q) v[q] = lg[min(lane + 64 * q, n_expert - 1)];
+}
+
+__device__ void route_token(const float (&v)[kLgPerLane], int n_expert, int k, int norm, float* s_p, int* e_out,
+                            float* w_out, int lane) {
+    // every cross-lane step is a DPP swizzle, a readlane or a ballot: no LDS round trips
+    // besides the ordered sum's reads
+    float lm = -INFINITY;
+#pragma unroll
+    for (int q = 0; q < kLgPerLane; ++q)
+        if (lane + 64 * q < n_expert) lm = fmaxf(lm, v[q]);
+    const float m = wave_max64(lm);
+    float ex[kLgPerLane];
+#pragma unroll
+    for (int q = 0; q < kLgPerLane; ++q) {
+        ex[q] = lane + 64 * q < n_expert ? expf(__fsub_rn(v[q], m)) : 0.0f;
+        s_p[lane + 64 * q] = ex[q];  // zeros past n_expert
+    }
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    // FISH's left-to-right sum, by lane 0, eight 16-byte reads in flight at a time. The
+    // zeros past n_expert (up to the next multiple of 32) leave it unchanged: the sum
+    // starts at +0 and every term is >= +0.
     float sum = 0.0f;
-    if (lane == 0)
-        for (int e = 0; e < n_expert; ++e) sum = __fadd_rn(sum, s_p[e]);
-    sum = __shfl(sum, 0);
-    const bool uniform = !(sum > 0.0f);
-    const float inv = uniform ? 0.0f : 1.0f / sum;
-    float p[kMaxExperts / 64];
-    for (int q = 0; q < kMaxExperts / 64; ++q) {
-        const int e = lane + 64 * q;
-        p[q] = (e < n_expert) ? (uniform ? 1.0f / float(n_expert) : __fmul_rn(s_p[e], inv)) : -1.0f;
+    if (lane == 0) {
+        const float4* s4 = reinterpret_cast<const float4*>(s_p);
+        for (int e0 = 0; e0 < n_expert; e0 += 32) {
+            float4 r[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) r[i] = s4[(e0 >> 2) + i];
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                sum = __fadd_rn(__fadd_rn(__fadd_rn(__fadd_rn(sum, r[i].x), r[i].y), r[i].z), r[i].w);
+        }
     }
+    sum = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sum), 0));
+    const bool uniform = !(sum > 0.0f);
+    const float inv = uniform ? 0.0f : 1.0f / sum, pu = 1.0f / float(n_expert);
+    float p[kLgPerLane];
+#pragma unroll
+    for (int q = 0; q < kLgPerLane; ++q)
+        p[q] = (lane + 64 * q < n_expert) ? (uniform ? pu : __fmul_rn(ex[q], inv)) : -1.0f;
+    // k rounds: the largest remaining probability, then the lowest expert holding it
     float wsum = 0.0f;
     for (int j = 0; j < k; ++j) {
-        float bp = -1.0f;
-        int be = 0x7fffffff;
-        for (int q = 0; q < kMaxExperts / 64; ++q) {
-            const int e = lane + 64 * q;
-            if (p[q] > bp) { bp = p[q]; be = e; }
+        const float mb = wave_max64(fmaxf(fmaxf(p[0], p[1]), fmaxf(p[2], p[3])));
+        int be = -1;
+#pragma unroll
+        for (int q = 0; q < kLgPerLane; ++q) {
+            const unsigned long long b = __ballot(p[q] == mb);
+            if (be < 0 && b) be = 64 * q + __builtin_ctzll(b);
         }
-        for (int off = 32; off > 0; off >>= 1) {
-            const float op = __shfl_xor(bp, off);
-            const int oe = __shfl_xor(be, off);
-            if (op > bp || (op == bp && oe < be)) { bp = op; be = oe; }
+        if (lane == 0) {
+            e_out[j] = be;
+            w_out[j] = mb;
         }
-        chosen[j] = be;
-        prob[j] = bp;
-        wsum = __fadd_rn(wsum, bp);
-        for (int q = 0; q < kMaxExperts / 64; ++q)
+        wsum = __fadd_rn(wsum, mb);
+#pragma unroll
+        for (int q = 0; q < kLgPerLane; ++q)
             if (lane + 64 * q == be) p[q] = -2.0f;  // taken
     }
-    if (norm && wsum > 0.0f)
-        for (int j = 0; j < k; ++j) prob[j] = prob[j] / wsum;
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    // renormalised by the sum of the k (model.cpp:1545-1546), one choice per lane
+    if (norm && wsum > 0.0f && lane < k) w_out[lane] = w_out[lane] / wsum;
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
 }
 
 // One wavefront per token.
 __global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ logits, int n_tok, int n_expert, int k,
                                                    int norm, MoeRouting r) {
-    __shared__ float s_p[4][kMaxExperts];
+    __shared__ __align__(16) float s_p[4][kMaxExperts];
+    __shared__ int s_e[4][kMaxK];
+    __shared__ float s_w[4][kMaxK];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int t = int(blockIdx.x) * 4 + w;
     if (t >= n_tok) return;
-    int chosen[kMaxK];
-    float prob[kMaxK];
-    route_token(logits + size_t(t) * n_expert, n_expert, k, norm, s_p[w], lane, chosen, prob);
-    if (lane == 0)
-        for (int j = 0; j < k; ++j) {
-            r.sel[t * k + j] = chosen[j];
-            r.wsel[t * k + j] = prob[j];
-        }
+    float lv[kLgPerLane];
+    load_logits(logits + size_t(t) * n_expert, n_expert, lane, lv);
+    route_token(lv, n_expert, k, norm, s_p[w], s_e[w], s_w[w], lane);
+    if (lane < k) {
+        r.sel[t * k + lane] = s_e[w][lane];
+        r.wsel[t * k + lane] = s_w[w][lane];
+    }
 }
 
 // Exclusive prefix sum of v over the 256 threads of the workgroup (LDS
@@ -212,9 +253,9 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
 // The expert FFN of a single token in two launches (decode). The slot order
 // is the workspace's: the k chosen experts ascending (model.cpp:1551-1561).
 //
-// Launch 1, gate and up: every workgroup routes the token itself (wavefront
-// 0, route_token), quantizes x into LDS while its weight loads are in
-// flight, and for rows i of its slot's expert e computes gate_e[i], up_e[i]
+// Launch 1, gate and up: every workgroup quantizes x into LDS while the
+// router logits are in flight, routes the token itself (wavefront 0,
+// route_token), then for rows i of its slot's expert e computes gate_e[i], up_e[i]
 // (the same lanes, so h = silu(gate) * up is formed in place) and writes
 // gate, up and h. Workgroup 0 also writes the routing (sel, wsel, tok_slot,
 // slot_tok).
@@ -228,10 +269,15 @@ __global__ __launch_bounds__(64 * kMoe1UpWaves) void moe1_gate_up_kernel(
     __shared__ uint4 s_codes[2 * kGemvXMaxGroups];
     __shared__ float s_d[kGemvXMaxGroups];
     __shared__ int s_s[kGemvXMaxGroups];
-    __shared__ float s_p[kMaxExperts];
+    __shared__ __align__(16) float s_p[kMaxExperts];
     __shared__ int s_exp[kMaxK];
+    __shared__ int s_sel[kMaxK];
+    __shared__ float s_wsel[kMaxK];
 
     const int tid = threadIdx.x, lane = tid & 63, sub = lane % LPR;
+    // the router logits first: the routing (wavefront 0) gates every weight load
+    float lv[kLgPerLane];
+    load_logits(logits, n_expert, lane, lv);
     float4 xv[XV];
 #pragma unroll
     for (int i = 0; i < XV; ++i) {
@@ -241,19 +287,17 @@ __global__ __launch_bounds__(64 * kMoe1UpWaves) void moe1_gate_up_kernel(
         // make the compiler wait for every outstanding load at the join
         xv[i] = *reinterpret_cast<const float4*>(x + min(k0, n_embd - 4));
     }
+    // x into LDS while the logits are in flight: the routing, not the quantization,
+    // then stands between the kernel's start and its weight loads
+    const LdsAct L{s_codes, s_d, s_s, kGemvXMaxGroups};
+    quantize_to_lds<kq, XV, TH>(xv, n_embd, tid, L);
     if (tid < 64) {
-        int chosen[kMaxK];
-        float prob[kMaxK];
-        route_token(logits, n_expert, k, norm, s_p, lane, chosen, prob);
+        route_token(lv, n_expert, k, norm, s_p, s_sel, s_wsel, lane);
         if (lane < k) {
-            int me = 0, rank = 0;
-            float mw = 0.0f;
-            for (int j = 0; j < k; ++j)
-                if (j == lane) {
-                    me = chosen[j];
-                    mw = prob[j];
-                }
-            for (int j = 0; j < k; ++j) rank += chosen[j] < me;
+            const int me = s_sel[lane];
+            const float mw = s_wsel[lane];
+            int rank = 0;
+            for (int j = 0; j < k; ++j) rank += s_sel[j] < me;
             s_exp[rank] = me;
             if (blockIdx.x == 0) {
                 r.sel[lane] = me;
@@ -287,9 +331,7 @@ __global__ __launch_bounds__(64 * kMoe1UpWaves) void moe1_gate_up_kernel(
             fu[rb][q] = load_group_raw<T, true>(Wu, row, cg[q], n_embd, lane);
         }
     }
-    // every load is issued before the first wait; the weight scales are
-    // decoded before the quantization of x (measured: 3-7 us faster for the
-    // Mixtral / Qwen3 expert shapes than decoding after it)
+    // every load is issued before the first wait
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb)
@@ -298,9 +340,6 @@ __global__ __launch_bounds__(64 * kMoe1UpWaves) void moe1_gate_up_kernel(
             finish_group<T, true>(fg[rb][q], cg[q], lane);
             finish_group<T, true>(fu[rb][q], cg[q], lane);
         }
-    const LdsAct L{s_codes, s_d, s_s, kGemvXMaxGroups};
-    quantize_to_lds<kq, XV, TH>(xv, n_embd, tid, L);
-    __syncthreads();
     if (wave_id * (RPP * RB) >= n_ff) return;  // uniform over the wavefront
     float ag[RB], au[RB];
 #pragma unroll

@@ -10,23 +10,59 @@
 
 namespace fishhip {
 
+// Cross-lane reductions on DPP lane swizzles (register-to-register, a few
+// cycles) rather than ds_bpermute (an LDS round trip each). The caller's
+// wavefront must have every lane active. Max and integer sums do not depend
+// on the order of their operands, so the results equal any other reduction's.
+//   quad_perm [1,0,3,2] = lane ^ 1, [2,3,0,1] = lane ^ 2,
+//   row_half_mirror: lane i of each 8-lane half row <- lane 7 - i (after a quad
+//     reduction, the other quad of the 8 lanes),
+//   row_mirror: lane i of each 16-lane row <- lane 15 - i (after an 8-lane
+//     reduction, the other 8 lanes of the row).
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140;
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, dpp_i<CTRL>(__builtin_bit_cast(int, v)));
+}
+
+// max over each aligned group of 8 lanes, in all 8
 __device__ __forceinline__ float wave_max8(float v) {
-    v = fmaxf(v, __shfl_xor(v, 1));
-    v = fmaxf(v, __shfl_xor(v, 2));
-    v = fmaxf(v, __shfl_xor(v, 4));
-    return v;
+    v = fmaxf(v, dpp_f<kDppXor1>(v));
+    v = fmaxf(v, dpp_f<kDppXor2>(v));
+    return fmaxf(v, dpp_f<kDppHalfMirror>(v));
 }
 
+// max over each 16-lane row, in all 16
+__device__ __forceinline__ float wave_max16(float v) {
+    v = wave_max8(v);
+    return fmaxf(v, dpp_f<kDppMirror>(v));
+}
+
+// max over the wavefront, in all lanes (the four row maxima through scalar registers)
 __device__ __forceinline__ float wave_max64(float v) {
-    for (int off = 1; off < 64; off <<= 1) v = fmaxf(v, __shfl_xor(v, off));
-    return v;
+    v = wave_max16(v);
+    const float a = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+    const float b = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+    const float c = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    const float d = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+    return fmaxf(fmaxf(a, b), fmaxf(c, d));
 }
 
+// sum over each aligned group of 4 lanes, in all 4
+__device__ __forceinline__ int wave_sum4(int v) {
+    v += dpp_i<kDppXor1>(v);
+    return v + dpp_i<kDppXor2>(v);
+}
+
+// sum over each aligned group of 8 lanes, in all 8
 __device__ __forceinline__ int wave_sum8(int v) {
-    v += __shfl_xor(v, 1);
-    v += __shfl_xor(v, 2);
-    v += __shfl_xor(v, 4);
-    return v;
+    v = wave_sum4(v);
+    return v + dpp_i<kDppHalfMirror>(v);
 }
 
 __device__ __forceinline__ int code(float x, float id) {
@@ -85,10 +121,8 @@ __device__ __forceinline__ void quantize_to_lds(const float4 (&xv)[XV], int n_in
         } else {
             const float d = block_d(wave_max64(a)), id = block_id(d);
             const int q0 = code(v.x, id), q1 = code(v.y, id), q2 = code(v.z, id), q3 = code(v.w, id);
-            int g16 = q0 + q1 + q2 + q3;
-            g16 += __shfl_xor(g16, 1);
-            g16 += __shfl_xor(g16, 2);
-            const int g16b = __shfl_xor(g16, 4);
+            const int g16 = wave_sum4(q0 + q1 + q2 + q3);
+            const int g16b = dpp_i<kDppHalfMirror>(g16);  // the other 16 values of the 32-value group
             if (active) {
                 *reinterpret_cast<uint32_t*>(dst) = pack4(q0, q1, q2, q3);
                 if (lane == 0) L.d[k0 >> 8] = d;

@@ -95,16 +95,14 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float* __restrict__
 
     // ---- 256-value blocks (only when every row is a whole number of them)
     if ((o.d256 || o.gA || o.aos256) && (n_in % 256) == 0) {
-        float amax = a;
-        for (int off = 1; off < 64; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+        const float amax = wave_max64(a);
         const float d = amax / 127.0f;
         const float id = d > 0.0f ? 1.0f / d : 0.0f;
         const int q0 = code(v.x, id), q1 = code(v.y, id), q2 = code(v.z, id), q3 = code(v.w, id);
         const int s4 = q0 + q1 + q2 + q3;
         // per-16 sums: lanes 4j..4j+3 hold one 16-value group; 8 lanes one 32-value group
-        int g16 = s4 + __shfl_xor(s4, 1);
-        g16 += __shfl_xor(g16, 2);
-        const int g32 = g16 + __shfl_xor(g16, 4);
+        const int g16 = wave_sum4(s4);
+        const int g32 = g16 + dpp_i<kDppHalfMirror>(g16);
         const uint32_t packed = pack4(q0, q1, q2, q3);
         if (o.gA) {
             // 32x32x32 MFMA planes: token block tb, step k0 / 32, half h, 4-byte slot of the lane
