@@ -413,7 +413,7 @@ public:
         std::lock_guard<std::mutex> lk(mu_);
         span_free();
         if (!ensure_init() || broken_ || p.n_layers <= 0 || !p.layers || p.n_embd <= 0 || p.n_head <= 0 ||
-            p.n_head_kv <= 0 || p.n_head % p.n_head_kv || p.head_dim <= 0 || p.head_dim > 256 || p.n_ff <= 0 ||
+            p.n_head_kv <= 0 || p.n_head % p.n_head_kv || p.head_dim <= 0 || p.head_dim > 256 || p.head_dim % 2 || p.n_ff <= 0 ||
             p.n_ctx <= 0 || p.rot_dim < 0 || p.rot_dim > p.head_dim || p.rot_dim % 2 || !p.rope_cos || !p.rope_sin)
             return false;
         if (p.kv_q8) return false;  // int8 KV cache: not kept here, FISH keeps per-matmul routing

@@ -163,14 +163,23 @@ __global__ __launch_bounds__(kTh) void qkv_prep_kernel(const float* __restrict__
 // order differs. Needs D <= 256.
 constexpr int kCh = 64;
 
-template <int DL>
+// The f16 K / V caches are read as element pairs, one dword per lane (2-byte
+// loads become half-register loads that the compiler waits on one by one):
+// lane l owns the pairs 2 (l + 64 j), j < NP, of a head of D (even) values.
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float2 f16x2(uint32_t u) {
+    const half2_t h = __builtin_bit_cast(half2_t, u);
+    return make_float2(float(h.x), float(h.y));
+}
+
+template <int NP>
 __global__ __launch_bounds__(kTh) void attn_part_kernel(const float* __restrict__ q, const _Float16* __restrict__ kc,
                                                         const _Float16* __restrict__ vc, float* __restrict__ part,
                                                         int S, int H, int HKV, int D, int pos0,
                                                         const int* __restrict__ pos_dev, float scale) {
     constexpr int PB = kCh / 4;
     __shared__ float s_e[kCh];
-    __shared__ float s_o[4][64 * DL];
+    __shared__ float s_o[4][128 * NP];
     __shared__ float s_ml[2];
     if (pos_dev) pos0 = *pos_dev;
     const int item = blockIdx.x, chunk = blockIdx.y, t = item / H, h = item % H;
@@ -187,25 +196,33 @@ __global__ __launch_bounds__(kTh) void attn_part_kernel(const float* __restrict_
         return;
     }
     const int jn = min(pos, j0 + kCh - 1);
-    float qv[DL];
+    float2 qv[NP];
 #pragma unroll
-    for (int i = 0; i < DL; ++i) qv[i] = lane + 64 * i < D ? q[size_t(t) * Q + size_t(h) * D + lane + 64 * i] : 0.0f;
-    const _Float16* kb = kc + size_t(kvh) * D;
-    const _Float16* vb = vc + size_t(kvh) * D;
+    for (int i = 0; i < NP; ++i) {
+        const int e = 2 * (lane + 64 * i);
+        qv[i] = e < D ? *reinterpret_cast<const float2*>(q + size_t(t) * Q + size_t(h) * D + e) : make_float2(0.f, 0.f);
+    }
+    const uint32_t* kb = reinterpret_cast<const uint32_t*>(kc + size_t(kvh) * D);
+    const uint32_t* vb = reinterpret_cast<const uint32_t*>(vc + size_t(kvh) * D);
+    const int KV2 = KV / 2;
 
     // scores of positions j0 + w + 4 b
-    float kv[PB][DL];
+    uint32_t kv[PB][NP];
 #pragma unroll
     for (int b = 0; b < PB; ++b) {
-        const _Float16* kr = kb + size_t(min(j0 + w + 4 * b, jn)) * KV;
+        const uint32_t* kr = kb + size_t(min(j0 + w + 4 * b, jn)) * KV2;
 #pragma unroll
-        for (int i = 0; i < DL; ++i) kv[b][i] = lane + 64 * i < D ? float(kr[lane + 64 * i]) : 0.0f;
+        for (int i = 0; i < NP; ++i) kv[b][i] = 2 * (lane + 64 * i) < D ? kr[lane + 64 * i] : 0u;
     }
 #pragma unroll
     for (int b = 0; b < PB; ++b) {
         float sum = 0.0f;
 #pragma unroll
-        for (int i = 0; i < DL; ++i) sum += qv[i] * kv[b][i];
+        for (int i = 0; i < NP; ++i) {
+            const float2 k2 = f16x2(kv[b][i]);
+            sum += qv[i].x * k2.x;
+            sum += qv[i].y * k2.y;
+        }
 #pragma unroll
         for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
         if (lane == 0) s_e[w + 4 * b] = j0 + w + 4 * b <= jn ? sum * scale : -INFINITY;
@@ -226,24 +243,28 @@ __global__ __launch_bounds__(kTh) void attn_part_kernel(const float* __restrict_
         }
     }
     __syncthreads();
-    float vv[PB][DL];
+    uint32_t vv[PB][NP];
 #pragma unroll
     for (int b = 0; b < PB; ++b) {
-        const _Float16* vr = vb + size_t(min(j0 + w + 4 * b, jn)) * KV;
+        const uint32_t* vr = vb + size_t(min(j0 + w + 4 * b, jn)) * KV2;
 #pragma unroll
-        for (int i = 0; i < DL; ++i) vv[b][i] = lane + 64 * i < D ? float(vr[lane + 64 * i]) : 0.0f;
+        for (int i = 0; i < NP; ++i) vv[b][i] = 2 * (lane + 64 * i) < D ? vr[lane + 64 * i] : 0u;
     }
-    float acc[DL];
+    float2 acc[NP];
 #pragma unroll
-    for (int i = 0; i < DL; ++i) acc[i] = 0.0f;
+    for (int i = 0; i < NP; ++i) acc[i] = make_float2(0.f, 0.f);
 #pragma unroll
     for (int b = 0; b < PB; ++b) {
         const float e = s_e[w + 4 * b];  // 0 past jn
 #pragma unroll
-        for (int i = 0; i < DL; ++i) acc[i] += e * vv[b][i];
+        for (int i = 0; i < NP; ++i) {
+            const float2 v2 = f16x2(vv[b][i]);
+            acc[i].x += e * v2.x;
+            acc[i].y += e * v2.y;
+        }
     }
 #pragma unroll
-    for (int i = 0; i < DL; ++i) s_o[w][lane + 64 * i] = acc[i];
+    for (int i = 0; i < NP; ++i) *reinterpret_cast<float2*>(&s_o[w][2 * (lane + 64 * i)]) = acc[i];
     __syncthreads();
     for (int d = tid; d < D; d += kTh) pp[d] = (s_o[0][d] + s_o[1][d]) + (s_o[2][d] + s_o[3][d]);
     if (tid == 0) {
@@ -290,39 +311,55 @@ __global__ __launch_bounds__(kTh) void attn_combine_kernel(const float* __restri
 // the chunks of kCh positions up to the token's own, each chunk as in
 // attn_part_kernel, and merges them into a running (max, sum, output) --
 // no partials in memory, so the scratch does not grow with tokens x context.
-template <int DL>
+template <int NP>
 __global__ __launch_bounds__(kTh) void attn_full_kernel(const float* __restrict__ q, const _Float16* __restrict__ kc,
                                                         const _Float16* __restrict__ vc, float* __restrict__ out,
                                                         int H, int HKV, int D, int pos0,
                                                         const int* __restrict__ pos_dev, float scale) {
     constexpr int PB = kCh / 4;
     __shared__ float s_e[kCh];
-    __shared__ float s_o[4][64 * DL];
+    __shared__ float s_o[4][128 * NP];
     __shared__ float s_ml[2];
     if (pos_dev) pos0 = *pos_dev;
     const int item = blockIdx.x, t = item / H, h = item % H;
     const int pos = pos0 + t, kvh = h / (H / HKV), KV = HKV * D, Q = H * D;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    float qv[DL];
+    float2 qv[NP];
 #pragma unroll
-    for (int i = 0; i < DL; ++i) qv[i] = lane + 64 * i < D ? q[size_t(t) * Q + size_t(h) * D + lane + 64 * i] : 0.0f;
-    const _Float16* kb = kc + size_t(kvh) * D;
-    const _Float16* vb = vc + size_t(kvh) * D;
+    for (int i = 0; i < NP; ++i) {
+        const int e = 2 * (lane + 64 * i);
+        qv[i] = e < D ? *reinterpret_cast<const float2*>(q + size_t(t) * Q + size_t(h) * D + e) : make_float2(0.f, 0.f);
+    }
+    const uint32_t* kb = reinterpret_cast<const uint32_t*>(kc + size_t(kvh) * D);
+    const uint32_t* vb = reinterpret_cast<const uint32_t*>(vc + size_t(kvh) * D);
+    const int KV2 = KV / 2;
     float o_run = 0.0f, m_run = -INFINITY, l_run = 0.0f;
     for (int j0 = 0; j0 <= pos; j0 += kCh) {
         const int jn = min(pos, j0 + kCh - 1);
-        float kv[PB][DL];
+        uint32_t kv[PB][NP];
 #pragma unroll
         for (int b = 0; b < PB; ++b) {
-            const _Float16* kr = kb + size_t(min(j0 + w + 4 * b, jn)) * KV;
+            const uint32_t* kr = kb + size_t(min(j0 + w + 4 * b, jn)) * KV2;
 #pragma unroll
-            for (int i = 0; i < DL; ++i) kv[b][i] = lane + 64 * i < D ? float(kr[lane + 64 * i]) : 0.0f;
+            for (int i = 0; i < NP; ++i) kv[b][i] = 2 * (lane + 64 * i) < D ? kr[lane + 64 * i] : 0u;
+        }
+        // V rows of the chunk in flight while the scores are formed
+        uint32_t vv[PB][NP];
+#pragma unroll
+        for (int b = 0; b < PB; ++b) {
+            const uint32_t* vr = vb + size_t(min(j0 + w + 4 * b, jn)) * KV2;
+#pragma unroll
+            for (int i = 0; i < NP; ++i) vv[b][i] = 2 * (lane + 64 * i) < D ? vr[lane + 64 * i] : 0u;
         }
 #pragma unroll
         for (int b = 0; b < PB; ++b) {
             float sum = 0.0f;
 #pragma unroll
-            for (int i = 0; i < DL; ++i) sum += qv[i] * kv[b][i];
+            for (int i = 0; i < NP; ++i) {
+                const float2 k2 = f16x2(kv[b][i]);
+                sum += qv[i].x * k2.x;
+                sum += qv[i].y * k2.y;
+            }
 #pragma unroll
             for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
             if (lane == 0) s_e[w + 4 * b] = j0 + w + 4 * b <= jn ? sum * scale : -INFINITY;
@@ -343,24 +380,21 @@ __global__ __launch_bounds__(kTh) void attn_full_kernel(const float* __restrict_
             }
         }
         __syncthreads();
-        float vv[PB][DL];
+        float2 acc[NP];
 #pragma unroll
-        for (int b = 0; b < PB; ++b) {
-            const _Float16* vr = vb + size_t(min(j0 + w + 4 * b, jn)) * KV;
-#pragma unroll
-            for (int i = 0; i < DL; ++i) vv[b][i] = lane + 64 * i < D ? float(vr[lane + 64 * i]) : 0.0f;
-        }
-        float acc[DL];
-#pragma unroll
-        for (int i = 0; i < DL; ++i) acc[i] = 0.0f;
+        for (int i = 0; i < NP; ++i) acc[i] = make_float2(0.f, 0.f);
 #pragma unroll
         for (int b = 0; b < PB; ++b) {
             const float e = s_e[w + 4 * b];  // 0 past jn
 #pragma unroll
-            for (int i = 0; i < DL; ++i) acc[i] += e * vv[b][i];
+            for (int i = 0; i < NP; ++i) {
+                const float2 v2 = f16x2(vv[b][i]);
+                acc[i].x += e * v2.x;
+                acc[i].y += e * v2.y;
+            }
         }
 #pragma unroll
-        for (int i = 0; i < DL; ++i) s_o[w][lane + 64 * i] = acc[i];
+        for (int i = 0; i < NP; ++i) *reinterpret_cast<float2*>(&s_o[w][2 * (lane + 64 * i)]) = acc[i];
         __syncthreads();
         // merge the chunk (mc, lc, oc) into the running softmax
         const float mc = s_ml[0], lc = s_ml[1], mn = fmaxf(m_run, mc);
@@ -416,26 +450,22 @@ hipError_t launch_qkv_prep(const float* q, const float* k, const float* v, const
 hipError_t launch_attention(const float* q, const _Float16* kc, const _Float16* vc, float* out, float* part, int ld,
                             int n_tok, int H, int HKV, int D, int pos0, float scale, hipStream_t s,
                             const int* pos_dev) {
-    if (n_tok <= 0 || D <= 0 || D > kTh || HKV <= 0 || H % HKV || ld < pos0 + n_tok) return hipErrorInvalidValue;
+    if (n_tok <= 0 || D <= 0 || D > kTh || D % 2 || HKV <= 0 || H % HKV || ld < pos0 + n_tok) return hipErrorInvalidValue;
     const dim3 block(kTh);
     if (n_tok > kAttnSplitTok) {
         const dim3 grid(unsigned(n_tok * H));
-        if (D <= 64)
+        if (D <= 128)
             hipLaunchKernelGGL(attn_full_kernel<1>, grid, block, 0, s, q, kc, vc, out, H, HKV, D, pos0, pos_dev, scale);
-        else if (D <= 128)
-            hipLaunchKernelGGL(attn_full_kernel<2>, grid, block, 0, s, q, kc, vc, out, H, HKV, D, pos0, pos_dev, scale);
         else
-            hipLaunchKernelGGL(attn_full_kernel<4>, grid, block, 0, s, q, kc, vc, out, H, HKV, D, pos0, pos_dev, scale);
+            hipLaunchKernelGGL(attn_full_kernel<2>, grid, block, 0, s, q, kc, vc, out, H, HKV, D, pos0, pos_dev, scale);
         return hipGetLastError();
     }
     const int S = (ld + kCh - 1) / kCh;
     const dim3 grid(unsigned(n_tok * H), unsigned(S));
-    if (D <= 64)
+    if (D <= 128)
         hipLaunchKernelGGL(attn_part_kernel<1>, grid, block, 0, s, q, kc, vc, part, S, H, HKV, D, pos0, pos_dev, scale);
-    else if (D <= 128)
-        hipLaunchKernelGGL(attn_part_kernel<2>, grid, block, 0, s, q, kc, vc, part, S, H, HKV, D, pos0, pos_dev, scale);
     else
-        hipLaunchKernelGGL(attn_part_kernel<4>, grid, block, 0, s, q, kc, vc, part, S, H, HKV, D, pos0, pos_dev, scale);
+        hipLaunchKernelGGL(attn_part_kernel<2>, grid, block, 0, s, q, kc, vc, part, S, H, HKV, D, pos0, pos_dev, scale);
     hipLaunchKernelGGL(attn_combine_kernel, dim3(unsigned(n_tok * H)), block, 0, s, part, out, S, H, D);
     return hipGetLastError();
 }
