@@ -110,17 +110,21 @@ def run_gemv(args, torch, fh, dev):
 
 def run_prefill(args, torch, fh, dev):
     """One Llama-3-8B layer's projections at M = 512 (Q4_K; down in Q6_K): q/k/v and
-    gate/up each as one grouped launch on the same activations, as FISH's matmul_tensors."""
+    gate/up each as one grouped launch on the same activations, as FISH's matmul_tensors.
+    Successive layer steps use the next of several weight copies, so no step finds the
+    previous step's weights in the 256 MB MALL."""
     from imurun_amd.synth import normal
     M = 512
     shapes = [("q", fh.Q4_K, E, E), ("k", fh.Q4_K, 1024, E), ("v", fh.Q4_K, 1024, E), ("o", fh.Q4_K, E, E),
               ("gate", fh.Q4_K, F, E), ("up", fh.Q4_K, F, E), ("down", fh.Q6_K, E, F)]
     # 1024 distinct packed rows per tensor, repeated to the full height (timing does not depend on values)
-    ws = {}
+    base, layer_bytes = {}, 0
     for i, (name, t, n_out, n_in) in enumerate(shapes):
-        base = fh.quantize_rows(t, normal(200 + i, (1024, n_in), 0.02))
-        full = torch.from_numpy(base).to(dev).repeat(n_out // 1024)
-        ws[name] = (t, n_out, n_in, fh.repack(t, full, n_in, n_out))
+        base[name] = torch.from_numpy(fh.quantize_rows(t, normal(200 + i, (1024, n_in), 0.02))).to(dev)
+        layer_bytes += base[name].numel() * (n_out // 1024)
+    copies = max(2, int(2 * MALL_BYTES // layer_bytes) + 2)
+    ws = [{name: (t, n_out, n_in, fh.repack(t, base[name].repeat(n_out // 1024), n_in, n_out))
+           for name, t, n_out, n_in in shapes} for _ in range(copies)]
     x = torch.from_numpy(normal(210, (M, E))).to(dev)
     hx = torch.from_numpy(normal(211, (M, F))).to(dev)
     ax = torch.empty(fh.act_bytes(M, E), dtype=torch.uint8, device=dev)
@@ -128,25 +132,27 @@ def run_prefill(args, torch, fh, dev):
     ys = {name: torch.empty((M, n_out), dtype=torch.float32, device=dev) for name, _, n_out, _ in shapes}
     ops = sum(2 * M * n_out * n_in for _, _, n_out, n_in in shapes)
 
-    def group(names, act):
-        t, _, n_in, _ = ws[names[0]]
-        fh.matmul_group(t, [ws[n][3] for n in names], act, M, n_in, [ws[n][1] for n in names],
+    def group(c, names, act):
+        t, _, n_in, _ = ws[c][names[0]]
+        fh.matmul_group(t, [ws[c][n][3] for n in names], act, M, n_in, [ws[c][n][1] for n in names],
                         ys=[ys[n] for n in names])
 
     parts = {
-        "quantize_x": lambda: fh.quantize(x, act=ax),
-        "qkv": lambda: group(["q", "k", "v"], ax),
-        "o": lambda: group(["o"], ax),
-        "gate_up": lambda: group(["gate", "up"], ax),
-        "quantize_h": lambda: fh.quantize(hx, act=ah),
-        "down": lambda: group(["down"], ah),
+        "quantize_x": lambda c: fh.quantize(x, act=ax),
+        "qkv": lambda c: group(c, ["q", "k", "v"], ax),
+        "o": lambda c: group(c, ["o"], ax),
+        "gate_up": lambda c: group(c, ["gate", "up"], ax),
+        "quantize_h": lambda c: fh.quantize(hx, act=ah),
+        "down": lambda c: group(c, ["down"], ah),
     }
     reps = max(10, args.steps // 4)
-    layer_us = graph_time(torch, [lambda: [f() for f in parts.values()]], reps)
-    # each part as eight back-to-back calls in one graph: a one-launch graph per replay would
-    # time the host's graph launches for the short parts, not the kernels
-    per = {name: graph_time_seq(torch, [f] * 8, reps) for name, f in parts.items()}
-    return ops, layer_us, per
+    layer_us = graph_time(torch, [lambda c=c: [f(c) for f in parts.values()] for c in range(copies)],
+                          max(reps, 2 * copies))
+    # each part as back-to-back calls over the copies in one graph: a one-launch graph per replay
+    # would time the host's graph launches for the short parts, not the kernels
+    per = {name: graph_time_seq(torch, [lambda c=c, f=f: f(c) for c in range(copies)] * 2, reps)
+           for name, f in parts.items()}
+    return ops, layer_us, per, copies
 
 
 def graph_time(torch, fns, reps):
@@ -390,15 +396,68 @@ def run_moe(args, torch, fh, dev, name, NE, K, E, F_, types, cases):
     return out
 
 
+def host_topology():
+    """Physical cores and sockets of this host (from /proc/cpuinfo), logical CPUs and the CPUs this
+    process may run on: FISH sizes its pool from the physical core count (threadpool.cpp:47-60)."""
+    pairs, sockets = set(), set()
+    phys = core = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                k, _, v = line.partition(":")
+                k = k.strip()
+                if k == "physical id":
+                    phys = v.strip()
+                elif k == "core id":
+                    core = v.strip()
+                elif not k:
+                    if phys is not None and core is not None:
+                        pairs.add((phys, core))
+                        sockets.add(phys)
+                    phys = core = None
+    except OSError:
+        pass
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        affinity = None
+    return {"physical_cores": len(pairs) or None, "sockets": len(sockets) or None,
+            "logical_cpus": os.cpu_count(), "affinity_cpus": affinity}
+
+
+def timed_loop(fn, seconds, n_sets=1):
+    """Run fn(i) once untimed, then until `seconds` have passed (at least once); (calls, elapsed s)."""
+    fn(0)
+    n, t0 = 0, time.perf_counter()
+    while True:
+        fn(n % n_sets)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            return n, el
+
+
 def run_cpu_baseline(args, step_bytes):
-    """The reference's own CPU path (FISH's quantize + threaded AVX2 matmul_batch)."""
-    threads = min(16, os.cpu_count() or 1)
-    os.environ.setdefault("FISH_THREADS", str(threads))
+    """The reference's own CPU path (FISH's quantize + threaded AVX2 matmul_batch and its moe_ffn
+    loop), one bounded sample per workload. FISH picks its thread count itself (FISH_THREADS unset:
+    min(physical cores, 32), threadpool.cpp:47-60); FISH_LOW_PRIORITY=0 keeps the pool un-niced."""
+    os.environ.pop("FISH_THREADS", None)
     os.environ["FISH_LOW_PRIORITY"] = "0"
     from imurun_amd.synth import normal
     import imurun_amd as fh
     from oracle.oracle import Oracle, Ref
     kind = "reference" if Ref.available() else "port"
+    if kind == "reference":
+        ref = Ref()
+        threads = ref.threads()
+        mm = lambda t, w, v, n_out: ref.matmul_f32(t, w, v, n_out)  # noqa: E731
+        moe = ref.moe_ffn
+    else:
+        orc = Oracle()
+        orc.threads = 1
+        threads = 1
+        mm = lambda t, w, v, n_out: orc.matmul_f32(t, w, v, n_out)  # noqa: E731
+        moe = orc.moe_ffn
     t = fh.Q4_0
     copies = 4  # > 4x any host LLC: weights come from DRAM like a real decode step
     base = (fh.quantize_rows(t, normal(101, (F, E), 0.02)), fh.quantize_rows(t, normal(102, (F, E), 0.02)),
@@ -406,90 +465,215 @@ def run_cpu_baseline(args, step_bytes):
     sets = [tuple(a.copy() for a in base) for _ in range(copies)]
     x = normal(104, (1, E))
     h = normal(105, (1, F))
-    if kind == "reference":
-        ref = Ref()
-        threads = ref.threads()
-        mm = lambda w, v, n_out: ref.matmul_f32(t, w, v, n_out)  # noqa: E731
-    else:
-        orc = Oracle()
-        orc.threads = 1
-        threads = 1
-        mm = lambda w, v, n_out: orc.matmul_f32(t, w, v, n_out)  # noqa: E731
-    for g, u, d in sets:
-        mm(g, x, F)
-    n = 0
-    t0 = time.perf_counter()
-    while True:
-        g, u, d = sets[n % copies]
-        mm(g, x, F)
-        mm(u, x, F)
-        mm(d, h, E)
-        n += 1
-        if time.perf_counter() - t0 >= args.cpu_seconds:
-            break
-    el = time.perf_counter() - t0
-    return {"value": round(step_bytes * n / el / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": kind,
-            "sample": f"{n} decode FFN steps (Q4_0 gate+up 14336x4096, down 4096x14336, M=1, int8 activations "
-                      f"quantized per call) over {copies} weight copies, {el:.1f} s"}
+
+    def ffn(i):
+        g, u, d = sets[i]
+        mm(t, g, x, F)
+        mm(t, u, x, F)
+        mm(t, d, h, E)
+    n, el = timed_loop(ffn, args.cpu_seconds, copies)
+    del sets
+    out = {"value": round(step_bytes * n / el / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": kind,
+           "sample": f"{n} decode FFN steps (Q4_0 gate+up 14336x4096, down 4096x14336, M=1, int8 activations "
+                     f"quantized per call) over {copies} weight copies, {el:.1f} s",
+           "host": dict(host_topology(), threads_used=threads,
+                        thread_policy="FISH default_threads(): min(physical cores, 32), FISH_THREADS unset")}
+    if args.no_extras:
+        return out
+    per = {}
+    budget = max(1.0, args.cpu_seconds / 4)
+
+    # Q8_0 GEMV 4096x4096, M=1
+    q8 = [fh.quantize_rows(fh.Q8_0, normal(121, (4096, 4096), 0.02)) for _ in range(1)]
+    q8 = [q8[0].copy() for _ in range(8)]  # 8 x 17.8 MB copies rotated past the host caches
+    xq = normal(122, (1, 4096))
+    n, el = timed_loop(lambda i: mm(fh.Q8_0, q8[i], xq, 4096), budget, len(q8))
+    us = el / n * 1e6
+    b = q8[0].size + 4096 * 8
+    per["q8_0_gemv"] = {"us": round(us, 1), "gbs": round(b / us / 1e3, 2),
+                        "sample": f"{n} calls over 8 weight copies, {el:.1f} s"}
+    del q8
+
+    # Llama-3-8B layer projections at M = 512 (Q4_K; down Q6_K), each matmul quantizing its input
+    M = 512
+    shapes = [("q", fh.Q4_K, E, E), ("k", fh.Q4_K, 1024, E), ("v", fh.Q4_K, 1024, E), ("o", fh.Q4_K, E, E),
+              ("gate", fh.Q4_K, F, E), ("up", fh.Q4_K, F, E), ("down", fh.Q6_K, E, F)]
+    lw = {}
+    for i, (name, tt, n_out, n_in) in enumerate(shapes):
+        lw[name] = np.tile(fh.quantize_rows(tt, normal(200 + i, (1024, n_in), 0.02)), n_out // 1024)
+    xp = normal(210, (M, E))
+    hp = normal(211, (M, F))
+
+    def layer(_):
+        for name, tt, n_out, n_in in shapes:
+            mm(tt, lw[name], hp if n_in == F else xp, n_out)
+    n, el = timed_loop(layer, budget)
+    ops = sum(2 * M * n_out * n_in for _, _, n_out, n_in in shapes)
+    per["prefill_layer_m512"] = {"ms": round(el / n * 1e3, 2), "tops": round(ops * n / el / 1e12, 3),
+                                 "sample": f"{n} layers (7 matmuls each, M=512), {el:.1f} s"}
+    del lw
+
+    # expert layers through FISH's moe_ffn loop (model.cpp:1523-1599)
+    for key, NE, K, E_, F_, types, cases in (("moe_mixtral", 8, 2, 4096, 14336, (fh.Q4_K, fh.Q4_K, fh.Q4_K), (1, 64)),
+                                             ("moe_qwen3", 128, 8, 2048, 768, (fh.Q4_K, fh.Q4_K, fh.Q6_K), (1, 256))):
+        tg, tu, td = types
+        pg = fh.quantize_rows(tg, normal(131, (F_, E_), 0.02))
+        pu = fh.quantize_rows(tu, normal(132, (F_, E_), 0.02))
+        pd = fh.quantize_rows(td, normal(133, (E_, F_), 0.02))
+        per_expert = pg.size + pu.size + pd.size
+        wg, wu, wd = np.tile(pg, NE), np.tile(pu, NE), np.tile(pd, NE)
+        res = {}
+        for M_ in cases:
+            xm = normal(134 + M_, (M_, E_))
+            if M_ == 1:
+                lsets = []
+                for s_ in range(NE // K):
+                    lg = np.full((1, NE), -4.0, np.float32)
+                    lg[0, s_ * K:(s_ + 1) * K] = 4.0 + np.arange(K, dtype=np.float32) * 0.1
+                    lsets.append(lg)
+                active = K
+            else:
+                lsets = [normal(135 + M_, (M_, NE))]
+                active = int(np.unique(Oracle().route(lsets[0], K, True)[0]).size)
+            n, el = timed_loop(lambda i: moe(xm, lsets[i], E_, F_, NE, K, True, tg, wg, tu, wu, td, wd),
+                               budget, len(lsets))
+            us = el / n * 1e6
+            b = active * per_expert + M_ * E_ * 8
+            res[f"M{M_}"] = {"us": round(us, 1), "gbs": round(b / us / 1e3, 2),
+                             "tops": round(2 * M_ * K * 3 * E_ * F_ / us / 1e6, 3),
+                             "sample": f"{n} layer calls, {el:.1f} s"}
+        per[key] = res
+        del wg, wu, wd
+    out["per_config"] = per
+    return out
 
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
 COPY_BYTES = 256 << 20
 
 
-def run_kernel_only(args, torch, fh, dev):
-    """For rocprofv3 counter passes: the dominant launch (gate + up on one x,
-    rotating weight copies past the MALL) `--steps` times, then a plain device
-    copy of COPY_BYTES that calibrates FETCH_SIZE / WRITE_SIZE against known bytes."""
-    from imurun_amd.synth import normal
-    t = fh.Q4_0
-    wg = fh.quantize_rows(t, normal(101, (F, E), 0.02))
-    wu = fh.quantize_rows(t, normal(102, (F, E), 0.02))
-    copies = max(2, int(2 * MALL_BYTES // (wg.size + wu.size)) + 2)
-    sets = [tuple(fh.repack(t, torch.from_numpy(a).to(dev), E, F) for a in (wg, wu)) for _ in range(copies)]
-    x = torch.from_numpy(normal(104, (1, E))).to(dev)
-    yg = torch.empty((1, F), dtype=torch.float32, device=dev)
-    yu = torch.empty((1, F), dtype=torch.float32, device=dev)
-    for i in range(args.steps):
-        g, u = sets[i % copies]
-        fh.matmul_tensors(t, [g, u], x, [F, F], ys=[yg, yu])
+def calibration_copy(torch, dev):
+    """A plain device copy of COPY_BYTES: what FETCH_SIZE / WRITE_SIZE (and the EA request counters)
+    read for known bytes, the factor that turns their per-dispatch values into HBM bytes."""
     src = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device=dev).fill_(1.0)
     dst = torch.empty_like(src)
     torch.cuda.synchronize()
     dst.copy_(src)
     torch.cuda.synchronize()
-    print(json.dumps({"kernel_only": "gemv_x_kernel<Q4_0> gate+up", "launches": args.steps,
+
+
+def kernel_only_launches(name, torch, fh, dev):
+    """(description, algorithmic bytes per launch, launch closures) of one decode kernel over weight
+    copies rotated past the MALL: the counter passes see the kernels the bench times, on the same
+    shapes, each launch reading weights that are not cache resident."""
+    from imurun_amd.synth import normal
+    if name in ("gemv_gate_up", "q4k_gate_up", "q4k_down"):
+        t = fh.Q4_0 if name == "gemv_gate_up" else fh.Q4_K
+        down = name == "q4k_down"
+        mats = [(103 if t == fh.Q4_0 else 143, F, E)] if down else \
+            [(101 if t == fh.Q4_0 else 141, E, F), (102 if t == fh.Q4_0 else 142, E, F)]
+        packed = [fh.quantize_rows(t, normal(seed, (n_out, n_in), 0.02)) for seed, n_in, n_out in mats]
+        wbytes = sum(p.size for p in packed)
+        copies = max(2, int(2 * MALL_BYTES // wbytes) + 2)
+        sets = [[fh.repack(t, torch.from_numpy(p).to(dev), n_in, n_out) for p, (_, n_in, n_out) in zip(packed, mats)]
+                for _ in range(copies)]
+        n_in = mats[0][1]
+        x = torch.from_numpy(normal(104, (1, n_in))).to(dev)
+        n_outs = [m[2] for m in mats]
+        ys = [torch.empty((1, n), dtype=torch.float32, device=dev) for n in n_outs]
+        desc = (f"gemv_x_kernel<{fh.TYPE_NAMES[t]}> " +
+                ("down 4096x14336" if down else "gate+up 2 x 14336x4096") + ", one token, x quantized in-kernel")
+        return desc, wbytes + n_in * 4 + sum(n_outs) * 4, \
+            [lambda w=w: fh.matmul_tensors(t, w, x, n_outs, ys=ys) for w in sets]
+    if name == "q8_gemv":
+        t, N, K = fh.Q8_0, 4096, 4096
+        p = fh.quantize_rows(t, normal(121, (N, K), 0.02))
+        g = torch.from_numpy(p).to(dev)
+        ws = [fh.repack(t, g, K, N) for _ in range(int(2 * MALL_BYTES // p.size) + 2)]
+        x = torch.from_numpy(normal(122, (1, K))).to(dev)
+        y = torch.empty((1, N), dtype=torch.float32, device=dev)
+        return "gemv_x_kernel<Q8_0> 4096x4096, one token, x quantized in-kernel", p.size + K * 4 + N * 4, \
+            [lambda w=w: fh.matmul_tensors(t, [w], x, [N], ys=[y]) for w in ws]
+    # expert layers: moe_mixtral_m1 / _m64, moe_qwen3_m1 / _m256
+    fam, m = name[4:].rsplit("_m", 1)
+    M = int(m)
+    NE, K, E_, F_, (tg, tu, td) = {"mixtral": (8, 2, 4096, 14336, (fh.Q4_K, fh.Q4_K, fh.Q4_K)),
+                                   "qwen3": (128, 8, 2048, 768, (fh.Q4_K, fh.Q4_K, fh.Q6_K))}[fam]
+    pg = fh.quantize_rows(tg, normal(131, (F_, E_), 0.02))
+    pu = fh.quantize_rows(tu, normal(132, (F_, E_), 0.02))
+    pd = fh.quantize_rows(td, normal(133, (E_, F_), 0.02))
+    wg = fh.repack(tg, torch.from_numpy(pg).to(dev).repeat(NE), E_, NE * F_)
+    wu = fh.repack(tu, torch.from_numpy(pu).to(dev).repeat(NE), E_, NE * F_)
+    wd = fh.repack(td, torch.from_numpy(pd).to(dev).repeat(NE), F_, NE * E_)
+    per_expert = pg.size + pu.size + pd.size
+    x = torch.from_numpy(normal(134 + M, (M, E_))).to(dev)
+    ws = torch.empty(fh.moe_workspace_bytes(M, E_, F_, NE, K), dtype=torch.uint8, device=dev)
+    y = torch.empty((M, E_), dtype=torch.float32, device=dev)
+    if M == 1:
+        logit_sets = []
+        for s_ in range(NE // K):
+            lg = np.full((1, NE), -4.0, np.float32)
+            lg[0, s_ * K:(s_ + 1) * K] = 4.0 + np.arange(K, dtype=np.float32) * 0.1
+            logit_sets.append(torch.from_numpy(lg).to(dev))
+        active = K
+    else:
+        logit_sets = [torch.from_numpy(normal(135 + M, (M, NE))).to(dev)]
+        sel, _ = fh.moe_route(logit_sets[0], K, True)
+        active = int(np.unique(sel.cpu().numpy()).size)
+    desc = f"{fam} expert layer ({NE} experts, top-{K}, hidden {E_}, FFN {F_}), M={M}"
+    return desc, active * per_expert + M * E_ * 8, \
+        [lambda lg=lg: fh.moe_ffn(x, lg, F_, NE, K, True, tg, wg, tu, wu, td, wd, out=y, workspace=ws)
+         for lg in logit_sets]
+
+
+KERNEL_ONLY = ["gemv_gate_up", "q8_gemv", "q4k_gate_up", "q4k_down", "moe_mixtral_m1", "moe_mixtral_m64",
+               "moe_qwen3_m1", "moe_qwen3_m256", "gemm_gate", "gemm_down"]
+
+
+def run_kernel_only(args, torch, fh, dev):
+    """For rocprofv3 counter passes: one workload's launches `--steps` times over rotated weight
+    copies, then the calibration copy."""
+    desc, algo, fns = kernel_only_launches(args.kernel_only, torch, fh, dev)
+    for i in range(args.steps):
+        fns[i % len(fns)]()
+    calibration_copy(torch, dev)
+    print(json.dumps({"kernel_only": desc, "launches": args.steps, "algorithmic_bytes": algo,
                       "copy_bytes": COPY_BYTES}))
     return 0
 
 
-def run_kernel_only_gemm(args, torch, fh, dev):
-    """For rocprofv3 counter passes: one M = 512 prefill GEMM (Q4_K gate 14336x4096 or Q6_K down
-    4096x14336, the prefill layer's weights: 1024 distinct packed rows, repeated) on activations
-    quantized once, `--steps` times back to back."""
-    from imurun_amd.synth import normal
-    M = 512
-    t, n_out, n_in, seed = {"gemm_gate": (fh.Q4_K, F, E, 204), "gemm_down": (fh.Q6_K, E, F, 206)}[args.kernel_only]
-    base = fh.quantize_rows(t, normal(seed, (1024, n_in), 0.02))
-    w = fh.repack(t, torch.from_numpy(base).to(dev).repeat(n_out // 1024), n_in, n_out)
-    x = torch.from_numpy(normal(210, (M, n_in))).to(dev)
-    act = fh.quantize(x)
-    y = torch.empty((M, n_out), dtype=torch.float32, device=dev)
-    for _ in range(args.steps):
-        fh.matmul_group(t, [w], act, M, n_in, [n_out], ys=[y])
-    torch.cuda.synchronize()
-    print(json.dumps({"kernel_only": f"gemm_kq_kernel {fh.TYPE_NAMES[t]} {n_out}x{n_in}, M={M}",
-                      "launches": args.steps}))
-    return 0
+# the device sources each counter-pass workload depends on: a traffic figure is reported only for
+# the sources it was measured on
+_CSRC = os.path.join("imurun_amd", "csrc")
+TRAFFIC_SOURCES = {
+    "gemv": ["gemv.hip", "dots.h", "qact.h", "common.h", "repack.hip"],
+    "moe": ["moe.hip", "batch.hip", "quantize.hip", "dots.h", "qact.h", "common.h", "repack.hip"],
+}
 
 
-def measured_traffic():
-    """HBM bytes per launch of the dominant kernel from the committed counter passes, or None."""
+def sources_sha(group):
+    import hashlib
+    h = hashlib.sha256()
+    for f in TRAFFIC_SOURCES[group]:
+        with open(os.path.join(ROOT, _CSRC, f), "rb") as fh_:
+            h.update(fh_.read())
+    return h.hexdigest()[:16]
+
+
+def measured_traffic(workload):
+    """HBM bytes per call of a counter-pass workload from profiles/traffic.json (FETCH_SIZE and
+    WRITE_SIZE scaled by a plain copy), with the commit-independent hash of the sources it was
+    measured on; (None, reason) when absent or measured on other sources."""
     try:
         with open(TRAFFIC_FILE) as f:
-            return json.load(f).get("bytes_per_launch")
-    except (OSError, ValueError):
-        return None
+            e = json.load(f)["workloads"][workload]
+    except (OSError, ValueError, KeyError):
+        return None, "not measured"
+    group = "moe" if workload.startswith("moe") else "gemv"
+    if e.get("sources_sha") != sources_sha(group):
+        return None, f"stale: measured on sources {e.get('sources_sha')}, now {sources_sha(group)}"
+    return e, (f"rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE passes of bench.py --kernel-only {workload}, scaled by "
+               f"a 256 MiB copy; sources {e['sources_sha']}")
 
 
 def main() -> int:
@@ -501,10 +685,10 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
-    ap.add_argument("--kernel-only", nargs="?", const="gemv_gate_up", default=None,
-                    choices=["gemv_gate_up", "gemm_gate", "gemm_down"],
-                    help="run only one launch --steps times (for rocprofv3 --pmc): the dominant GEMV "
-                         "(then a calibration copy), or the M=512 Q4_K gate / Q6_K down GEMM")
+    ap.add_argument("--kernel-only", nargs="?", const="gemv_gate_up", default=None, choices=KERNEL_ONLY,
+                    help="run only one workload's launches --steps times (for rocprofv3 --pmc): a decode "
+                         "GEMV or expert layer over rotated weight copies, then a calibration copy; or the "
+                         "M=512 Q4_K gate / Q6_K down GEMM")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the path shards by rows/experts "
@@ -516,10 +700,10 @@ def main() -> int:
     assert torch.cuda.is_available(), "bench needs a ROCm GPU"
     dev = torch.device("cuda:0")
     fh.load()
-    if args.kernel_only == "gemv_gate_up":
-        return run_kernel_only(args, torch, fh, dev)
-    if args.kernel_only:
+    if args.kernel_only in ("gemm_gate", "gemm_down"):
         return run_kernel_only_gemm(args, torch, fh, dev)
+    if args.kernel_only:
+        return run_kernel_only(args, torch, fh, dev)
 
     step_bytes, gate_bytes = gemv_step_bytes()
     elapsed, copies, gate_us = run_gemv(args, torch, fh, dev)
@@ -547,9 +731,12 @@ def main() -> int:
                    "weight_type": "Q4_0", "hbm_pct_of_peak": round(100 * value / HBM_PEAK_GBS, 2)},
         "roofline": {"bound": "hbm", "kernel": "gemv_x_kernel<Q4_0> gate+up 2 x 14336x4096, x quantized in-kernel",
                      "achieved": round(gate_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gate_gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+                     "frac": round(gate_gbs / HBM_PEAK_GBS, 4), "traffic": None,
                      "median_kernel_us": round(gate_us, 3), "algorithmic_bytes": gate_bytes},
     }
+    tr, why = measured_traffic("gemv_gate_up")
+    out["roofline"]["traffic"] = tr["bytes_per_call"] if tr else None
+    out["roofline"]["traffic_source"] = why
     if not args.no_extras:
         out["q8_0_gemv"] = run_q8_gemv(args, torch, fh, dev)
         out["q4_k_gemv"] = run_kquant_gemv(args, torch, fh, dev, fh.Q4_K, "Q4_K")
@@ -561,16 +748,25 @@ def main() -> int:
                                      (fh.Q4_K, fh.Q4_K, fh.Q4_K), (1, 64))
         out["moe_qwen3"] = run_moe(args, torch, fh, dev, "Qwen3-30B-A3B", 128, 8, 2048, 768,
                                    (fh.Q4_K, fh.Q4_K, fh.Q6_K), (1, 256))
+        # measured HBM bytes over algorithmic bytes, where a counter pass covers these sources
+        for key, sub, wl in (("q8_0_gemv", None, "q8_gemv"), ("q4_k_gemv", "gate_up", "q4k_gate_up"),
+                             ("q4_k_gemv", "down", "q4k_down"), ("moe_mixtral", "M1", "moe_mixtral_m1"),
+                             ("moe_mixtral", "M64", "moe_mixtral_m64"), ("moe_qwen3", "M1", "moe_qwen3_m1"),
+                             ("moe_qwen3", "M256", "moe_qwen3_m256")):
+            tr, why = measured_traffic(wl)
+            dst = out[key] if sub is None or sub not in out[key] else out[key][sub]
+            name = "traffic_over_algorithmic" if sub is None or sub in out[key] else f"{sub}_traffic_over_algorithmic"
+            dst[name] = tr["traffic_over_algorithmic"] if tr else why
     if not args.no_prefill:
         if not args.no_extras:
             out["q5_k_prefill"] = run_q5k_prefill(args, torch, fh, dev)
-        ops, layer_us, per = run_prefill(args, torch, fh, dev)
+        ops, layer_us, per, pcopies = run_prefill(args, torch, fh, dev)
         tops = ops / layer_us / 1e6
         proj_ops = {"qkv": 2 * 512 * 6144 * E, "o": 2 * 512 * E * E, "gate_up": 2 * 512 * 2 * F * E,
                     "down": 2 * 512 * E * F}
         out["prefill"] = {"workload": "Llama-3-8B layer projections, M=512 (q,k,v,o,gate,up Q4_K; down Q6_K) + "
                                       "activation quantization; q/k/v and gate/up as grouped launches",
-                          "int_ops": ops, "us": round(layer_us, 2), "tops": round(tops, 2),
+                          "weight_copies": pcopies, "int_ops": ops, "us": round(layer_us, 2), "tops": round(tops, 2),
                           "pct_int8_peak": round(100 * tops / INT8_PEAK_TOPS, 2),
                           "parts_us": {k: round(v, 2) for k, v in per.items()},
                           "parts_tops": {k: round(proj_ops[k] / per[k] / 1e6, 1) for k in proj_ops}}
