@@ -642,6 +642,26 @@ def run_kernel_only(args, torch, fh, dev):
     return 0
 
 
+def run_kernel_only_gemm(args, torch, fh, dev):
+    """For rocprofv3 counter passes: one M = 512 prefill GEMM (Q4_K gate 14336x4096 or Q6_K down
+    4096x14336, the prefill layer's weights: 1024 distinct packed rows, repeated) on activations
+    quantized once, `--steps` times back to back."""
+    from imurun_amd.synth import normal
+    M = 512
+    t, n_out, n_in, seed = {"gemm_gate": (fh.Q4_K, F, E, 204), "gemm_down": (fh.Q6_K, E, F, 206)}[args.kernel_only]
+    base = fh.quantize_rows(t, normal(seed, (1024, n_in), 0.02))
+    w = fh.repack(t, torch.from_numpy(base).to(dev).repeat(n_out // 1024), n_in, n_out)
+    x = torch.from_numpy(normal(210, (M, n_in))).to(dev)
+    act = fh.quantize(x)
+    y = torch.empty((M, n_out), dtype=torch.float32, device=dev)
+    for _ in range(args.steps):
+        fh.matmul_group(t, [w], act, M, n_in, [n_out], ys=[y])
+    torch.cuda.synchronize()
+    print(json.dumps({"kernel_only": f"gemm_kq_kernel {fh.TYPE_NAMES[t]} {n_out}x{n_in}, M={M}",
+                      "launches": args.steps}))
+    return 0
+
+
 # the device sources each counter-pass workload depends on: a traffic figure is reported only for
 # the sources it was measured on
 _CSRC = os.path.join("imurun_amd", "csrc")

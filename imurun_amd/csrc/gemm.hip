@@ -381,9 +381,11 @@ __global__ __launch_bounds__(64 * WT * WR) __attribute__((amdgpu_waves_per_eu(2)
         const int tbb = min(tok_tile * TBW + b, A.n_tb - 1);
         e_x = reinterpret_cast<const float4*>(A.gX + (size_t(tbb) * n_sb + sb) * 32)[q];
     };
+    uint4 cur_j = make_uint4(0, 0, 0, 0);  // the mins operand of the super-block in flight (J_REG)
     auto store_epi = [&]() {
         s_meta[tid % RWG] = e_meta;
         if constexpr (has_mins(T) && !J_REG) s_j[tid % EJ] = e_j;
+        if constexpr (has_mins(T) && J_REG) cur_j = e_j;
         s_xd[tid % EX] = e_x;
     };
 
@@ -425,7 +427,7 @@ __global__ __launch_bounds__(64 * WT * WR) __attribute__((amdgpu_waves_per_eu(2)
             for (int r = 0; r < RPW; ++r) {
                 v16f J = v16f{};
                 if constexpr (has_mins(T)) {
-                    const v8h aj = __builtin_bit_cast(v8h, J_REG ? e_j : s_j[wb * 64 + lane]);
+                    const v8h aj = __builtin_bit_cast(v8h, J_REG ? cur_j : s_j[wb * 64 + lane]);
                     J = __builtin_amdgcn_mfma_f32_32x32x16_f16(aj, bj[r], v16f{}, 0, 0, 0);
                 }
 #pragma unroll
@@ -441,8 +443,10 @@ __global__ __launch_bounds__(64 * WT * WR) __attribute__((amdgpu_waves_per_eu(2)
         }
     };
 
-    // ---- prologue: stages 0 and 1 into the ring, stage 2 raw in registers
+    // ---- prologue: stages 0 and 1 into the ring, stage 2 raw in registers,
+    // super-block 0's epilogue data in registers
     Raw raw0[IPT], raw1[IPT];
+    load_epi(0);
     load_stage(raw0, 0);
     load_stage(raw1, min(1, stages - 1));
     store_stage(raw0, 0, 0);
@@ -453,19 +457,27 @@ __global__ __launch_bounds__(64 * WT * WR) __attribute__((amdgpu_waves_per_eu(2)
 
     // ---- main loop, one super-block (two stages) per iteration; stage i
     // computes from slot i % 3, prefetches raw(i + 3) and A(i + 1), and
-    // dequantises raw(i + 2) into slot (i + 2) % 3.
+    // dequantises raw(i + 2) into slot (i + 2) % 3. Every global load is
+    // consumed one stage after it is issued: the epilogue data of super-block
+    // sb + 1 is loaded during the second stage of sb, ahead of that stage's
+    // weight loads (the scheduling barriers keep the issue order, so waiting
+    // for it never waits for weights still on their way from HBM).
     int slot = 0;
     for (int i = 0; i < stages; i += 2) {
         // even stage i: raw0 holds stage i + 2
         __syncthreads();
-        load_epi(i >> 1);
-        load_stage(raw1, min(i + 3, stages - 1));
-        compute_stage(a0, slot, i + 1, raw0, i + 2, slot + 2 >= RING ? slot + 2 - RING : slot + 2);
         store_epi();
+        __builtin_amdgcn_sched_barrier(0);
+        load_stage(raw1, min(i + 3, stages - 1));
+        __builtin_amdgcn_sched_barrier(0);
+        compute_stage(a0, slot, i + 1, raw0, i + 2, slot + 2 >= RING ? slot + 2 - RING : slot + 2);
         slot = slot + 1 == RING ? 0 : slot + 1;
         // odd stage i + 1: raw1 holds stage i + 3
         __syncthreads();
+        load_epi(min((i >> 1) + 1, n_sb - 1));
+        __builtin_amdgcn_sched_barrier(0);
         load_stage(raw0, min(i + 4, stages - 1));
+        __builtin_amdgcn_sched_barrier(0);
         compute_stage(a0, slot, min(i + 2, stages - 1), raw1, i + 3, slot + 2 >= RING ? slot + 2 - RING : slot + 2);
         slot = slot + 1 == RING ? 0 : slot + 1;
         epilogue();
