@@ -98,12 +98,26 @@ def tiny_llama(path: str, types: dict, seed: int = 7, n_layers: int = 2, n_embd:
     output and embd to ggml type ids. Types without a block writer in
     imurun_amd take their bytes from raw(type, n_out, n_in, seed). Returns the
     configuration."""
+    return tiny_model(path, types, seed=seed, n_layers=n_layers, n_embd=n_embd, n_ff=n_ff, n_head=n_head,
+                      n_head_kv=n_head_kv, n_ctx=n_ctx, raw=raw)
+
+
+def tiny_model(path: str, types: dict, arch: str = "llama", seed: int = 7, n_layers: int = 2, n_embd: int = 256,
+               n_ff: int = 768, n_head: int = 4, n_head_kv: int = 2, n_ctx: int = 512, raw=None,
+               head_dim: int = 0, qk_norm: bool = False, biases: bool = False) -> dict:
+    """tiny_llama for the llama-family architectures FISH loads (model.cpp:116-118):
+    `arch` names the metadata keys ("qwen3" and "qwen2" get NeoX RoPE from FISH);
+    head_dim != 0 writes attention.key_length / value_length, so n_head * head_dim
+    may differ from n_embd (as in Qwen-3); qk_norm adds the per-head attn_q_norm /
+    attn_k_norm vectors (model.cpp:335-341); biases adds attn_q / attn_k / attn_v
+    biases (model.cpp:344-346)."""
     import imurun_amd as fh
 
     rng = np.random.default_rng(seed)
     toks, scores, ttypes = spm_vocab()
     vocab = len(toks)
-    head_dim = n_embd // n_head
+    head_dim = head_dim or n_embd // n_head
+    qd = head_dim * n_head
     kv = head_dim * n_head_kv
 
     def mat(name, t, n_out, n_in, std=0.02):
@@ -116,9 +130,13 @@ def tiny_llama(path: str, types: dict, seed: int = 7, n_layers: int = 2, n_embd:
             data = raw(t, n_out, n_in, int(rng.integers(1 << 30))).tobytes()
         return (name, (n_in, n_out), t, data)
 
-    def norm(name):
-        w = (1.0 + 0.1 * rng.standard_normal(n_embd)).astype(np.float32)
-        return (name, (n_embd,), fh.F32, w.tobytes())
+    def norm(name, n=n_embd):
+        w = (1.0 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+        return (name, (n,), fh.F32, w.tobytes())
+
+    def bias(name, n):
+        w = (0.1 * rng.standard_normal(n)).astype(np.float32)
+        return (name, (n,), fh.F32, w.tobytes())
 
     tensors = [mat("token_embd.weight", types["embd"], vocab, n_embd, 1.0), norm("output_norm.weight"),
                mat("output.weight", types["output"], vocab, n_embd)]
@@ -126,25 +144,30 @@ def tiny_llama(path: str, types: dict, seed: int = 7, n_layers: int = 2, n_embd:
         p = f"blk.{i}."
         tensors += [
             norm(p + "attn_norm.weight"), norm(p + "ffn_norm.weight"),
-            mat(p + "attn_q.weight", types["q"], n_embd, n_embd),
+            mat(p + "attn_q.weight", types["q"], qd, n_embd),
             mat(p + "attn_k.weight", types["k"], kv, n_embd),
             mat(p + "attn_v.weight", types["v"], kv, n_embd),
-            mat(p + "attn_output.weight", types["o"], n_embd, n_embd),
+            mat(p + "attn_output.weight", types["o"], n_embd, qd),
             mat(p + "ffn_gate.weight", types["gate"], n_ff, n_embd),
             mat(p + "ffn_up.weight", types["up"], n_ff, n_embd),
             mat(p + "ffn_down.weight", types["down"], n_embd, n_ff),
         ]
+        if qk_norm:
+            tensors += [norm(p + "attn_q_norm.weight", head_dim), norm(p + "attn_k_norm.weight", head_dim)]
+        if biases:
+            tensors += [bias(p + "attn_q.bias", qd), bias(p + "attn_k.bias", kv), bias(p + "attn_v.bias", kv)]
+    a = arch
     meta = [
-        ("general.architecture", STR, "llama"),
+        ("general.architecture", STR, arch),
         ("general.alignment", U32, ALIGN),
-        ("llama.block_count", U32, n_layers),
-        ("llama.embedding_length", U32, n_embd),
-        ("llama.feed_forward_length", U32, n_ff),
-        ("llama.attention.head_count", U32, n_head),
-        ("llama.attention.head_count_kv", U32, n_head_kv),
-        ("llama.attention.layer_norm_rms_epsilon", F32, 1e-5),
-        ("llama.rope.freq_base", F32, 10000.0),
-        ("llama.context_length", U32, n_ctx),
+        (a + ".block_count", U32, n_layers),
+        (a + ".embedding_length", U32, n_embd),
+        (a + ".feed_forward_length", U32, n_ff),
+        (a + ".attention.head_count", U32, n_head),
+        (a + ".attention.head_count_kv", U32, n_head_kv),
+        (a + ".attention.layer_norm_rms_epsilon", F32, 1e-5),
+        (a + ".rope.freq_base", F32, 10000.0),
+        (a + ".context_length", U32, n_ctx),
         ("tokenizer.ggml.model", STR, "llama"),
         ("tokenizer.ggml.tokens", ARR, (STR, toks)),
         ("tokenizer.ggml.scores", ARR, (F32, scores)),
@@ -153,6 +176,8 @@ def tiny_llama(path: str, types: dict, seed: int = 7, n_layers: int = 2, n_embd:
         ("tokenizer.ggml.eos_token_id", U32, 2),
         ("tokenizer.ggml.unknown_token_id", U32, 0),
     ]
+    if head_dim != n_embd // n_head:
+        meta += [(a + ".attention.key_length", U32, head_dim), (a + ".attention.value_length", U32, head_dim)]
     write_gguf(path, meta, tensors)
     return {"n_layers": n_layers, "n_embd": n_embd, "n_ff": n_ff, "n_head": n_head, "n_head_kv": n_head_kv,
-            "vocab": vocab, "n_ctx": n_ctx}
+            "vocab": vocab, "n_ctx": n_ctx, "head_dim": head_dim}
