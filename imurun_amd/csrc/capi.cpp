@@ -559,12 +559,12 @@ public:
             if (e == hipSuccess)
                 for (size_t i = 0; i < tmp.size(); ++i) out[i] = float(tmp[i]);
         } else {
-            if (last_tok_ <= 0 || part < 0 || part >= kSpanBufs - 1) return false;
+            if (last_tok_ <= 0 || part < 0 || part >= kSpanParts) return false;
             size_t z[kSpanBufs], cnt[kSpanBufs];
             span_sizes(last_tok_, last_bufs_.ld, z, cnt);
-            float* const bufs[kSpanBufs - 1] = {last_bufs_.x,   last_bufs_.xb,  last_bufs_.q,    last_bufs_.k,
-                                                last_bufs_.v,   last_bufs_.qr,  last_bufs_.att,  last_bufs_.proj,
-                                                last_bufs_.xb2, last_bufs_.g,   last_bufs_.u,    last_bufs_.dn};
+            float* const bufs[kSpanParts] = {last_bufs_.x,   last_bufs_.xb, last_bufs_.q,   last_bufs_.k,
+                                             last_bufs_.v,   last_bufs_.qr, last_bufs_.att, last_bufs_.proj,
+                                             last_bufs_.xb2, last_bufs_.g,  last_bufs_.u,   last_bufs_.dn};
             if (n_floats < cnt[part]) return false;
             e = hipMemcpy(out, bufs[part], cnt[part] * 4, hipMemcpyDeviceToHost);
         }
@@ -590,6 +590,7 @@ private:
     // projection), xb2 (FFN norm out), g (silu(g) * u after the FFN), u, dn
     // (down projection), attention partials (positions < ld); then the position.
     static constexpr int kSpanBufs = 13;
+    static constexpr int kSpanParts = 12;  // inspectable: x .. dn
     struct SpanBufs {
         float *x, *xb, *q, *k, *v, *qr, *att, *proj, *xb2, *g, *u, *dn, *sc;
         int* pos;
@@ -622,8 +623,8 @@ private:
             p[i] = reinterpret_cast<float*>(b);
             b += z[i];
         }
-        return SpanBufs{p[0], p[1], p[2], p[3], p[4], p[5], p[6], p[7], p[8], p[9], p[10], p[11], p[12],
-                        reinterpret_cast<int*>(b), ld};
+        return SpanBufs{p[0], p[1], p[2],  p[3],  p[4],  p[5], p[6],
+                        p[7], p[8], p[9], p[10], p[11], p[12], reinterpret_cast<int*>(b), ld};
     }
     // device copy of per-layer vector i of layer l, or nullptr when the layer has none
     const float* span_vec(int l, int i) const {
@@ -640,7 +641,7 @@ private:
         const size_t T = size_t(n_tok);
         const float scale = sp_.attn_scale > 0.0f ? sp_.attn_scale : 1.0f / std::sqrt(float(D));
         hipError_t e = hipSuccess;
-        // the FFN residual of layer l - 1 is added by layer l's first rmsnorm
+        // the FFN residual of an unfolded layer l - 1 is added by layer l's first rmsnorm
         const float* pending = nullptr;
         for (int l = 0; l < sp_.n_layers && e == hipSuccess; ++l) {
             const Resident* const* W = rs.data() + size_t(7 * l);
@@ -652,13 +653,36 @@ private:
             float* y_o[1] = {B.proj};
             float* y_gu[2] = {B.g, B.u};
             float* y_d[1] = {B.dn};
-            e = launch_rmsnorm(B.x, pending, nullptr, span_vec(l, 0), B.xb, n_tok, E, sp_.eps, stream_);
-            if (e == hipSuccess) e = run_group(W, 3, B.xb, n_tok, E, n_qkv, y_qkv, act);
+            // one token: each norm is the prologue of its projections' fused launch and each
+            // residual add the epilogue of the projection it follows, so x is rewritten only
+            // by the o and down launches, row by row, and no other launch runs for them
+            const bool fold = n_tok == 1 && E <= 8192 && foldable(W, 7);
+            if (fold && pending) {
+                e = launch_add(B.x, pending, T * E, stream_);
+                pending = nullptr;
+            }
+            if (e == hipSuccess && fold) {
+                const RowNorm an{span_vec(l, 0), B.xb, sp_.eps};
+                e = run_group(W, 3, B.x, n_tok, E, n_qkv, y_qkv, act, &an);
+            } else if (e == hipSuccess) {
+                e = launch_rmsnorm(B.x, pending, nullptr, span_vec(l, 0), B.xb, n_tok, E, sp_.eps, stream_);
+                if (e == hipSuccess) e = run_group(W, 3, B.xb, n_tok, E, n_qkv, y_qkv, act);
+            }
             if (e == hipSuccess)
                 e = launch_qkv_prep(B.q, B.k, B.v, vecs, B.qr, kc, vc, n_tok, H, HKV, D, sp_.rot_dim,
                                     sp_.rope_neox != 0, sp_.eps, pos0, d_cos_, d_sin_, stream_, pos_dev);
             if (e == hipSuccess)
                 e = launch_attention(B.qr, kc, vc, B.att, B.sc, B.ld, n_tok, H, HKV, D, pos0, scale, stream_, pos_dev);
+            if (e == hipSuccess && fold) {
+                const RowResid ro{B.x, span_vec(l, 7)};
+                const RowNorm fn{span_vec(l, 1), B.xb2, sp_.eps};
+                e = run_group(W + 3, 1, B.att, n_tok, Q, n_e, y_o, act, nullptr, &ro);
+                if (e == hipSuccess) e = run_group(W + 4, 2, B.x, n_tok, E, n_f, y_gu, act, &fn);
+                if (e == hipSuccess) e = launch_silu_mul(B.g, B.u, T * F, stream_);
+                const RowResid rd{B.x, nullptr};
+                if (e == hipSuccess) e = run_group(W + 6, 1, B.g, n_tok, F, n_e, y_d, act, nullptr, &rd);
+                continue;
+            }
             if (e == hipSuccess) e = run_group(W + 3, 1, B.att, n_tok, Q, n_e, y_o, act);
             if (e == hipSuccess)
                 e = launch_rmsnorm(B.x, B.proj, span_vec(l, 7), span_vec(l, 1), B.xb2, n_tok, E, sp_.eps, stream_);
@@ -667,7 +691,7 @@ private:
             if (e == hipSuccess) e = run_group(W + 6, 1, B.g, n_tok, F, n_e, y_d, act);
             pending = B.dn;
         }
-        if (e == hipSuccess) e = launch_add(B.x, pending, T * E, stream_);
+        if (e == hipSuccess && pending) e = launch_add(B.x, pending, T * E, stream_);
         return e;
     }
 
@@ -726,8 +750,20 @@ private:
     // The matmuls of n resident tensors on one device input (f32 [n_tok][n_in]):
     // y_i [n_tok][n_out_i] (device). Asynchronous on stream_; d_act_ must hold
     // act_layout(n_tok, n_in).total bytes.
+    // tensors whose one-token matmul is a fused launch (launch_gemv_x), which can also
+    // take a RowNorm prologue
+    static bool foldable(const Resident* const* rs, int n) {
+        for (int i = 0; i < n; ++i)
+            if (!int8_type(rs[i]->layout.type) || !gemv_x_supported(rs[i]->layout)) return false;
+        return true;
+    }
+
+    // norm (one token, foldable tensors only): the RowNorm prologue of every fused launch
     hipError_t run_group(const Resident* const* rs, int n, const float* dx, int n_tok, int n_in, const int* n_outs,
-                         float* const* dys, void* act) {
+                         float* const* dys, void* act, const RowNorm* norm = nullptr,
+                         const RowResid* resid = nullptr) {
+        if ((norm || resid) && (n_tok != 1 || n > kGemmGroupMax || !foldable(rs, n))) return hipErrorInvalidValue;
+        if (resid && n != 1) return hipErrorInvalidValue;
         bool any_int8 = false;
         for (int i = 0; i < n; ++i) any_int8 = any_int8 || int8_type(rs[i]->layout.type);
         // one token, one type: each workgroup quantizes x itself (one launch)
@@ -755,7 +791,7 @@ private:
                     ys[m] = dys[j];
                     ++m;
                 }
-                e = launch_gemv_x(m, ws, Ls, dx, ys, stream_);
+                e = launch_gemv_x(m, ws, Ls, dx, ys, stream_, norm, resid);
             }
             return e;
         }
@@ -774,7 +810,7 @@ private:
                 ws[i] = rs[size_t(i)]->dev;
                 Ls[i] = rs[size_t(i)]->layout;
             }
-            e = launch_gemv_x(n, ws, Ls, dx, dys, stream_);
+            e = launch_gemv_x(n, ws, Ls, dx, dys, stream_, norm, resid);
         } else if (e == hipSuccess && one_group) {
             const void* ws[kGemmGroupMax];
             WeightLayout Ls[kGemmGroupMax];

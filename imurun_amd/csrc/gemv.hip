@@ -224,9 +224,44 @@ struct GemvXGroup {
     int n_out[kGemmGroupMax];
     int wg_end[kGemmGroupMax];  // cumulative workgroups
     int n;
+    RowNorm norm;               // norm.w == nullptr: x as given
+    RowResid resid;             // resid.x == nullptr: y only
 };
 
-template <uint32_t T, int LPR, int MAXC, int RB, int XV>
+// The RowNorm prologue on the workgroup's x chunks (thread tid holds values
+// 4 (tid + TH i) ..): the double sum of x^2 over the row (rmsnorm,
+// ops.cpp:18-23: products and sums in double, then one float scale), then
+// x * scale * w in place; workgroup 0 writes the result.
+template <int XV, int TH>
+__device__ __forceinline__ void row_norm(float4 (&xv)[XV], const RowNorm& nm, int n_in, int tid, double* red) {
+    const int lane = tid & 63, wave = tid >> 6;
+    double s = 0.0;
+#pragma unroll
+    for (int i = 0; i < XV; ++i) {
+        if (4 * (tid + TH * i) < n_in) {
+            s = __dadd_rn(s, __dmul_rn(double(xv[i].x), double(xv[i].x)));
+            s = __dadd_rn(s, __dmul_rn(double(xv[i].y), double(xv[i].y)));
+            s = __dadd_rn(s, __dmul_rn(double(xv[i].z), double(xv[i].z)));
+            s = __dadd_rn(s, __dmul_rn(double(xv[i].w), double(xv[i].w)));
+        }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) s = __dadd_rn(s, __shfl_xor(s, off));
+    if (lane == 0) red[wave] = s;
+    __syncthreads();
+    double sum = 0.0;
+    for (int w = 0; w < TH / 64; ++w) sum = __dadd_rn(sum, red[w]);
+    const float scale = 1.0f / sqrtf(float(sum / n_in) + nm.eps);
+#pragma unroll
+    for (int i = 0; i < XV; ++i) {
+        const int k0 = 4 * (tid + TH * i);
+        const float4 v = xv[i], wv = *reinterpret_cast<const float4*>(nm.w + min(k0, n_in - 4));
+        xv[i] = make_float4(v.x * scale * wv.x, v.y * scale * wv.y, v.z * scale * wv.z, v.w * scale * wv.w);
+        if (blockIdx.x == 0 && k0 < n_in && nm.xn_out) *reinterpret_cast<float4*>(nm.xn_out + k0) = xv[i];
+    }
+}
+
+template <uint32_t T, int LPR, int MAXC, int RB, int XV, bool NORM>
 __global__ __launch_bounds__(64 * kGemvXWaves) void gemv_x_kernel(GemvXGroup G, const float* __restrict__ x,
                                                                   int n_in) {
     constexpr bool kq = kquant_type(T);
@@ -280,6 +315,10 @@ __global__ __launch_bounds__(64 * kGemvXWaves) void gemv_x_kernel(GemvXGroup G, 
 
     // every load is issued before the quantization's first use of x
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (NORM) {
+        __shared__ double s_red[kGemvXWaves];
+        row_norm<XV, 64 * kGemvXWaves>(xv, G.norm, n_in, tid, s_red);
+    }
     const LdsAct L{s_codes, s_d, s_s, kGemvXMaxGroups};
     quantize_to_lds<kq, XV, 64 * kGemvXWaves>(xv, n_in, tid, L);
     __syncthreads();
@@ -308,7 +347,11 @@ __global__ __launch_bounds__(64 * kGemvXWaves) void gemv_x_kernel(GemvXGroup G, 
 #pragma unroll
         for (int off = LPR / 2; off > 0; off >>= 1) v += __shfl_xor(v, off);
         const int row = row_base + rb * RPP;
-        if (sub == 0 && row < n_out) y[row] = v;
+        if (sub == 0 && row < n_out) {
+            y[row] = v;
+            // the residual add, FISH's order x + (v + bias) (single-tensor launches)
+            if (G.resid.x) G.resid.x[row] = G.resid.x[row] + (G.resid.bias ? v + G.resid.bias[row] : v);
+        }
     }
 }
 
@@ -326,7 +369,16 @@ hipError_t gemv_x_launch(GemvXGroup G, const float* x, int n_in, hipStream_t s) 
         wgs += ((G.n_out[j] + RPW - 1) / RPW + kGemvXWaves - 1) / kGemvXWaves;
         G.wg_end[j] = wgs;
     }
-    hipLaunchKernelGGL((gemv_x_kernel<T, LPR, MAXC, RB, XV>), dim3(unsigned(wgs)), dim3(TH), 0, s, G, x, n_in);
+    if (G.norm.w) {
+        // rows of up to 4 groups per lane (n_in <= 8192): the prologue spills registers beyond
+        if constexpr (MAXC <= 4)
+            hipLaunchKernelGGL((gemv_x_kernel<T, LPR, MAXC, RB, XV, true>), dim3(unsigned(wgs)), dim3(TH), 0, s, G,
+                               x, n_in);
+        else
+            return hipErrorInvalidValue;
+    } else
+        hipLaunchKernelGGL((gemv_x_kernel<T, LPR, MAXC, RB, XV, false>), dim3(unsigned(wgs)), dim3(TH), 0, s, G, x,
+                           n_in);
     return hipGetLastError();
 }
 
@@ -417,10 +469,14 @@ bool gemv_x_supported(const WeightLayout& L) {
 }
 
 hipError_t launch_gemv_x(int n, const void* const* ws, const WeightLayout* WLs, const float* x, float* const* ys,
-                         hipStream_t s) {
+                         hipStream_t s, const RowNorm* norm, const RowResid* resid) {
     if (n <= 0 || n > kGemmGroupMax || !gemv_x_supported(WLs[0])) return hipErrorInvalidValue;
+    if ((norm && (!norm->w || WLs[0].n_in % 4)) || (resid && (!resid->x || n != 1 || resid->x == x)))
+        return hipErrorInvalidValue;
     GemvXGroup G{};
     G.n = n;
+    if (norm) G.norm = *norm;
+    if (resid) G.resid = *resid;
     for (int j = 0; j < n; ++j) {
         if (!WLs[j].total || WLs[j].type != WLs[0].type || WLs[j].n_in != WLs[0].n_in) return hipErrorInvalidValue;
         G.w[j] = weight_ptrs(ws[j], WLs[j]);

@@ -117,8 +117,24 @@ hipError_t launch_gemv(const void* w, const WeightLayout& L, const void* act, in
 // tensors of one type and n_in on the same x in one launch; y_i [n_out_i].
 constexpr int kGemvXMaxGroups = 512;  // n_in <= 16384
 bool gemv_x_supported(const WeightLayout& L);
+// Optional prologue of launch_gemv_x (a layer's RMS norm in front of its
+// projections, model.cpp:1654-1660 and 1770-1776), for n_in <= 8192: the GEMV
+// input is rmsnorm(x) * w over the row, computed by every workgroup;
+// workgroup 0 also writes it to xn_out.
+struct RowNorm {
+    const float* w;
+    float* xn_out;
+    float eps;
+};
+// Optional epilogue (a residual add after a projection, model.cpp:1749-1756
+// and 1795-1800), single-tensor launches only: besides y[i] = v, x[i] =
+// x[i] + (v + bias[i]) (bias may be null), by the lane that owns row i.
+struct RowResid {
+    float* x;
+    const float* bias;
+};
 hipError_t launch_gemv_x(int n, const void* const* ws, const WeightLayout* WLs, const float* x, float* const* ys,
-                         hipStream_t stream);
+                         hipStream_t stream, const RowNorm* norm = nullptr, const RowResid* resid = nullptr);
 
 // Few-token matmul on int8 MFMA (16x16 tiles), same token mapping as
 // launch_gemv; work-list items of up to kBatchItemTokens tokens. Needs

@@ -12,6 +12,15 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs a gfx950 GPU (runs on the MI355X box)")
 
 
+def pytest_collection_modifyitems(config, items):
+    # torch's HIP runtime first: libfish_hip.so (loaded by ctypes) and torch must share one
+    # runtime, and it is the first one loaded that the process keeps, whatever order the
+    # selected tests run in
+    if any(item.get_closest_marker("gpu") for item in items):
+        import torch
+        torch.cuda.is_available()
+
+
 @pytest.fixture(scope="session")
 def oracle():
     from oracle.oracle import Oracle
