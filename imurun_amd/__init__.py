@@ -379,13 +379,15 @@ def silu_mul_quantize(g, u, stream=None):
 # ------------------------------------------------------------------ backend (host buffers)
 
 SPAN_VECS = ("q_norm", "k_norm", "bias_q", "bias_k", "bias_v", "bias_o")
+SPAN_VECS2 = ("bias_qkv", "post_attn_norm", "post_ffn_norm")  # after the wqkv key
 
 
 class SpanLayer(ctypes.Structure):
     """fish_hip_span_layer (include/fish_hip.h)."""
     _fields_ = [(n, ctypes.c_void_p) for n in ("wq", "wk", "wv", "wo", "wg", "wu", "wd")] + \
                [("attn_norm", ctypes.c_void_p), ("ffn_norm", ctypes.c_void_p)] + \
-               [(n, ctypes.c_void_p) for n in SPAN_VECS]
+               [(n, ctypes.c_void_p) for n in SPAN_VECS] + [("wqkv", ctypes.c_void_p)] + \
+               [(n, ctypes.c_void_p) for n in SPAN_VECS2] + [("sliding_window", ctypes.c_int)]
 
 
 class SpanParams(ctypes.Structure):
@@ -394,7 +396,8 @@ class SpanParams(ctypes.Structure):
                 ("n_head_kv", ctypes.c_int), ("head_dim", ctypes.c_int), ("n_ff", ctypes.c_int),
                 ("n_ctx", ctypes.c_int), ("eps", ctypes.c_float), ("attn_scale", ctypes.c_float),
                 ("rope_cos", ctypes.c_void_p), ("rope_sin", ctypes.c_void_p), ("rot_dim", ctypes.c_int),
-                ("rope_neox", ctypes.c_int), ("layers", ctypes.c_void_p), ("kv_q8", ctypes.c_int)]
+                ("rope_neox", ctypes.c_int), ("layers", ctypes.c_void_p), ("kv_q8", ctypes.c_int),
+                ("attn_softcap", ctypes.c_float), ("window", ctypes.c_int), ("gelu", ctypes.c_int)]
 
 
 class HipBackend:
@@ -460,34 +463,37 @@ class HipBackend:
         return y if ok else None
 
     def span_prepare(self, layers, n_embd, n_head, n_head_kv, head_dim, n_ff, n_ctx, rope_cos, rope_sin,
-                     rope_neox=False, eps=1e-5, attn_scale=0.0, kv_q8=False) -> bool:
+                     rope_neox=False, eps=1e-5, attn_scale=0.0, kv_q8=False, attn_softcap=0.0, window=0,
+                     gelu=False) -> bool:
         """ComputeBackend::span_prepare over uploaded tensors: layers = [(names of
         wq, wk, wv, wo, wg, wu, wd), attn_norm, ffn_norm] or [(names, attn_norm, ffn_norm,
-        extras)] with extras a dict of the optional SPAN_VECS (Qwen-3 q/k norms, biases);
-        RoPE tables [n_ctx][rot_dim / 2]."""
+        extras)] with extras a dict of the optional SPAN_VECS / SPAN_VECS2 vectors (Qwen-3 q/k
+        norms, biases, Gemma-2 post norms), "wqkv" (the fused q|k|v tensor's name, with wq, wk,
+        wv None) and "sliding_window"; a None wg makes wu the fused gate|up. RoPE tables
+        [n_ctx][rot_dim / 2]."""
         arr = (SpanLayer * len(layers))()
         keep = []
+
+        def vec(v):
+            if v is None:
+                return None
+            v = np.ascontiguousarray(v, np.float32)
+            keep.append(v)
+            return v.ctypes.data
+
         for i, layer in enumerate(layers):
             names, an, fn = layer[:3]
             extras = layer[3] if len(layer) > 3 else {}
-            an = np.ascontiguousarray(an, np.float32)
-            fn = np.ascontiguousarray(fn, np.float32)
-            keep += [an, fn]
-            vecs = []
-            for n in SPAN_VECS:
-                v = extras.get(n)
-                if v is None:
-                    vecs.append(None)
-                else:
-                    v = np.ascontiguousarray(v, np.float32)
-                    keep.append(v)
-                    vecs.append(v.ctypes.data)
-            arr[i] = SpanLayer(*[self._key(n).value for n in names], an.ctypes.data, fn.ctypes.data, *vecs)
+            keys = [self._key(n).value if n is not None else None for n in names]
+            wqkv = self._key(extras["wqkv"]).value if extras.get("wqkv") else None
+            arr[i] = SpanLayer(*keys, vec(an), vec(fn), *[vec(extras.get(n)) for n in SPAN_VECS], wqkv,
+                               *[vec(extras.get(n)) for n in SPAN_VECS2], 1 if extras.get("sliding_window") else 0)
         rc = np.ascontiguousarray(rope_cos, np.float32)
         rs = np.ascontiguousarray(rope_sin, np.float32)
         p = SpanParams(len(layers), n_embd, n_head, n_head_kv, head_dim, n_ff, n_ctx, eps, attn_scale,
                        rc.ctypes.data, rs.ctypes.data, 2 * rc.shape[1], 1 if rope_neox else 0,
-                       ctypes.cast(arr, ctypes.c_void_p), 1 if kv_q8 else 0)
+                       ctypes.cast(arr, ctypes.c_void_p), 1 if kv_q8 else 0, attn_softcap, window,
+                       1 if gelu else 0)
         return bool(self.L.fish_hip_span_prepare(ctypes.byref(p)))
 
     def span_kv_truncate(self, n_past: int) -> None:

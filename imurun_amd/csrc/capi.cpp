@@ -418,31 +418,49 @@ public:
             return false;
         if (p.kv_q8) return false;  // int8 KV cache: not kept here, FISH keeps per-matmul routing
         const int E = p.n_embd, Q = p.n_head * p.head_dim, KV = p.n_head_kv * p.head_dim, F = p.n_ff;
-        // every weight resident, unsplit, with the shapes of a dense layer
+        if (p.attn_softcap < 0.0f || p.window < 0) return false;
+        // every weight resident, unsplit, with the shapes of a dense layer; a fused q|k|v
+        // (wq, wk, wv null) or a fused gate|up (wg null) in the first and sixth slot
+        span_fused_qkv_.assign(size_t(p.n_layers), 0);
+        span_fused_gu_.assign(size_t(p.n_layers), 0);
+        span_window_.assign(size_t(p.n_layers), 0);
+        span_any_fused_ = false;
         for (int l = 0; l < p.n_layers; ++l) {
             const fish_hip_span_layer& L = p.layers[l];
-            const void* keys[7] = {L.wq, L.wk, L.wv, L.wo, L.wg, L.wu, L.wd};
-            const int n_in[7] = {E, E, E, Q, E, E, F}, n_out[7] = {Q, KV, KV, E, F, F, E};
+            const bool fq = L.wqkv != nullptr, fg = L.wg == nullptr;
+            if ((fq && (L.wq || L.wk || L.wv || L.bias_q || L.bias_k || L.bias_v)) || (!fq && L.bias_qkv) ||
+                !L.attn_norm || !L.ffn_norm || (!L.q_norm) != (!L.k_norm) || (L.sliding_window && p.window <= 0)) {
+                span_keys_.clear();
+                return false;
+            }
+            const void* keys[7] = {fq ? L.wqkv : L.wq, L.wk, L.wv, L.wo, L.wg, L.wu, L.wd};
+            const int n_in[7] = {E, E, E, Q, E, E, F};
+            const int n_out[7] = {fq ? Q + 2 * KV : Q, KV, KV, E, F, fg ? 2 * F : F, E};
             for (int i = 0; i < 7; ++i) {
+                if ((fq && (i == 1 || i == 2)) || (fg && i == 4)) {  // absent in the fused form
+                    span_keys_.push_back(nullptr);
+                    continue;
+                }
                 auto it = map_.find(keys[i]);
-                if (it == map_.end() || it->second.n_expert != 1 || it->second.layout.n_in != n_in[i] ||
+                if (!keys[i] || it == map_.end() || it->second.n_expert != 1 || it->second.layout.n_in != n_in[i] ||
                     it->second.layout.n_out != n_out[i]) {
                     span_keys_.clear();
                     return false;
                 }
                 span_keys_.push_back(keys[i]);
             }
-            if (!L.attn_norm || !L.ffn_norm || (!L.q_norm) != (!L.k_norm)) {
-                span_keys_.clear();
-                return false;
-            }
+            span_fused_qkv_[size_t(l)] = fq;
+            span_fused_gu_[size_t(l)] = fg;
+            span_window_[size_t(l)] = L.sliding_window != 0;
+            span_any_fused_ = span_any_fused_ || fq || fg;
         }
         sp_ = p;
         sp_.layers = nullptr;
-        // per-layer vectors: attn_norm, ffn_norm, q_norm, k_norm, bias_q, bias_k, bias_v, bias_o
+        // per-layer vectors: attn_norm, ffn_norm, q_norm, k_norm, bias_q, bias_k, bias_v, bias_o,
+        // post_attn_norm, post_ffn_norm (a fused bias_qkv is kept as its three parts)
         const int D = p.head_dim;
         const size_t vlen[kSpanVecs] = {size_t(E), size_t(E), size_t(D), size_t(D), size_t(Q), size_t(KV), size_t(KV),
-                                        size_t(E)};
+                                        size_t(E), size_t(E), size_t(E)};
         size_t voff[kSpanVecs], per_layer = 0;
         for (int i = 0; i < kSpanVecs; ++i) {
             voff[i] = per_layer;
@@ -477,8 +495,11 @@ public:
         hipError_t e = hipSuccess;
         for (int l = 0; l < p.n_layers && e == hipSuccess; ++l) {
             const fish_hip_span_layer& L = p.layers[l];
-            const float* src[kSpanVecs] = {L.attn_norm, L.ffn_norm, L.q_norm, L.k_norm,
-                                           L.bias_q,    L.bias_k,   L.bias_v, L.bias_o};
+            const float* bq = L.bias_qkv ? L.bias_qkv : L.bias_q;
+            const float* bk = L.bias_qkv ? L.bias_qkv + Q : L.bias_k;
+            const float* bv = L.bias_qkv ? L.bias_qkv + Q + KV : L.bias_v;
+            const float* src[kSpanVecs] = {L.attn_norm, L.ffn_norm, L.q_norm, L.k_norm,         bq,
+                                           bk,          bv,         L.bias_o, L.post_attn_norm, L.post_ffn_norm};
             for (int i = 0; i < kSpanVecs && e == hipSuccess; ++i) {
                 if (!src[i]) continue;
                 const size_t at = size_t(l) * per_layer + voff[i];
@@ -507,8 +528,9 @@ public:
         std::lock_guard<std::mutex> lk(mu_);
         if (!span_on_ || broken_ || !x || n_tok <= 0 || pos0 < 0 || pos0 + n_tok > sp_.n_ctx) return false;
         const size_t E = size_t(sp_.n_embd);
-        std::vector<const Resident*> rs(span_keys_.size());
+        std::vector<const Resident*> rs(span_keys_.size(), nullptr);
         for (size_t i = 0; i < rs.size(); ++i) {
+            if (!span_keys_[i]) continue;  // a fused layer's absent slot
             auto it = map_.find(span_keys_[i]);
             if (it == map_.end()) return false;
             rs[i] = &it->second;
@@ -582,17 +604,19 @@ public:
 
 private:
     static constexpr int kSpanChunk = 256;  // FISH's largest forward batch (model.h:292)
-    static constexpr int kSpanVecs = 8;     // per-layer vectors kept on the device
+    static constexpr int kSpanVecs = 10;    // per-layer vectors kept on the device
 
     // Device scratch of one span call, each buffer 256-byte aligned, in this
     // order (the fish_hip_span_inspect part ids): x, xb (attention norm out),
     // q, k, v (projections), qr (q after bias, norm and RoPE), att, proj (o
     // projection), xb2 (FFN norm out), g (silu(g) * u after the FFN), u, dn
-    // (down projection), attention partials (positions < ld); then the position.
-    static constexpr int kSpanBufs = 13;
+    // (down projection), fz (a fused projection's output before its split;
+    // empty when no layer is fused), attention partials (positions < ld); then
+    // the position.
+    static constexpr int kSpanBufs = 14;
     static constexpr int kSpanParts = 12;  // inspectable: x .. dn
     struct SpanBufs {
-        float *x, *xb, *q, *k, *v, *qr, *att, *proj, *xb2, *g, *u, *dn, *sc;
+        float *x, *xb, *q, *k, *v, *qr, *att, *proj, *xb2, *g, *u, *dn, *fz, *sc;
         int* pos;
         int ld;
     };
@@ -601,8 +625,9 @@ private:
                      KV = size_t(sp_.n_head_kv) * sp_.head_dim, F = size_t(sp_.n_ff);
         // partials for the largest call that splits attention (at most kAttnSplitTok tokens)
         const size_t part = attention_scratch_floats(std::min(n_tok, kAttnSplitTok), sp_.n_head, sp_.head_dim, ld);
+        const size_t fz = span_any_fused_ ? T * std::max(Q + 2 * KV, 2 * F) : 0;
         const size_t v[kSpanBufs] = {T * E, T * E, T * Q, T * KV, T * KV, T * Q, T * Q,
-                                     T * E, T * E, T * F, T * F, T * E, part};
+                                     T * E, T * E, T * F, T * F, T * E, fz, part};
         for (int i = 0; i < kSpanBufs; ++i) {
             cnt[i] = v[i];
             z[i] = (v[i] * 4 + 255) / 256 * 256;
@@ -623,8 +648,8 @@ private:
             p[i] = reinterpret_cast<float*>(b);
             b += z[i];
         }
-        return SpanBufs{p[0], p[1], p[2],  p[3],  p[4],  p[5], p[6],
-                        p[7], p[8], p[9], p[10], p[11], p[12], reinterpret_cast<int*>(b), ld};
+        return SpanBufs{p[0], p[1], p[2],  p[3],  p[4],  p[5],  p[6], p[7],
+                        p[8], p[9], p[10], p[11], p[12], p[13], reinterpret_cast<int*>(b), ld};
     }
     // device copy of per-layer vector i of layer l, or nullptr when the layer has none
     const float* span_vec(int l, int i) const {
@@ -648,15 +673,21 @@ private:
             _Float16* kc = d_kc_ + size_t(l) * sp_.n_ctx * KV;
             _Float16* vc = d_vc_ + size_t(l) * sp_.n_ctx * KV;
             const SpanVecs vecs{span_vec(l, 2), span_vec(l, 3), span_vec(l, 4), span_vec(l, 5), span_vec(l, 6)};
-            const int n_qkv[3] = {Q, KV, KV}, n_e[1] = {E}, n_f[2] = {F, F};
+            const bool fq = span_fused_qkv_[size_t(l)] != 0, fg = span_fused_gu_[size_t(l)] != 0;
+            const float* post_a = span_vec(l, 8);
+            const float* post_f = span_vec(l, 9);
+            const int window = span_window_[size_t(l)] ? sp_.window : 0;
+            const int n_qkv[3] = {Q, KV, KV}, n_e[1] = {E}, n_f[2] = {F, F}, n_fq[1] = {Q + 2 * KV}, n_fg[1] = {2 * F};
             float* y_qkv[3] = {B.q, B.k, B.v};
             float* y_o[1] = {B.proj};
             float* y_gu[2] = {B.g, B.u};
             float* y_d[1] = {B.dn};
+            float* y_fz[1] = {B.fz};
             // one token: each norm is the prologue of its projections' fused launch and each
             // residual add the epilogue of the projection it follows, so x is rewritten only
             // by the o and down launches, row by row, and no other launch runs for them
-            const bool fold = n_tok == 1 && E <= 8192 && foldable(W, 7);
+            // (layers with a fused projection or a post norm take the general sequence)
+            const bool fold = n_tok == 1 && E <= 8192 && !fq && !fg && !post_a && !post_f && foldable(W, 7);
             if (fold && pending) {
                 e = launch_add(B.x, pending, T * E, stream_);
                 pending = nullptr;
@@ -666,29 +697,51 @@ private:
                 e = run_group(W, 3, B.x, n_tok, E, n_qkv, y_qkv, act, &an);
             } else if (e == hipSuccess) {
                 e = launch_rmsnorm(B.x, pending, nullptr, span_vec(l, 0), B.xb, n_tok, E, sp_.eps, stream_);
-                if (e == hipSuccess) e = run_group(W, 3, B.xb, n_tok, E, n_qkv, y_qkv, act);
+                if (e == hipSuccess && fq) {
+                    // fused q|k|v (model.cpp:1665-1674): one matmul, then its columns split
+                    e = run_group(W, 1, B.xb, n_tok, E, n_fq, y_fz, act);
+                    if (e == hipSuccess) e = launch_split_rows(B.fz, n_tok, B.q, Q, B.k, KV, B.v, KV, stream_);
+                } else if (e == hipSuccess) {
+                    e = run_group(W, 3, B.xb, n_tok, E, n_qkv, y_qkv, act);
+                }
             }
             if (e == hipSuccess)
                 e = launch_qkv_prep(B.q, B.k, B.v, vecs, B.qr, kc, vc, n_tok, H, HKV, D, sp_.rot_dim,
                                     sp_.rope_neox != 0, sp_.eps, pos0, d_cos_, d_sin_, stream_, pos_dev);
             if (e == hipSuccess)
-                e = launch_attention(B.qr, kc, vc, B.att, B.sc, B.ld, n_tok, H, HKV, D, pos0, scale, stream_, pos_dev);
+                e = launch_attention(B.qr, kc, vc, B.att, B.sc, B.ld, n_tok, H, HKV, D, pos0, scale, stream_, pos_dev,
+                                     sp_.attn_softcap, window);
             if (e == hipSuccess && fold) {
                 const RowResid ro{B.x, span_vec(l, 7)};
                 const RowNorm fn{span_vec(l, 1), B.xb2, sp_.eps};
                 e = run_group(W + 3, 1, B.att, n_tok, Q, n_e, y_o, act, nullptr, &ro);
                 if (e == hipSuccess) e = run_group(W + 4, 2, B.x, n_tok, E, n_f, y_gu, act, &fn);
-                if (e == hipSuccess) e = launch_silu_mul(B.g, B.u, T * F, stream_);
+                if (e == hipSuccess) e = launch_silu_mul(B.g, B.u, T * F, stream_, sp_.gelu != 0);
                 const RowResid rd{B.x, nullptr};
                 if (e == hipSuccess) e = run_group(W + 6, 1, B.g, n_tok, F, n_e, y_d, act, nullptr, &rd);
                 continue;
             }
             if (e == hipSuccess) e = run_group(W + 3, 1, B.att, n_tok, Q, n_e, y_o, act);
-            if (e == hipSuccess)
+            if (e == hipSuccess && post_a) {
+                // Gemma-2: proj = rmsnorm(proj + bias_o) before the residual add (model.cpp:1756-1760)
+                e = launch_rmsnorm(B.proj, nullptr, span_vec(l, 7), post_a, B.proj, n_tok, E, sp_.eps, stream_);
+                if (e == hipSuccess)
+                    e = launch_rmsnorm(B.x, B.proj, nullptr, span_vec(l, 1), B.xb2, n_tok, E, sp_.eps, stream_);
+            } else if (e == hipSuccess) {
                 e = launch_rmsnorm(B.x, B.proj, span_vec(l, 7), span_vec(l, 1), B.xb2, n_tok, E, sp_.eps, stream_);
-            if (e == hipSuccess) e = run_group(W + 4, 2, B.xb2, n_tok, E, n_f, y_gu, act);
-            if (e == hipSuccess) e = launch_silu_mul(B.g, B.u, T * F, stream_);
+            }
+            if (e == hipSuccess && fg) {
+                // fused gate|up, gate rows first (model.cpp:1481-1490)
+                e = run_group(W + 5, 1, B.xb2, n_tok, E, n_fg, y_fz, act);
+                if (e == hipSuccess) e = launch_split_rows(B.fz, n_tok, B.g, F, B.u, F, nullptr, 0, stream_);
+            } else if (e == hipSuccess) {
+                e = run_group(W + 4, 2, B.xb2, n_tok, E, n_f, y_gu, act);
+            }
+            if (e == hipSuccess) e = launch_silu_mul(B.g, B.u, T * F, stream_, sp_.gelu != 0);
             if (e == hipSuccess) e = run_group(W + 6, 1, B.g, n_tok, F, n_e, y_d, act);
+            // Gemma-2: the FFN output normed before the residual add (model.cpp:1791-1793)
+            if (e == hipSuccess && post_f)
+                e = launch_rmsnorm(B.dn, nullptr, nullptr, post_f, B.dn, n_tok, E, sp_.eps, stream_);
             pending = B.dn;
         }
         if (e == hipSuccess && pending) e = launch_add(B.x, pending, T * E, stream_);
@@ -704,7 +757,7 @@ private:
         hipError_t e = hipSuccess;
         // the graph holds the weights' device addresses: rebuild it if any changed
         std::vector<const void*> devs(rs.size());
-        for (size_t i = 0; i < rs.size(); ++i) devs[i] = rs[i]->dev;
+        for (size_t i = 0; i < rs.size(); ++i) devs[i] = rs[i] ? rs[i]->dev : nullptr;  // null: a fused layer's gap
         if (dec_exec_ && devs != dec_devs_) {
             (void)hipGraphExecDestroy(dec_exec_);
             dec_exec_ = nullptr;
@@ -928,7 +981,9 @@ private:
     // per-layer vectors, RoPE tables, f16 KV cache and every per-call buffer
     bool span_on_ = false;
     fish_hip_span_params sp_{};
-    std::vector<const void*> span_keys_;
+    std::vector<const void*> span_keys_;  // 7 per layer; null: a fused layer's absent slot
+    std::vector<uint8_t> span_fused_qkv_, span_fused_gu_, span_window_;  // per layer
+    bool span_any_fused_ = false;
     std::vector<size_t> span_vec_off_;  // [layer][kSpanVecs] byte offset in d_vecs_, SIZE_MAX = absent
     void* d_span_fixed_ = nullptr;
     float *d_vecs_ = nullptr, *d_cos_ = nullptr, *d_sin_ = nullptr;

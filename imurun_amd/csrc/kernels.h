@@ -189,10 +189,13 @@ hipError_t launch_qkv_prep(const float* q, const float* k, const float* v, const
                            const int* pos_dev = nullptr);
 // `part` holds attention_scratch_floats(n_tok, H, D, ld) floats (0 above kAttnSplitTok tokens).
 size_t attention_scratch_floats(int n_tok, int H, int D, int ld);
+// softcap > 0: scores c tanh(s / c); window > 0: positions pos - window + 1 .. pos only.
 hipError_t launch_attention(const float* q, const _Float16* kc, const _Float16* vc, float* out, float* part, int ld,
                             int n_tok, int H, int HKV, int D, int pos0, float scale, hipStream_t s,
-                            const int* pos_dev = nullptr);
-hipError_t launch_silu_mul(float* g, const float* u, size_t n, hipStream_t s);
+                            const int* pos_dev = nullptr, float softcap = 0.0f, int window = 0);
+hipError_t launch_silu_mul(float* g, const float* u, size_t n, hipStream_t s, bool gelu = false);
+hipError_t launch_split_rows(const float* src, int n_tok, float* d0, int w0, float* d1, int w1, float* d2, int w2,
+                             hipStream_t s);
 hipError_t launch_add(float* x, const float* y, size_t n, hipStream_t s);
 
 // Per-block integer dots of every row with token 0 of `act`.

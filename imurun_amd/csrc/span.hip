@@ -59,7 +59,9 @@ __device__ __forceinline__ float block_reduce_f(float v, float* red, bool is_max
 
 // one workgroup of kNormTh threads per token; with y, first x += y (the
 // residual add, written back to x; with b, y + b is added: the projection's
-// bias, then the residual), then out = rmsnorm(x)
+// bias, then the residual); with b and no y, x += b (a projection's bias
+// before its own norm, model.cpp:1756-1760); then out = rmsnorm(x), which
+// may be x itself
 __global__ __launch_bounds__(kNormTh) void rmsnorm_kernel(float* __restrict__ x, const float* __restrict__ y,
                                                           const float* __restrict__ b, const float* __restrict__ w,
                                                           float* __restrict__ out, int n, float eps) {
@@ -73,6 +75,9 @@ __global__ __launch_bounds__(kNormTh) void rmsnorm_kernel(float* __restrict__ x,
         float v = xr[i];
         if (yr) {
             v = v + (b ? yr[i] + b[i] : yr[i]);
+            xr[i] = v;
+        } else if (b) {
+            v = v + b[i];
             xr[i] = v;
         }
         s += double(v) * double(v);
@@ -158,7 +163,8 @@ __global__ __launch_bounds__(kTh) void qkv_prep_kernel(const float* __restrict__
 //     score m, its sum l of exp(s - m), and o = sum exp(s - m) v.
 //   attn_combine_kernel: one workgroup per (token, head): M = max m,
 //     L = sum l exp(m - M), out = (sum o exp(m - M)) * (1 / L).
-// Chunks that start past the token's position hold m = -inf, l = 0, o = 0.
+// Chunks that start past the token's position, or end before a sliding window's
+// first position, hold m = -inf, l = 0, o = 0.
 // Mathematically FISH's single-pass softmax (ops.cpp:331-350); the rounding
 // order differs. Needs D <= 256.
 constexpr int kCh = 64;
@@ -172,11 +178,19 @@ __device__ __forceinline__ float2 f16x2(uint32_t u) {
     return make_float2(float(h.x), float(h.y));
 }
 
+// A position's score: dot * scale, then Gemma-2's soft cap c tanh(s / c) when c > 0
+// (ops.cpp:334-335)
+__device__ __forceinline__ float score(float dot, float scale, float softcap) {
+    const float s = dot * scale;
+    return softcap > 0.0f ? softcap * tanhf(s / softcap) : s;
+}
+
 template <int NP>
 __global__ __launch_bounds__(kTh) void attn_part_kernel(const float* __restrict__ q, const _Float16* __restrict__ kc,
                                                         const _Float16* __restrict__ vc, float* __restrict__ part,
                                                         int S, int H, int HKV, int D, int pos0,
-                                                        const int* __restrict__ pos_dev, float scale) {
+                                                        const int* __restrict__ pos_dev, float scale, float softcap,
+                                                        int window) {
     constexpr int PB = kCh / 4;
     __shared__ float s_e[kCh];
     __shared__ float s_o[4][128 * NP];
@@ -186,8 +200,10 @@ __global__ __launch_bounds__(kTh) void attn_part_kernel(const float* __restrict_
     const int pos = pos0 + t, kvh = h / (H / HKV), KV = HKV * D, Q = H * D;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int j0 = chunk * kCh;
+    // a sliding window attends over positions jlo..pos (ops.cpp:327-328)
+    const int jlo = window > 0 ? max(0, pos - window + 1) : 0;
     float* pp = part + (size_t(item) * S + chunk) * size_t(D + 2);
-    if (j0 > pos) {  // uniform over the workgroup
+    if (j0 > pos || j0 + kCh <= jlo) {  // uniform over the workgroup
         for (int d = tid; d < D; d += kTh) pp[d] = 0.0f;
         if (tid == 0) {
             pp[D] = -INFINITY;
@@ -225,14 +241,17 @@ __global__ __launch_bounds__(kTh) void attn_part_kernel(const float* __restrict_
         }
 #pragma unroll
         for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
-        if (lane == 0) s_e[w + 4 * b] = j0 + w + 4 * b <= jn ? sum * scale : -INFINITY;
+        if (lane == 0) {
+            const int j = j0 + w + 4 * b;
+            s_e[w + 4 * b] = (j <= jn && j >= jlo) ? score(sum, scale, softcap) : -INFINITY;
+        }
     }
     __syncthreads();
     if (w == 0) {
         float m = s_e[lane];
 #pragma unroll
         for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-        const float e = lane <= jn - j0 ? expf(s_e[lane] - m) : 0.0f;
+        const float e = (lane <= jn - j0 && j0 + lane >= jlo) ? expf(s_e[lane] - m) : 0.0f;
         float l = e;
 #pragma unroll
         for (int off = 32; off > 0; off >>= 1) l += __shfl_xor(l, off);
@@ -315,7 +334,8 @@ template <int NP>
 __global__ __launch_bounds__(kTh) void attn_full_kernel(const float* __restrict__ q, const _Float16* __restrict__ kc,
                                                         const _Float16* __restrict__ vc, float* __restrict__ out,
                                                         int H, int HKV, int D, int pos0,
-                                                        const int* __restrict__ pos_dev, float scale) {
+                                                        const int* __restrict__ pos_dev, float scale, float softcap,
+                                                        int window) {
     constexpr int PB = kCh / 4;
     __shared__ float s_e[kCh];
     __shared__ float s_o[4][128 * NP];
@@ -323,6 +343,7 @@ __global__ __launch_bounds__(kTh) void attn_full_kernel(const float* __restrict_
     if (pos_dev) pos0 = *pos_dev;
     const int item = blockIdx.x, t = item / H, h = item % H;
     const int pos = pos0 + t, kvh = h / (H / HKV), KV = HKV * D, Q = H * D;
+    const int jlo = window > 0 ? max(0, pos - window + 1) : 0;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     float2 qv[NP];
 #pragma unroll
@@ -334,7 +355,7 @@ __global__ __launch_bounds__(kTh) void attn_full_kernel(const float* __restrict_
     const uint32_t* vb = reinterpret_cast<const uint32_t*>(vc + size_t(kvh) * D);
     const int KV2 = KV / 2;
     float o_run = 0.0f, m_run = -INFINITY, l_run = 0.0f;
-    for (int j0 = 0; j0 <= pos; j0 += kCh) {
+    for (int j0 = jlo / kCh * kCh; j0 <= pos; j0 += kCh) {
         const int jn = min(pos, j0 + kCh - 1);
         uint32_t kv[PB][NP];
 #pragma unroll
@@ -362,14 +383,17 @@ __global__ __launch_bounds__(kTh) void attn_full_kernel(const float* __restrict_
             }
 #pragma unroll
             for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
-            if (lane == 0) s_e[w + 4 * b] = j0 + w + 4 * b <= jn ? sum * scale : -INFINITY;
+            if (lane == 0) {
+                const int j = j0 + w + 4 * b;
+                s_e[w + 4 * b] = (j <= jn && j >= jlo) ? score(sum, scale, softcap) : -INFINITY;
+            }
         }
         __syncthreads();
         if (w == 0) {
             float m = s_e[lane];
 #pragma unroll
             for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-            const float e = lane <= jn - j0 ? expf(s_e[lane] - m) : 0.0f;
+            const float e = (lane <= jn - j0 && j0 + lane >= jlo) ? expf(s_e[lane] - m) : 0.0f;
             float l = e;
 #pragma unroll
             for (int off = 32; off > 0; off >>= 1) l += __shfl_xor(l, off);
@@ -411,12 +435,37 @@ __global__ __launch_bounds__(kTh) void attn_full_kernel(const float* __restrict_
 }
 
 // g = silu(g) * u
-__global__ __launch_bounds__(kTh) void silu_mul_kernel(float* __restrict__ g, const float* __restrict__ u, size_t n) {
+// g = act(g) * u: SiLU v / (1 + exp(-v)) (silu_inplace, ops.cpp:25-30), or with
+// gelu FISH's tanh GELU 0.5 v (1 + tanh(sqrt(2/pi) (v + 0.044715 v^3)))
+// (gelu_inplace, ops.cpp:32-38), each step rounded as there (no contraction)
+__global__ __launch_bounds__(kTh) void act_mul_kernel(float* __restrict__ g, const float* __restrict__ u, size_t n,
+                                                      int gelu) {
     const size_t i = size_t(blockIdx.x) * kTh + threadIdx.x;
     if (i >= n) return;
     const float v = g[i];
-    const float a = v / (1.0f + expf(-v));
+    float a;
+    if (gelu) {
+        const float k = 0.7978845608028654f;
+        a = 0.5f * v * (1.0f + tanhf(k * (v + 0.044715f * v * v * v)));
+    } else {
+        a = v / (1.0f + expf(-v));
+    }
     g[i] = a * u[i];
+}
+
+// Row t of src [n_tok][w0 + w1 + w2] split into d0 [n_tok][w0], d1, d2 (a fused
+// projection's output, model.cpp:1666-1673 and 1481-1490); w2 may be 0.
+__global__ __launch_bounds__(kTh) void split_rows_kernel(const float* __restrict__ src, float* __restrict__ d0,
+                                                         float* __restrict__ d1, float* __restrict__ d2, int w0,
+                                                         int w1, int w2) {
+    const int t = blockIdx.y, W = w0 + w1 + w2;
+    const float* r = src + size_t(t) * W;
+    for (int i = int(blockIdx.x) * kTh + threadIdx.x; i < W; i += int(gridDim.x) * kTh) {
+        const float v = r[i];
+        if (i < w0) d0[size_t(t) * w0 + i] = v;
+        else if (i < w0 + w1) d1[size_t(t) * w1 + (i - w0)] = v;
+        else d2[size_t(t) * w2 + (i - w0 - w1)] = v;
+    }
 }
 
 // x += y
@@ -449,23 +498,27 @@ hipError_t launch_qkv_prep(const float* q, const float* k, const float* v, const
 
 hipError_t launch_attention(const float* q, const _Float16* kc, const _Float16* vc, float* out, float* part, int ld,
                             int n_tok, int H, int HKV, int D, int pos0, float scale, hipStream_t s,
-                            const int* pos_dev) {
+                            const int* pos_dev, float softcap, int window) {
     if (n_tok <= 0 || D <= 0 || D > kTh || D % 2 || HKV <= 0 || H % HKV || ld < pos0 + n_tok) return hipErrorInvalidValue;
     const dim3 block(kTh);
     if (n_tok > kAttnSplitTok) {
         const dim3 grid(unsigned(n_tok * H));
         if (D <= 128)
-            hipLaunchKernelGGL(attn_full_kernel<1>, grid, block, 0, s, q, kc, vc, out, H, HKV, D, pos0, pos_dev, scale);
+            hipLaunchKernelGGL(attn_full_kernel<1>, grid, block, 0, s, q, kc, vc, out, H, HKV, D, pos0, pos_dev, scale,
+                               softcap, window);
         else
-            hipLaunchKernelGGL(attn_full_kernel<2>, grid, block, 0, s, q, kc, vc, out, H, HKV, D, pos0, pos_dev, scale);
+            hipLaunchKernelGGL(attn_full_kernel<2>, grid, block, 0, s, q, kc, vc, out, H, HKV, D, pos0, pos_dev, scale,
+                               softcap, window);
         return hipGetLastError();
     }
     const int S = (ld + kCh - 1) / kCh;
     const dim3 grid(unsigned(n_tok * H), unsigned(S));
     if (D <= 128)
-        hipLaunchKernelGGL(attn_part_kernel<1>, grid, block, 0, s, q, kc, vc, part, S, H, HKV, D, pos0, pos_dev, scale);
+        hipLaunchKernelGGL(attn_part_kernel<1>, grid, block, 0, s, q, kc, vc, part, S, H, HKV, D, pos0, pos_dev, scale,
+                           softcap, window);
     else
-        hipLaunchKernelGGL(attn_part_kernel<2>, grid, block, 0, s, q, kc, vc, part, S, H, HKV, D, pos0, pos_dev, scale);
+        hipLaunchKernelGGL(attn_part_kernel<2>, grid, block, 0, s, q, kc, vc, part, S, H, HKV, D, pos0, pos_dev, scale,
+                           softcap, window);
     hipLaunchKernelGGL(attn_combine_kernel, dim3(unsigned(n_tok * H)), block, 0, s, part, out, S, H, D);
     return hipGetLastError();
 }
@@ -475,9 +528,18 @@ size_t attention_scratch_floats(int n_tok, int H, int D, int ld) {
     return size_t(n_tok) * H * size_t((ld + kCh - 1) / kCh) * size_t(D + 2);
 }
 
-hipError_t launch_silu_mul(float* g, const float* u, size_t n, hipStream_t s) {
+hipError_t launch_silu_mul(float* g, const float* u, size_t n, hipStream_t s, bool gelu) {
     if (!n) return hipSuccess;
-    hipLaunchKernelGGL(silu_mul_kernel, dim3(blocks_for(n)), dim3(kTh), 0, s, g, u, n);
+    hipLaunchKernelGGL(act_mul_kernel, dim3(blocks_for(n)), dim3(kTh), 0, s, g, u, n, gelu ? 1 : 0);
+    return hipGetLastError();
+}
+
+hipError_t launch_split_rows(const float* src, int n_tok, float* d0, int w0, float* d1, int w1, float* d2, int w2,
+                             hipStream_t s) {
+    if (n_tok <= 0 || w0 <= 0 || w1 <= 0 || w2 < 0 || (w2 > 0 && !d2)) return hipErrorInvalidValue;
+    const int W = w0 + w1 + w2;
+    hipLaunchKernelGGL(split_rows_kernel, dim3(unsigned((W + kTh - 1) / kTh), unsigned(n_tok)), dim3(kTh), 0, s, src,
+                       d0, d1, d2, w0, w1, w2);
     return hipGetLastError();
 }
 

@@ -57,15 +57,34 @@ public:
     // routing per matmul.
     bool span_prepare(const SpanParams& p) override {
         const int n = p.layer_end - p.layer_begin;
-        if (n <= 0 || !p.layers || p.attn_softcap > 0.0f || p.window > 0 || p.gelu || p.kv_q8) return false;
+        if (n <= 0 || !p.layers || p.kv_q8) return false;
         std::vector<fish_hip_span_layer> ls(static_cast<size_t>(n));
         for (int i = 0; i < n; ++i) {
             const SpanLayer& L = p.layers[i];
-            if (L.wqkv || !L.wq || !L.wk || !L.wv || !L.wo || !L.wg || !L.wu || !L.wd || !L.attn_norm ||
-                !L.ffn_norm || L.post_attn_norm || L.post_ffn_norm || L.bias_qkv || L.sliding_window)
-                return false;
-            ls[size_t(i)] = {L.wq,     L.wk,     L.wv,     L.wo,     L.wg,     L.wu,     L.wd,     L.attn_norm,
-                             L.ffn_norm, L.q_norm, L.k_norm, L.bias_q, L.bias_k, L.bias_v, L.bias_o};
+            fish_hip_span_layer& h = ls[size_t(i)];
+            h = fish_hip_span_layer{};
+            h.wq = L.wq;
+            h.wk = L.wk;
+            h.wv = L.wv;
+            h.wo = L.wo;
+            h.wg = L.wg;
+            h.wu = L.wu;
+            h.wd = L.wd;
+            h.attn_norm = L.attn_norm;
+            h.ffn_norm = L.ffn_norm;
+            h.q_norm = L.q_norm;
+            h.k_norm = L.k_norm;
+            h.bias_q = L.bias_q;
+            h.bias_k = L.bias_k;
+            h.bias_v = L.bias_v;
+            h.bias_o = L.bias_o;
+            h.wqkv = L.wqkv;
+            h.bias_qkv = L.bias_qkv;
+            h.post_attn_norm = L.post_attn_norm;
+            h.post_ffn_norm = L.post_ffn_norm;
+            h.sliding_window = L.sliding_window ? 1 : 0;
+            // a fused q|k|v comes with wq / wk / wv unset (model.cpp:1665-1674)
+            if (h.wqkv) h.wq = h.wk = h.wv = nullptr;
         }
         fish_hip_span_params hp{};
         hp.n_layers = n;
@@ -83,6 +102,9 @@ public:
         hp.rope_neox = p.rope_neox ? 1 : 0;
         hp.layers = ls.data();
         hp.kv_q8 = p.kv_q8 ? 1 : 0;
+        hp.attn_softcap = p.attn_softcap;
+        hp.window = p.window;
+        hp.gelu = p.gelu ? 1 : 0;
         return fish_hip_span_prepare(&hp) != 0;
     }
     bool span_forward(float* x, int n_tok, int pos0) override { return fish_hip_span_forward(x, n_tok, pos0) != 0; }

@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define FISH_HIP_ABI_VERSION 2
+#define FISH_HIP_ABI_VERSION 3
 
 #define FISH_HIP_ERR_ARG (-1)     /* bad argument or unsupported type/shape */
 #define FISH_HIP_ERR_DEVICE (-2)  /* HIP runtime error; the backend is disabled */
@@ -247,12 +247,18 @@ FISH_HIP_API int fish_hip_backend_moe_ffn(const void* key_gate, const void* key_
 
 /* ---------------------------------------------------------------- layer spans (host pointers, synchronous) */
 
-/* One dense layer of a span (backend.h:114-134 SpanLayer, the subset this
- * backend runs): the weight keys given to fish_hip_upload (all resident), the
- * two RMS-norm weight vectors [n_embd], and optionally the Qwen-3 per-head
- * q / k RMS-norm weights [head_dim] and the q / k / v / o projection biases
- * ([q_dim], [kv_dim], [kv_dim], [n_embd]); NULL = absent. Vectors are host
- * memory, copied at fish_hip_span_prepare. */
+/* One dense layer of a span (backend.h:114-134 SpanLayer): the weight keys
+ * given to fish_hip_upload (all resident) -- wq, wk, wv, or instead the fused
+ * q|k|v wqkv [q_dim + 2 kv_dim][n_embd] (Phi-3) with wq / wk / wv NULL; wg
+ * and wu, or wg NULL and wu the fused gate|up [2 n_ff][n_embd], gate rows
+ * first (model.cpp:1481-1490) -- the two RMS-norm weight vectors [n_embd],
+ * and optionally the Qwen-3 per-head q / k RMS-norm weights [head_dim], the
+ * q / k / v / o projection biases ([q_dim], [kv_dim], [kv_dim], [n_embd]) or
+ * the fused bias_qkv [q_dim + 2 kv_dim] instead of the first three, and the
+ * Gemma-2 post norms [n_embd] of the attention and FFN outputs
+ * (model.cpp:1758-1760, 1791-1793); NULL = absent. sliding_window: this
+ * layer attends over the last fish_hip_span_params.window positions only.
+ * Vectors are host memory, copied at fish_hip_span_prepare. */
 typedef struct fish_hip_span_layer {
     const void* wq;
     const void* wk;
@@ -269,6 +275,11 @@ typedef struct fish_hip_span_layer {
     const float* bias_k;
     const float* bias_v;
     const float* bias_o;
+    const void* wqkv;
+    const float* bias_qkv;
+    const float* post_attn_norm;
+    const float* post_ffn_norm;
+    int sliding_window;
 } fish_hip_span_layer;
 
 /* backend.h:136-154 SpanParams, same meaning: head_dim <= 256, n_head a
@@ -287,6 +298,12 @@ typedef struct fish_hip_span_params {
     /* SpanParams::kv_q8 (backend.h:150-153): an int8 KV cache requested by
      * FISH's planner; this backend keeps f16 K and V only, so nonzero is refused */
     int kv_q8;
+    /* SpanParams attn_softcap (Gemma-2: scores become c tanh(s / c), 0 = none),
+     * window (positions a sliding-window layer attends over) and gelu (the FFN
+     * activation is FISH's tanh GELU instead of SiLU), backend.h:141-143 */
+    float attn_softcap;
+    int window;
+    int gelu;
 } fish_hip_span_params;
 
 /* ComputeBackend::span_prepare (backend.h:156): keeps the layers' weights,

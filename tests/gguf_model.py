@@ -104,13 +104,18 @@ def tiny_llama(path: str, types: dict, seed: int = 7, n_layers: int = 2, n_embd:
 
 def tiny_model(path: str, types: dict, arch: str = "llama", seed: int = 7, n_layers: int = 2, n_embd: int = 256,
                n_ff: int = 768, n_head: int = 4, n_head_kv: int = 2, n_ctx: int = 512, raw=None,
-               head_dim: int = 0, qk_norm: bool = False, biases: bool = False) -> dict:
+               head_dim: int = 0, qk_norm: bool = False, biases: bool = False, fused_qkv: bool = False,
+               fused_gate_up: bool = False, post_norms: bool = False, extra_meta=()) -> dict:
     """tiny_llama for the llama-family architectures FISH loads (model.cpp:116-118):
     `arch` names the metadata keys ("qwen3" and "qwen2" get NeoX RoPE from FISH);
     head_dim != 0 writes attention.key_length / value_length, so n_head * head_dim
     may differ from n_embd (as in Qwen-3); qk_norm adds the per-head attn_q_norm /
     attn_k_norm vectors (model.cpp:335-341); biases adds attn_q / attn_k / attn_v
-    biases (model.cpp:344-346)."""
+    biases (model.cpp:344-346); fused_qkv writes one attn_qkv [q|k|v] tensor and
+    fused_gate_up one ffn_up of 2 n_ff rows, gate first, with no ffn_gate (Phi-3,
+    model.cpp:253, 1481-1490), both in the q / gate type; post_norms adds Gemma-2's
+    post_attention_norm / post_ffw_norm (model.cpp:322-326); extra_meta appends
+    (key under the arch, type, value) entries."""
     import imurun_amd as fh
 
     rng = np.random.default_rng(seed)
@@ -144,14 +149,23 @@ def tiny_model(path: str, types: dict, arch: str = "llama", seed: int = 7, n_lay
         p = f"blk.{i}."
         tensors += [
             norm(p + "attn_norm.weight"), norm(p + "ffn_norm.weight"),
-            mat(p + "attn_q.weight", types["q"], qd, n_embd),
-            mat(p + "attn_k.weight", types["k"], kv, n_embd),
-            mat(p + "attn_v.weight", types["v"], kv, n_embd),
-            mat(p + "attn_output.weight", types["o"], n_embd, qd),
-            mat(p + "ffn_gate.weight", types["gate"], n_ff, n_embd),
-            mat(p + "ffn_up.weight", types["up"], n_ff, n_embd),
-            mat(p + "ffn_down.weight", types["down"], n_embd, n_ff),
         ]
+        # (drawn in q, k, v, o, gate, up, down order: the seeded models stay the same)
+        if fused_qkv:
+            tensors += [mat(p + "attn_qkv.weight", types["q"], qd + 2 * kv, n_embd)]
+        else:
+            tensors += [mat(p + "attn_q.weight", types["q"], qd, n_embd),
+                        mat(p + "attn_k.weight", types["k"], kv, n_embd),
+                        mat(p + "attn_v.weight", types["v"], kv, n_embd)]
+        tensors += [mat(p + "attn_output.weight", types["o"], n_embd, qd)]
+        if fused_gate_up:
+            tensors += [mat(p + "ffn_up.weight", types["gate"], 2 * n_ff, n_embd)]
+        else:
+            tensors += [mat(p + "ffn_gate.weight", types["gate"], n_ff, n_embd),
+                        mat(p + "ffn_up.weight", types["up"], n_ff, n_embd)]
+        tensors += [mat(p + "ffn_down.weight", types["down"], n_embd, n_ff)]
+        if post_norms:
+            tensors += [norm(p + "post_attention_norm.weight"), norm(p + "post_ffw_norm.weight")]
         if qk_norm:
             tensors += [norm(p + "attn_q_norm.weight", head_dim), norm(p + "attn_k_norm.weight", head_dim)]
         if biases:
@@ -178,6 +192,7 @@ def tiny_model(path: str, types: dict, arch: str = "llama", seed: int = 7, n_lay
     ]
     if head_dim != n_embd // n_head:
         meta += [(a + ".attention.key_length", U32, head_dim), (a + ".attention.value_length", U32, head_dim)]
+    meta += [(a + "." + k, kind, v) for k, kind, v in extra_meta]
     write_gguf(path, meta, tensors)
     return {"n_layers": n_layers, "n_embd": n_embd, "n_ff": n_ff, "n_head": n_head, "n_head_kv": n_head_kv,
             "vocab": vocab, "n_ctx": n_ctx, "head_dim": head_dim}

@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_identity():
     L = fh.load()
-    assert L.fish_hip_abi_version() == 2
+    assert L.fish_hip_abi_version() == 3
     assert L.fish_hip_kernel_name() == b"hip-gfx950"
 
 

@@ -24,7 +24,7 @@ import pytest
 
 import imurun_amd as fh
 
-from gguf_model import tiny_llama, tiny_model
+from gguf_model import F32, U32, tiny_llama, tiny_model
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 FULL_SO = os.path.join(ROOT, "oracle", "_ref", "libfish_full_hip.so")
@@ -189,10 +189,17 @@ def test_model_generates_through_a_layer_span(fish, tmp_path, name):
 
 
 # Qwen-family layers: Qwen-3 (per-head q / k RMSNorm, n_head * head_dim != n_embd) and
-# Qwen-2 (q / k / v biases), both with FISH's NeoX RoPE
+# Qwen-2 (q / k / v biases), both with FISH's NeoX RoPE; Phi-3 (fused q|k|v and fused
+# gate|up); Gemma-2 (post norms, GELU, attention soft cap 5 and a 32-position sliding
+# window on even layers -- the prompt is longer -- plus FISH's embedding scale and final soft
+# cap outside the span)
 QWEN = {
     "qwen3": dict(arch="qwen3", head_dim=128, qk_norm=True),
     "qwen2": dict(arch="qwen2", biases=True),
+    "phi3": dict(arch="phi3", fused_qkv=True, fused_gate_up=True),
+    "gemma2": dict(arch="gemma2", post_norms=True,
+                   extra_meta=(("attn_logit_softcapping", F32, 5.0), ("final_logit_softcapping", F32, 30.0),
+                               ("attention.sliding_window", U32, 32))),
 }
 
 

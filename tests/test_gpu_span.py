@@ -14,7 +14,13 @@ so later calls attend over the cache the earlier ones wrote and every graph
 replay is checked. The KV cache holds f16 K and V, as FISH's own device span
 does (vulkan_backend.cpp:1650); the reference stores them rounded to f16 the
 same way. Layer variants: llama; Qwen-2 projection biases (q/k/v, and o);
-Qwen-3 per-head q/k RMS norms before RoPE (model.cpp:1704-1719, :1749).
+Qwen-3 per-head q/k RMS norms before RoPE (model.cpp:1704-1719, :1749);
+Phi-3 fused q|k|v with its fused bias and fused gate|up, gate rows first
+(model.cpp:1665-1674, 1481-1490; the fused tensors are the separate ones'
+rows concatenated, so the reference keeps them apart); Gemma-2 post norms of
+the attention and FFN outputs (model.cpp:1758-1760, 1791-1793), attention
+logits soft-capped c tanh(s / c) and a sliding window (ops.cpp:327-335), and
+FISH's tanh GELU in the FFN (ops.cpp:32-38).
 
 Bars, per call, on the device's own intermediate values of that call
 (fish_hip_span_inspect), each stage against the reference applied to the
@@ -54,15 +60,35 @@ def rope_tables(rot_dim, ctx=CTX):
 
 
 class RefLayer:
-    def __init__(self, oracle, packed, an, fn, cos, sin, neox=True, extras=None):
+    def __init__(self, oracle, packed, an, fn, cos, sin, neox=True, extras=None, types=None, opts=None):
         self.o, self.w, self.an, self.fn, self.cos, self.sin = oracle, packed, an, fn, cos, sin
         self.neox = neox
         self.x = extras or {}
+        self.types = types or TYPES
+        self.opts = opts or {}
         self.kc = np.zeros((cos.shape[0], KV), np.float32)
         self.vc = np.zeros((cos.shape[0], KV), np.float32)
 
     def mm(self, name, x):
-        return self.o.matmul_f32(TYPES[name], self.w[name], x, SHAPES[name][0])
+        return self.o.matmul_f32(self.types[name], self.w[name], x, SHAPES[name][0])
+
+    def act(self, g, u):
+        """silu(g) * u, or FISH's tanh GELU (ops.cpp:32-38) when the variant has it."""
+        if self.opts.get("gelu"):
+            g64 = g.astype(np.float64)
+            return (0.5 * g64 * (1.0 + np.tanh(0.7978845608028654 * (g64 + 0.044715 * g64 ** 3)))) * u
+        return (g / (1.0 + np.exp(-g.astype(np.float64)))) * u
+
+    def attend(self, q_row, kk, vv, p):
+        """One head of one token over cache rows 0..p (float64), with the variant's soft cap
+        and sliding window (ops.cpp:327-350)."""
+        lo = max(0, p - self.opts["window"] + 1) if self.opts.get("window") else 0
+        sc = kk[lo:p + 1] @ q_row / np.sqrt(D)
+        if self.opts.get("softcap"):
+            c = self.opts["softcap"]
+            sc = c * np.tanh(sc / c)
+        e = np.exp(sc - sc.max())
+        return (e / e.sum()) @ vv[lo:p + 1]
 
     @staticmethod
     def rms(x, w):
@@ -116,21 +142,34 @@ class RefLayer:
                 kh = h // (H // HKV)
                 kk = self.kc[:p + 1, kh * D:(kh + 1) * D].astype(np.float64)
                 vv = self.vc[:p + 1, kh * D:(kh + 1) * D].astype(np.float64)
-                sc = kk @ q[t, h * D:(h + 1) * D].astype(np.float64) / np.sqrt(D)
-                e = np.exp(sc - sc.max())
-                att[t, h * D:(h + 1) * D] = (e / e.sum()) @ vv
+                att[t, h * D:(h + 1) * D] = self.attend(q[t, h * D:(h + 1) * D].astype(np.float64), kk, vv, p)
         proj = self.mm("wo", att.astype(np.float32))
         if "bias_o" in self.x:
             proj = proj + self.x["bias_o"]
+        if "post_attn_norm" in self.x:
+            proj = self.rms(proj, self.x["post_attn_norm"])
         x = x + proj
         xb = self.rms(x, self.fn)
         g, u = self.mm("wg", xb), self.mm("wu", xb)
-        h = (g / (1.0 + np.exp(-g))) * u
-        return x + self.mm("wd", h.astype(np.float32))
+        dn = self.mm("wd", self.act(g, u).astype(np.float32))
+        if "post_ffn_norm" in self.x:
+            dn = self.rms(dn, self.x["post_ffn_norm"])
+        return x + dn
+
+
+# per variant: weight types (a fused tensor has one type), span options
+VARIANT_TYPES = {"phi3": dict(TYPES, wv=fh.Q4_K)}
+VARIANT_OPTS = {"gemma2": dict(softcap=5.0, window=24, gelu=True)}
 
 
 def layer_extras(variant):
     """The optional per-layer vectors of a variant (backend.h:129-134)."""
+    if variant == "phi3":
+        return {"bias_q": normal(676, (Q,), 0.5), "bias_k": normal(677, (KV,), 0.5),
+                "bias_v": normal(678, (KV,), 0.5)}
+    if variant == "gemma2":
+        return {"post_attn_norm": (1.0 + 0.2 * normal(679, (E,), 1.0)).astype(np.float32),
+                "post_ffn_norm": (1.0 + 0.2 * normal(680, (E,), 1.0)).astype(np.float32)}
     if variant == "qwen3":
         return {"q_norm": (1.0 + 0.2 * normal(670, (D,), 1.0)).astype(np.float32),
                 "k_norm": (1.0 + 0.2 * normal(671, (D,), 1.0)).astype(np.float32)}
@@ -141,16 +180,37 @@ def layer_extras(variant):
 
 
 def setup_span(oracle, be, rot_dim, variant, tag, ctx=CTX):
-    packed = {n: fh.quantize_rows(TYPES[n], normal(600 + i, SHAPES[n], 0.03)) for i, n in enumerate(TYPES)}
-    for n in TYPES:
-        assert be.upload(f"{tag}.{n}", TYPES[n], packed[n], SHAPES[n][1], SHAPES[n][0])
+    types = VARIANT_TYPES.get(variant, TYPES)
+    opts = VARIANT_OPTS.get(variant, {})
+    packed = {n: fh.quantize_rows(types[n], normal(600 + i, SHAPES[n], 0.03)) for i, n in enumerate(types)}
+    for n in types:
+        assert be.upload(f"{tag}.{n}", types[n], packed[n], SHAPES[n][1], SHAPES[n][0])
     an = (1.0 + 0.1 * normal(640, (E,), 1.0)).astype(np.float32)
     fn = (1.0 + 0.1 * normal(641, (E,), 1.0)).astype(np.float32)
     cos, sin = rope_tables(rot_dim, ctx)
-    names = [f"{tag}.{n}" for n in TYPES]
+    names = [f"{tag}.{n}" for n in types]
+    uploaded = list(names)
     extras = layer_extras(variant)
-    assert be.span_prepare([(names, an, fn, extras)], E, H, HKV, D, F, ctx, cos, sin, rope_neox=True)
-    return names, RefLayer(oracle, packed, an, fn, cos, sin, extras=extras), (packed, an, fn, cos, sin, extras)
+    span_extras = dict(extras)
+    if variant == "phi3":
+        # the fused tensors: rows of q, k, v (and of gate, up) concatenated, one bias for q|k|v
+        fq = np.concatenate([packed["wq"], packed["wk"], packed["wv"]])
+        fgu = np.concatenate([packed["wg"], packed["wu"]])
+        assert be.upload(f"{tag}.wqkv", fh.Q4_K, fq, E, Q + 2 * KV)
+        assert be.upload(f"{tag}.wgu", fh.Q4_K, fgu, E, 2 * F)
+        uploaded += [f"{tag}.wqkv", f"{tag}.wgu"]
+        span_extras = {"wqkv": f"{tag}.wqkv",
+                       "bias_qkv": np.concatenate([extras["bias_q"], extras["bias_k"], extras["bias_v"]])}
+        names_span = [None, None, None, names[3], None, f"{tag}.wgu", names[6]]
+    else:
+        names_span = names
+    if opts.get("window"):
+        span_extras["sliding_window"] = True
+    assert be.span_prepare([(names_span, an, fn, span_extras)], E, H, HKV, D, F, ctx, cos, sin, rope_neox=True,
+                           attn_softcap=opts.get("softcap", 0.0), window=opts.get("window", 0),
+                           gelu=opts.get("gelu", False))
+    ref = RefLayer(oracle, packed, an, fn, cos, sin, extras=extras, types=types, opts=opts)
+    return uploaded, ref, (packed, an, fn, cos, sin, extras)
 
 
 def close(got, want, tol, what):
@@ -189,17 +249,24 @@ def check_stages(be, ref, x_in, x_out, pos0, what):
             kh = hh // (H // HKV)
             kk = kc[:p + 1, kh * D:(kh + 1) * D].astype(np.float64)
             vv = vc[:p + 1, kh * D:(kh + 1) * D].astype(np.float64)
-            sc = kk @ qr[t, hh * D:(hh + 1) * D].astype(np.float64) / np.sqrt(D)
-            e = np.exp(sc - sc.max())
-            a_want[t, hh * D:(hh + 1) * D] = (e / e.sum()) @ vv
+            a_want[t, hh * D:(hh + 1) * D] = ref.attend(qr[t, hh * D:(hh + 1) * D].astype(np.float64), kk, vv, p)
     close(att, a_want, 1e-5, f"{what}: attention")
-    close(proj, ref.mm("wo", att), 1e-4, f"{what}: o projection")
-    x1 = x_in + (proj + X["bias_o"] if "bias_o" in X else proj)
+    if "post_attn_norm" in X:
+        # proj holds rmsnorm(o + bias_o) * post_attn_norm
+        p_want = ref.mm("wo", att) + (X["bias_o"] if "bias_o" in X else 0.0)
+        close(proj, ref.rms(p_want.astype(np.float32), X["post_attn_norm"]), 1e-4, f"{what}: o projection, post norm")
+        x1 = x_in + proj
+    else:
+        close(proj, ref.mm("wo", att), 1e-4, f"{what}: o projection")
+        x1 = x_in + (proj + X["bias_o"] if "bias_o" in X else proj)
     close(xb2, ref.rms(x1, ref.fn), 1e-6, f"{what}: FFN norm")
     close(u, ref.mm("wu", xb2), 1e-4, f"{what}: up")
     g = ref.mm("wg", xb2)
-    close(h, (g / (1.0 + np.exp(-g.astype(np.float64)))) * u, 1e-4, f"{what}: silu(gate) * up")
-    close(dn, ref.mm("wd", h), 1e-4, f"{what}: down")
+    close(h, ref.act(g, u), 1e-4, f"{what}: act(gate) * up")
+    d_want = ref.mm("wd", h)
+    if "post_ffn_norm" in X:
+        d_want = ref.rms(d_want, X["post_ffn_norm"])
+    close(dn, d_want, 1e-4, f"{what}: down")
     assert np.array_equal(x_out, x1 + dn), f"{what}: residual stream"
 
 
@@ -217,7 +284,8 @@ def check_call(be, ref, x, pos0, what):
     return d_dev, d_ref
 
 
-@pytest.mark.parametrize("rot_dim,variant", [(D, "llama"), (D // 2, "llama"), (D, "qwen3"), (D, "bias")])
+@pytest.mark.parametrize("rot_dim,variant", [(D, "llama"), (D // 2, "llama"), (D, "qwen3"), (D, "bias"),
+                                             (D, "phi3"), (D, "gemma2")])
 def test_span_layer_matches_fish_forward(oracle, rot_dim, variant):
     be = fh.HipBackend()
     assert be.available()
@@ -235,9 +303,27 @@ def test_span_layer_matches_fish_forward(oracle, rot_dim, variant):
                 wrong = RefLayer(oracle, packed, an, fn, cos, sin, neox=False, extras=extras)
                 bad = wrong.prep(q, extras.get("bias_q"), extras.get("q_norm"), pos, H)
                 assert np.abs(qr - bad).max() > 1e-2 * np.abs(qr).max()
-                if extras:
+                if "bias_q" in extras or "q_norm" in extras:
                     plain = ref.prep(q, None, None, pos, H)
                     assert np.abs(qr - plain).max() > 1e-2 * np.abs(qr).max()
+            if i == 4 and ref.opts:
+                # the bars reject attention without the soft cap or without the window, and SiLU
+                # for GELU: each is far outside the 1e-5 / 1e-4 stage bars on this call
+                att, qr = be.span_inspect("att", Q), be.span_inspect("qr", Q)
+                kc = be.span_inspect("kc", KV, 0, 0, pos0 + n)
+                vc = be.span_inspect("vc", KV, 0, 0, pos0 + n)
+                for drop in ("softcap", "window"):
+                    alt = RefLayer(oracle, packed, an, fn, cos, sin, extras=extras, types=ref.types,
+                                   opts={k: v for k, v in ref.opts.items() if k != drop})
+                    t, p = n - 1, pos0 + n - 1
+                    a_alt = alt.attend(qr[t, :D].astype(np.float64), kc[:, :D].astype(np.float64),
+                                       vc[:, :D].astype(np.float64), p)
+                    assert np.abs(att[t, :D] - a_alt).max() > 1e-3 * np.abs(a_alt).max(), drop
+                g, u = be.span_inspect("h", F), be.span_inspect("u", F)
+                silu = RefLayer(oracle, packed, an, fn, cos, sin, extras=extras, types=ref.types, opts={})
+                xb2 = be.span_inspect("xb2", E)
+                gg = ref.mm("wg", xb2)
+                assert np.abs(silu.act(gg, u) - ref.act(gg, u)).max() > 1e-2 * np.abs(ref.act(gg, u)).max()
             pos0 += n
         # past the context: refused, x untouched
         x = normal(660, (CTX - pos0 + 1, E), 1.0)
@@ -316,3 +402,40 @@ def test_span_refuses_missing_or_misshaped_weights():
     assert not be.span_prepare([(names, an, an)], E, 1, 1, 512, F, CTX, cos, sin)
     x = normal(661, (1, E), 1.0)
     assert not be.span_forward(x, 0)
+
+
+def test_span_refuses_inconsistent_fused_forms():
+    """A fused q|k|v with separate q/k/v keys or separate biases, a fused bias without the fused
+    tensor, a fused gate|up of the wrong height, and a sliding-window layer without a window
+    size are refused (the descriptor contract of include/fish_hip.h)."""
+    be = fh.HipBackend()
+    types = VARIANT_TYPES["phi3"]
+    packed = {n: fh.quantize_rows(types[n], normal(600 + i, SHAPES[n], 0.03)) for i, n in enumerate(types)}
+    names = [f"fz.{n}" for n in types]
+    for n, name in zip(types, names):
+        assert be.upload(name, types[n], packed[n], SHAPES[n][1], SHAPES[n][0])
+    assert be.upload("fz.wqkv", fh.Q4_K, np.concatenate([packed["wq"], packed["wk"], packed["wv"]]), E, Q + 2 * KV)
+    assert be.upload("fz.wgu", fh.Q4_K, np.concatenate([packed["wg"], packed["wu"]]), E, 2 * F)
+    an = np.ones(E, np.float32)
+    cos, sin = rope_tables(D)
+    fused = [None, None, None, names[3], None, "fz.wgu", names[6]]
+    bqkv = np.zeros(Q + 2 * KV, np.float32)
+    try:
+        ok = be.span_prepare([(fused, an, an, {"wqkv": "fz.wqkv", "bias_qkv": bqkv})], E, H, HKV, D, F, CTX, cos,
+                             sin)
+        assert ok
+        bad = [
+            [(names, an, an, {"wqkv": "fz.wqkv"})],                                   # fused and separate
+            [(fused, an, an, {"wqkv": "fz.wqkv", "bias_q": np.zeros(Q, np.float32)})],  # separate bias
+            [(names, an, an, {"bias_qkv": bqkv})],                                    # fused bias alone
+            [(names[:4] + [None, names[5], names[6]], an, an)],                      # gate|up of F rows
+        ]
+        for layers in bad:
+            assert not be.span_prepare(layers, E, H, HKV, D, F, CTX, cos, sin)
+        assert not be.span_prepare([(names, an, an, {"sliding_window": True})], E, H, HKV, D, F, CTX, cos, sin)
+        assert be.span_prepare([(names, an, an, {"sliding_window": True})], E, H, HKV, D, F, CTX, cos, sin,
+                               window=8)
+    finally:
+        be.span_release()
+        for n in names + ["fz.wqkv", "fz.wgu"]:
+            be.release(n)
