@@ -172,7 +172,9 @@ hipError_t launch_gemm_group(int n, const void* const* ws, const WeightLayout* W
 // x += y. With pos_dev, the kernels read the first position from device memory
 // instead of pos0 (a graph replayed for every decode position; the caller
 // keeps pos_dev[0] + n_tok <= the cache and ld). rmsnorm with y != nullptr
-// first adds y (+ b when given) into x (written back).
+// first adds y (+ b when given) into x (written back). Attention of more than
+// kAttnSplitTok tokens with head dims 64 or 128 (and no pos_dev) runs on f32
+// MFMA tiles of 32 tokens x 32 positions.
 struct SpanVecs {
     const float* q_norm;  // [head_dim] or null (Qwen-3)
     const float* k_norm;

@@ -434,6 +434,159 @@ __global__ __launch_bounds__(kTh) void attn_full_kernel(const float* __restrict_
     if (tid < D) out[size_t(t) * Q + size_t(h) * D + tid] = o_run * (1.0f / l_run);
 }
 
+// Attention of more tokens on f32 MFMA (v_mfma_f32_32x32x2_f32), for head
+// dims D of 64 or 128. One workgroup (four wavefronts) per (block of 32
+// tokens, head); wavefront w takes the key blocks of 32 positions
+// b = b_lo + w, b_lo + w + 4, ... that the block's tokens can see, keeps a
+// running max, sum and output per token, and the four are merged at the end
+// (exact max, then the four sums and outputs rescaled and added in wavefront
+// order). The tiles are transposed so that tokens run along lanes:
+//   S^T = K Q^T   (32 keys x 32 tokens; k = the D head values, two per step),
+//   O^T += V^T P^T (D values x 32 tokens in D / 32 tiles; k = the 32 keys).
+// In the 32x32 MFMA output a lane holds one column (its token) and 16 rows:
+// register r of lane half h is row 8 (r / 4) + 4 h + r % 4. So a token's
+// softmax statistics stay in its own two lanes (l, l + 32), and the
+// probabilities of S^T are already the B operand of the second product when
+// its k order is taken to be that row order (step r pairs the keys of
+// register r in the two halves). K and V rows are staged through LDS per
+// wavefront, rows past the block's last position as zeros (so a masked
+// probability of 0 never meets a never-written cache row). Mathematically
+// FISH's softmax (ops.cpp:331-350); the rounding order differs.
+constexpr int kAttnMfmaTok = 32;
+
+template <int D>
+__global__ __launch_bounds__(256) void attn_mfma_kernel(const float* __restrict__ q, const _Float16* __restrict__ kc,
+                                                        const _Float16* __restrict__ vc, float* __restrict__ out,
+                                                        int n_tok, int ld, int H, int HKV, int pos0, float scale,
+                                                        float softcap, int window) {
+    typedef float v16f __attribute__((ext_vector_type(16)));
+    constexpr int NS = D / 2;      // k-steps of S^T
+    constexpr int DT = D / 32;     // 32-row tiles of O^T
+    constexpr int KROW = D + 8;    // LDS row stride in halves (16 bytes of padding)
+    constexpr int STAGE = 2 * 4 * 32 * KROW * 2;                // K and V rows of the four wavefronts
+    constexpr int MERGE = 4 * (D * 32 + 64) * 4;                // per wavefront: O^T, m, l
+    __shared__ __align__(16) unsigned char s_mem[STAGE > MERGE ? STAGE : MERGE];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, hf = lane >> 5, col = lane & 31;
+    const int head = int(blockIdx.x) % H, qb = int(blockIdx.x) / H;
+    const int kvh = head / (H / HKV), Q = H * D, KV = HKV * D;
+    const int t0 = qb * kAttnMfmaTok, t = t0 + col;
+    const int tc = min(t, n_tok - 1);                 // tokens past the call read the last one, unused
+    const int pos = pos0 + tc;
+    const int jlo = window > 0 ? max(0, pos - window + 1) : 0;  // this token's first position
+    const int pos_last = pos0 + min(t0 + kAttnMfmaTok - 1, n_tok - 1);
+    const int first_lo = window > 0 ? max(0, pos0 + t0 - window + 1) : 0;
+    const int kb_lo = first_lo / 32, kb_hi = pos_last / 32;
+
+    // Q^T operand: step s uses q[t][2 s + hf]
+    float qv[NS];
+    const float* qr = q + size_t(tc) * Q + size_t(head) * D;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) qv[s] = qr[2 * s + hf];
+
+    _Float16* sk = reinterpret_cast<_Float16*>(s_mem) + size_t(w) * 32 * KROW;
+    _Float16* sv = reinterpret_cast<_Float16*>(s_mem) + size_t(4 + w) * 32 * KROW;
+    v16f o[DT];
+#pragma unroll
+    for (int c = 0; c < DT; ++c) o[c] = v16f{};
+    float m_run = -INFINITY, l_run = 0.0f;
+    for (int kb = kb_lo + w; kb <= kb_hi; kb += 4) {  // uniform over the wavefront
+        const int j0 = kb * 32;
+        // stage rows j0 .. j0 + 31 of K and V, 16 bytes per lane per step
+#pragma unroll
+        for (int i = lane; i < 32 * (D / 8); i += 64) {
+            const int r = i / (D / 8), c8 = i % (D / 8), j = j0 + r;
+            uint4 kv4 = make_uint4(0, 0, 0, 0), vv4 = make_uint4(0, 0, 0, 0);
+            const size_t at = size_t(min(j, ld - 1)) * KV + size_t(kvh) * D + size_t(c8) * 8;
+            const uint4 kl = *reinterpret_cast<const uint4*>(kc + at);
+            const uint4 vl = *reinterpret_cast<const uint4*>(vc + at);
+            if (j <= pos_last) {
+                kv4 = kl;
+                vv4 = vl;
+            }
+            *reinterpret_cast<uint4*>(sk + r * KROW + c8 * 8) = kv4;
+            *reinterpret_cast<uint4*>(sv + r * KROW + c8 * 8) = vv4;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        // S^T = K Q^T, two accumulators
+        v16f s0 = v16f{}, s1 = v16f{};
+#pragma unroll
+        for (int s = 0; s < NS; s += 2) {
+            const float k0 = float(sk[col * KROW + 2 * s + hf]);
+            const float k1 = float(sk[col * KROW + 2 * s + 2 + hf]);
+            s0 = __builtin_amdgcn_mfma_f32_32x32x2f32(k0, qv[s], s0, 0, 0, 0);
+            s1 = __builtin_amdgcn_mfma_f32_32x32x2f32(k1, qv[s + 1], s1, 0, 0, 0);
+        }
+        // scores of this lane's token over its 16 keys (the other 16 are in lane l ^ 32)
+        float p[16];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int j = j0 + 8 * (r >> 2) + 4 * hf + (r & 3);
+            const float sc = score(s0[r] + s1[r], scale, softcap);
+            p[r] = (j <= pos && j >= jlo) ? sc : -INFINITY;
+            mx = fmaxf(mx, p[r]);
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float mn = fmaxf(m_run, mx);
+        const float a = mn == -INFINITY ? 1.0f : expf(m_run - mn);
+        float ls = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            p[r] = p[r] == -INFINITY ? 0.0f : expf(p[r] - mn);
+            ls += p[r];
+        }
+        ls += __shfl_xor(ls, 32);
+        l_run = l_run * a + ls;
+        m_run = mn;
+#pragma unroll
+        for (int c = 0; c < DT; ++c) o[c] *= a;
+        // O^T += V^T P^T; step r pairs the keys of register r in the two halves
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int kr = 8 * (r >> 2) + 4 * hf + (r & 3);
+#pragma unroll
+            for (int c = 0; c < DT; ++c) {
+                const float vv = float(sv[kr * KROW + 32 * c + col]);
+                o[c] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv, p[r], o[c], 0, 0, 0);
+            }
+        }
+        __builtin_amdgcn_wave_barrier();  // the next block overwrites this wavefront's rows
+    }
+    // merge the four wavefronts: O^T rows (dims) of register r of tile c are 32 c + 8 (r / 4) + 4 hf + r % 4
+    __syncthreads();
+    float* mo = reinterpret_cast<float*>(s_mem) + size_t(w) * (D * 32 + 64);
+#pragma unroll
+    for (int c = 0; c < DT; ++c)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mo[(32 * c + 8 * (r >> 2) + 4 * hf + (r & 3)) * 32 + col] = o[c][r];
+    if (hf == 0) {
+        mo[D * 32 + col] = m_run;
+        mo[D * 32 + 32 + col] = l_run;
+    }
+    __syncthreads();
+    const float* mb = reinterpret_cast<const float*>(s_mem);
+    for (int i = tid; i < D * 32; i += 256) {
+        const int d = i >> 5, tk = i & 31;
+        if (t0 + tk >= n_tok) continue;
+        float mw[4], M = -INFINITY;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            mw[v] = mb[size_t(v) * (D * 32 + 64) + D * 32 + tk];
+            M = fmaxf(M, mw[v]);
+        }
+        float L = 0.0f, O = 0.0f;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const float f = mw[v] == -INFINITY ? 0.0f : expf(mw[v] - M);
+            L = L + mb[size_t(v) * (D * 32 + 64) + D * 32 + 32 + tk] * f;
+            O = O + mb[size_t(v) * (D * 32 + 64) + d * 32 + tk] * f;
+        }
+        out[size_t(t0 + tk) * Q + size_t(head) * D + d] = O * (1.0f / L);
+    }
+}
+
 // g = silu(g) * u
 // g = act(g) * u: SiLU v / (1 + exp(-v)) (silu_inplace, ops.cpp:25-30), or with
 // gelu FISH's tanh GELU 0.5 v (1 + tanh(sqrt(2/pi) (v + 0.044715 v^3)))
@@ -501,6 +654,16 @@ hipError_t launch_attention(const float* q, const _Float16* kc, const _Float16* 
                             const int* pos_dev, float softcap, int window) {
     if (n_tok <= 0 || D <= 0 || D > kTh || D % 2 || HKV <= 0 || H % HKV || ld < pos0 + n_tok) return hipErrorInvalidValue;
     const dim3 block(kTh);
+    if (n_tok > kAttnSplitTok && !pos_dev && (D == 64 || D == 128)) {
+        const dim3 grid(unsigned((n_tok + kAttnMfmaTok - 1) / kAttnMfmaTok * H));
+        if (D == 64)
+            hipLaunchKernelGGL(attn_mfma_kernel<64>, grid, block, 0, s, q, kc, vc, out, n_tok, ld, H, HKV, pos0, scale,
+                               softcap, window);
+        else
+            hipLaunchKernelGGL(attn_mfma_kernel<128>, grid, block, 0, s, q, kc, vc, out, n_tok, ld, H, HKV, pos0, scale,
+                               softcap, window);
+        return hipGetLastError();
+    }
     if (n_tok > kAttnSplitTok) {
         const dim3 grid(unsigned(n_tok * H));
         if (D <= 128)
