@@ -44,6 +44,7 @@ typedef short v2s __attribute__((ext_vector_type(2)));
 typedef unsigned short v2us __attribute__((ext_vector_type(2)));
 
 constexpr int SSTEPS = 4;  // 32-value steps per stage
+constexpr int kGemmCUs = 256;  // MI355X compute units
 constexpr int RING = 3;    // LDS stages in flight
 
 // Raw weight data of one (row, 32-value step) item, between its global load
@@ -531,12 +532,30 @@ hipError_t launch_gemm_group(int n, const void* const* ws, const WeightLayout* W
         G.ldy[j] = ldys[j];
     }
     const ActPtrs A = act_ptrs(act, AL);
+    // a grid of the default tiles that leaves half the CUs without a workgroup (a
+    // 4096-row projection of a 256-token chunk: 128 workgroups) takes tiles of half the
+    // rows (Q4_K / Q5_K) or half the tokens (Q6_K) instead: 256 workgroups, measured
+    // 20 % (o, 4096x4096) and 14 % (down, 4096x14336) faster at M = 256; at 192 and more
+    // workgroups the default tiles were as fast or faster
+    int rows64 = 0, rows32 = 0;
+    for (int j = 0; j < n; ++j) {
+        rows64 += (n_outs[j] + 63) / 64;
+        rows32 += (n_outs[j] + 31) / 32;
+    }
+    const bool small = type == kQ6_K ? rows32 * ((n_tok + 255) / 256) <= kGemmCUs / 2
+                                     : rows64 * ((n_tok + 127) / 128) <= kGemmCUs / 2;
     switch (type) {
-        case kQ4_K: return gemm_launch<kQ4_K, 4, 1, 1, 2>(G, n_outs, A, n_in, n_tok, s);
-        case kQ5_K: return gemm_launch<kQ5_K, 4, 1, 1, 2>(G, n_outs, A, n_in, n_tok, s);
+        case kQ4_K:
+            return small ? gemm_launch<kQ4_K, 4, 1, 1, 1>(G, n_outs, A, n_in, n_tok, s)
+                         : gemm_launch<kQ4_K, 4, 1, 1, 2>(G, n_outs, A, n_in, n_tok, s);
+        case kQ5_K:
+            return small ? gemm_launch<kQ5_K, 4, 1, 1, 1>(G, n_outs, A, n_in, n_tok, s)
+                         : gemm_launch<kQ5_K, 4, 1, 1, 2>(G, n_outs, A, n_in, n_tok, s);
         // Q6_K (no mins MFMA, heavier dequantization): four token wavefronts share each
         // dequantized stage (measured 8-11 % faster on the 4096 x 14336 down projection)
-        case kQ6_K: return gemm_launch<kQ6_K, 4, 1, 2, 1>(G, n_outs, A, n_in, n_tok, s);
+        case kQ6_K:
+            return small ? gemm_launch<kQ6_K, 4, 1, 1, 1>(G, n_outs, A, n_in, n_tok, s)
+                         : gemm_launch<kQ6_K, 4, 1, 2, 1>(G, n_outs, A, n_in, n_tok, s);
         default: return hipErrorInvalidValue;
     }
 }
