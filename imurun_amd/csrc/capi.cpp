@@ -828,6 +828,14 @@ private:
         for (int i = 0; i < n && per_type; ++i)
             per_type = int8_type(rs[i]->layout.type) && gemv_x_supported(rs[i]->layout);
         if (per_type) {
+            // two K-quant types in one launch when instantiated, else one launch per type
+            WeightLayout Lm[kGemmGroupMax];
+            const void* wm[kGemmGroupMax];
+            for (int i = 0; i < n; ++i) {
+                Lm[i] = rs[i]->layout;
+                wm[i] = rs[i]->dev;
+            }
+            if (gemv_x_mixed_supported(n, Lm)) return launch_gemv_x(n, wm, Lm, dx, dys, stream_, norm, resid);
             hipError_t e = hipSuccess;
             bool done[kGemmGroupMax] = {};
             for (int i = 0; i < n && e == hipSuccess; ++i) {

@@ -11,6 +11,8 @@
 //
 // Also here: the per-block integer dump used by the parity tests, built from
 // the same dots.h functions.
+#include <algorithm>
+
 #include "common.h"
 #include "dots.h"
 #include "kernels.h"
@@ -221,6 +223,7 @@ constexpr int kGemvXWaves = 16;
 struct GemvXGroup {
     WeightPtrs w[kGemmGroupMax];
     float* y[kGemmGroupMax];
+    uint32_t type[kGemmGroupMax];
     int n_out[kGemmGroupMax];
     int wg_end[kGemmGroupMax];  // cumulative workgroups
     int n;
@@ -261,38 +264,22 @@ __device__ __forceinline__ void row_norm(float4 (&xv)[XV], const RowNorm& nm, in
     }
 }
 
-template <uint32_t T, int LPR, int MAXC, int RB, int XV, bool NORM>
-__global__ __launch_bounds__(64 * kGemvXWaves) void gemv_x_kernel(GemvXGroup G, const float* __restrict__ x,
-                                                                  int n_in) {
+// The rows of group member gm for workgroup wg of that member, on x held as
+// the float4 chunks xv (loaded by the caller before anything else).
+template <uint32_t T, int LPR, int MAXC, int XV, bool NORM>
+__device__ __forceinline__ void gemv_x_rows(const GemvXGroup& G, int gm, int wg, float4 (&xv)[XV], int n_in,
+                                            uint4* s_codes, float* s_d, int* s_s, double* s_red) {
     constexpr bool kq = kquant_type(T);
     constexpr int RPP = 64 / LPR;
-    __shared__ uint4 s_codes[2 * kGemvXMaxGroups];  // [half][group]: elements 16 h .. 16 h + 15
-    __shared__ float s_d[kGemvXMaxGroups];           // Q8Act d per group / Q8ActK d per super-block
-    __shared__ int s_s[kGemvXMaxGroups];             // Q8Act sum per group / the group's two per-16 sums
-
+    constexpr int RB = gemv_rb<T, MAXC>();
     const int tid = threadIdx.x, lane = tid & 63, sub = lane % LPR;
-    int gm = 0;
-#pragma unroll
-    for (int j = 1; j < kGemmGroupMax; ++j)
-        if (j < G.n && int(blockIdx.x) >= G.wg_end[j - 1]) gm = j;
-    const int wg = int(blockIdx.x) - (gm ? G.wg_end[gm - 1] : 0);
     const WeightPtrs W = G.w[gm];
     const int n_out = G.n_out[gm];
     const int wave_id = wg * kGemvXWaves + (tid >> 6);
     const int row_base = wave_id * (RPP * RB) + lane / LPR;
     const int groups = n_in / 32;
 
-    // x loads first
-    float4 xv[XV];
-#pragma unroll
-    for (int i = 0; i < XV; ++i) {
-        const int k0 = 4 * (tid + 64 * kGemvXWaves * i);
-        // unconditional load from a clamped address: chunks past the end lie in whole
-        // 32/256-value blocks the quantizer discards, and a load inside a branch would
-        // make the compiler wait for every outstanding load at the join
-        xv[i] = *reinterpret_cast<const float4*>(x + min(k0, n_in - 4));
-    }
-    // then every weight load of the wavefront (clamped, unconditional)
+    // every weight load of the wavefront (clamped, unconditional)
     int cg[MAXC];
     bool cv[MAXC];
 #pragma unroll
@@ -315,10 +302,7 @@ __global__ __launch_bounds__(64 * kGemvXWaves) void gemv_x_kernel(GemvXGroup G, 
 
     // every load is issued before the quantization's first use of x
     __builtin_amdgcn_sched_barrier(0);
-    if constexpr (NORM) {
-        __shared__ double s_red[kGemvXWaves];
-        row_norm<XV, 64 * kGemvXWaves>(xv, G.norm, n_in, tid, s_red);
-    }
+    if constexpr (NORM) row_norm<XV, 64 * kGemvXWaves>(xv, G.norm, n_in, tid, s_red);
     const LdsAct L{s_codes, s_d, s_s, kGemvXMaxGroups};
     quantize_to_lds<kq, XV, 64 * kGemvXWaves>(xv, n_in, tid, L);
     __syncthreads();
@@ -355,31 +339,131 @@ __global__ __launch_bounds__(64 * kGemvXWaves) void gemv_x_kernel(GemvXGroup G, 
     }
 }
 
-template <uint32_t T, int LPR, int MAXC>
-hipError_t gemv_x_launch(GemvXGroup G, const float* x, int n_in, hipStream_t s) {
-    // the plain GEMV's rows per wavefront; one quantization of x serves the
-    // kGemvXWaves wavefronts of a workgroup
-    constexpr int RB = gemv_rb<T, MAXC>();
-    constexpr int RPW = (64 / LPR) * RB;
-    constexpr int TH = 64 * kGemvXWaves;
-    // 4-value chunks per thread: >= n_in / (4 TH) for every n_in of this (LPR, MAXC)
-    constexpr int XV = LPR == 64 ? (64 * 32 * MAXC / 4 + TH - 1) / TH : 1;
+// The group member of this workgroup and the workgroup's index within it.
+__device__ __forceinline__ int gemv_x_member(const GemvXGroup& G, int& wg) {
+    int gm = 0;
+#pragma unroll
+    for (int j = 1; j < kGemmGroupMax; ++j)
+        if (j < G.n && int(blockIdx.x) >= G.wg_end[j - 1]) gm = j;
+    wg = int(blockIdx.x) - (gm ? G.wg_end[gm - 1] : 0);
+    return gm;
+}
+
+// x loads first: unconditional, from a clamped address (chunks past the end lie in
+// whole 32/256-value blocks the quantizer discards, and a load inside a branch would
+// make the compiler wait for every outstanding load at the join)
+template <int XV>
+__device__ __forceinline__ void gemv_x_loads(const float* __restrict__ x, int n_in, float4 (&xv)[XV]) {
+#pragma unroll
+    for (int i = 0; i < XV; ++i) {
+        const int k0 = 4 * (int(threadIdx.x) + 64 * kGemvXWaves * i);
+        xv[i] = *reinterpret_cast<const float4*>(x + min(k0, n_in - 4));
+    }
+}
+
+template <uint32_t T, int LPR, int MAXC, int XV, bool NORM>
+__global__ __launch_bounds__(64 * kGemvXWaves) void gemv_x_kernel(GemvXGroup G, const float* __restrict__ x,
+                                                                  int n_in) {
+    __shared__ uint4 s_codes[2 * kGemvXMaxGroups];  // [half][group]: elements 16 h .. 16 h + 15
+    __shared__ float s_d[kGemvXMaxGroups];           // Q8Act d per group / Q8ActK d per super-block
+    __shared__ int s_s[kGemvXMaxGroups];             // Q8Act sum per group / the group's two per-16 sums
+    __shared__ double s_red[kGemvXWaves];
+    int wg;
+    const int gm = gemv_x_member(G, wg);
+    float4 xv[XV];
+    gemv_x_loads<XV>(x, n_in, xv);
+    gemv_x_rows<T, LPR, MAXC, XV, NORM>(G, gm, wg, xv, n_in, s_codes, s_d, s_s, s_red);
+}
+
+// Two K-quant types in one launch (a layer's q / k in Q4_K and v in Q6_K): both
+// read the same Q8ActK quantization of x; each workgroup takes its member's
+// type's path (a branch uniform over the workgroup).
+template <uint32_t T1, uint32_t T2, int LPR, int MAXC, int XV, bool NORM>
+__global__ __launch_bounds__(64 * kGemvXWaves) void gemv_x2_kernel(GemvXGroup G, const float* __restrict__ x,
+                                                                   int n_in) {
+    static_assert(kquant_type(T1) && kquant_type(T2), "one activation layout for both types");
+    __shared__ uint4 s_codes[2 * kGemvXMaxGroups];
+    __shared__ float s_d[kGemvXMaxGroups];
+    __shared__ int s_s[kGemvXMaxGroups];
+    __shared__ double s_red[kGemvXWaves];
+    int wg;
+    const int gm = gemv_x_member(G, wg);
+    float4 xv[XV];
+    gemv_x_loads<XV>(x, n_in, xv);
+    if (G.type[gm] == T1)
+        gemv_x_rows<T1, LPR, MAXC, XV, NORM>(G, gm, wg, xv, n_in, s_codes, s_d, s_s, s_red);
+    else
+        gemv_x_rows<T2, LPR, MAXC, XV, NORM>(G, gm, wg, xv, n_in, s_codes, s_d, s_s, s_red);
+}
+
+// rows per wavefront of type t at MAXC groups per lane (gemv_rb)
+inline int gemv_rb_of(uint32_t t, int maxc) {
+    const int per_group = t == kQ8_0 ? 32 : 16;
+    const int rb = 64 / (per_group * maxc);
+    return rb < 1 ? 1 : (rb > 8 ? 8 : rb);
+}
+
+// 4-value chunks per thread: >= n_in / (4 TH) for every n_in of this (LPR, MAXC)
+template <int LPR, int MAXC>
+constexpr int gemv_x_xv() {
+    return LPR == 64 ? (64 * 32 * MAXC / 4 + 64 * kGemvXWaves - 1) / (64 * kGemvXWaves) : 1;
+}
+
+// workgroups of each member (each type's own rows per wavefront; one quantization of x
+// serves the kGemvXWaves wavefronts of a workgroup)
+template <int LPR, int MAXC>
+int gemv_x_grid(GemvXGroup& G) {
     int wgs = 0;
     for (int j = 0; j < G.n; ++j) {
-        wgs += ((G.n_out[j] + RPW - 1) / RPW + kGemvXWaves - 1) / kGemvXWaves;
+        const int rpw = (64 / LPR) * gemv_rb_of(G.type[j], MAXC);
+        wgs += ((G.n_out[j] + rpw - 1) / rpw + kGemvXWaves - 1) / kGemvXWaves;
         G.wg_end[j] = wgs;
     }
+    return wgs;
+}
+
+template <uint32_t T, int LPR, int MAXC>
+hipError_t gemv_x_launch(GemvXGroup G, const float* x, int n_in, hipStream_t s) {
+    static_assert(gemv_rb<T, MAXC>() >= 1, "rows per wavefront");
+    constexpr int TH = 64 * kGemvXWaves;
+    constexpr int XV = gemv_x_xv<LPR, MAXC>();
+    const int wgs = gemv_x_grid<LPR, MAXC>(G);
     if (G.norm.w) {
         // rows of up to 4 groups per lane (n_in <= 8192): the prologue spills registers beyond
         if constexpr (MAXC <= 4)
-            hipLaunchKernelGGL((gemv_x_kernel<T, LPR, MAXC, RB, XV, true>), dim3(unsigned(wgs)), dim3(TH), 0, s, G,
-                               x, n_in);
+            hipLaunchKernelGGL((gemv_x_kernel<T, LPR, MAXC, XV, true>), dim3(unsigned(wgs)), dim3(TH), 0, s, G, x,
+                               n_in);
         else
             return hipErrorInvalidValue;
     } else
-        hipLaunchKernelGGL((gemv_x_kernel<T, LPR, MAXC, RB, XV, false>), dim3(unsigned(wgs)), dim3(TH), 0, s, G, x,
+        hipLaunchKernelGGL((gemv_x_kernel<T, LPR, MAXC, XV, false>), dim3(unsigned(wgs)), dim3(TH), 0, s, G, x,
                            n_in);
     return hipGetLastError();
+}
+
+template <uint32_t T1, uint32_t T2, int MAXC>
+hipError_t gemv_x2_launch(GemvXGroup G, const float* x, int n_in, hipStream_t s) {
+    constexpr int TH = 64 * kGemvXWaves;
+    constexpr int XV = gemv_x_xv<64, MAXC>();
+    const int wgs = gemv_x_grid<64, MAXC>(G);
+    if (G.norm.w)
+        hipLaunchKernelGGL((gemv_x2_kernel<T1, T2, 64, MAXC, XV, true>), dim3(unsigned(wgs)), dim3(TH), 0, s, G, x,
+                           n_in);
+    else
+        hipLaunchKernelGGL((gemv_x2_kernel<T1, T2, 64, MAXC, XV, false>), dim3(unsigned(wgs)), dim3(TH), 0, s, G,
+                           x, n_in);
+    return hipGetLastError();
+}
+
+template <uint32_t T1, uint32_t T2>
+hipError_t gemv_x2_pick(GemvXGroup G, const float* x, int n_in, hipStream_t s) {
+    switch ((n_in / 32 + 63) / 64) {
+        case 1: return gemv_x2_launch<T1, T2, 1>(G, x, n_in, s);
+        case 2: return gemv_x2_launch<T1, T2, 2>(G, x, n_in, s);
+        case 3: return gemv_x2_launch<T1, T2, 3>(G, x, n_in, s);
+        case 4: return gemv_x2_launch<T1, T2, 4>(G, x, n_in, s);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 template <uint32_t T, int LPR>
@@ -468,6 +552,29 @@ bool gemv_x_supported(const WeightLayout& L) {
     return L.total && L.n_in <= 32 * kGemvXMaxGroups && (!is_kquant(L.type) || L.n_in % 256 == 0);
 }
 
+namespace {
+
+// the two-type launches instantiated: K-quants of one layer's projections
+bool gemv_x2_pair(uint32_t a, uint32_t b) {
+    return (a == kQ4_K && (b == kQ5_K || b == kQ6_K)) || (a == kQ5_K && b == kQ6_K);
+}
+
+}  // namespace
+
+bool gemv_x_mixed_supported(int n, const WeightLayout* WLs) {
+    if (n < 2 || n > kGemmGroupMax) return false;
+    uint32_t a = WLs[0].type, b = WLs[0].type;
+    for (int j = 0; j < n; ++j) {
+        if (!gemv_x_supported(WLs[j]) || WLs[j].n_in != WLs[0].n_in) return false;
+        a = std::min(a, WLs[j].type);
+        b = std::max(b, WLs[j].type);
+    }
+    for (int j = 0; j < n; ++j)
+        if (WLs[j].type != a && WLs[j].type != b) return false;
+    const int n_in = WLs[0].n_in;
+    return a != b && gemv_x2_pair(a, b) && n_in / 32 >= 64 && (n_in / 32 + 63) / 64 <= 4;
+}
+
 hipError_t launch_gemv_x(int n, const void* const* ws, const WeightLayout* WLs, const float* x, float* const* ys,
                          hipStream_t s, const RowNorm* norm, const RowResid* resid) {
     if (n <= 0 || n > kGemmGroupMax || !gemv_x_supported(WLs[0])) return hipErrorInvalidValue;
@@ -477,11 +584,25 @@ hipError_t launch_gemv_x(int n, const void* const* ws, const WeightLayout* WLs, 
     G.n = n;
     if (norm) G.norm = *norm;
     if (resid) G.resid = *resid;
+    bool mixed = false;
     for (int j = 0; j < n; ++j) {
-        if (!WLs[j].total || WLs[j].type != WLs[0].type || WLs[j].n_in != WLs[0].n_in) return hipErrorInvalidValue;
+        if (!WLs[j].total || WLs[j].n_in != WLs[0].n_in) return hipErrorInvalidValue;
+        mixed = mixed || WLs[j].type != WLs[0].type;
         G.w[j] = weight_ptrs(ws[j], WLs[j]);
         G.y[j] = ys[j];
+        G.type[j] = WLs[j].type;
         G.n_out[j] = WLs[j].n_out;
+    }
+    if (mixed) {
+        if (!gemv_x_mixed_supported(n, WLs)) return hipErrorInvalidValue;
+        uint32_t a = WLs[0].type, b = WLs[0].type;
+        for (int j = 0; j < n; ++j) {
+            a = std::min(a, WLs[j].type);
+            b = std::max(b, WLs[j].type);
+        }
+        if (a == kQ4_K && b == kQ5_K) return gemv_x2_pick<kQ4_K, kQ5_K>(G, x, WLs[0].n_in, s);
+        if (a == kQ4_K && b == kQ6_K) return gemv_x2_pick<kQ4_K, kQ6_K>(G, x, WLs[0].n_in, s);
+        return gemv_x2_pick<kQ5_K, kQ6_K>(G, x, WLs[0].n_in, s);
     }
     switch (WLs[0].type) {
         case kQ8_0: return gemv_x_pick<kQ8_0>(G, x, WLs[0].n_in, s);

@@ -133,6 +133,10 @@ struct RowResid {
     float* x;
     const float* bias;
 };
+// Tensors of two K-quant types (Q4_K with Q5_K or Q6_K, Q5_K with Q6_K) may share
+// one launch when gemv_x_mixed_supported (n_in 2048..8192): both read the same
+// quantization of x.
+bool gemv_x_mixed_supported(int n, const WeightLayout* WLs);
 hipError_t launch_gemv_x(int n, const void* const* ws, const WeightLayout* WLs, const float* x, float* const* ys,
                          hipStream_t stream, const RowNorm* norm = nullptr, const RowResid* resid = nullptr);
 

@@ -306,6 +306,30 @@ def test_backend_upload_matmul_group(torch_dev, oracle):
     assert not be.resident("q")
 
 
+@pytest.mark.parametrize("types", [(fh.Q4_K, fh.Q4_K, fh.Q6_K), (fh.Q5_K, fh.Q6_K, fh.Q5_K), (fh.Q6_K, fh.Q4_K, fh.Q5_K)],
+                         ids=["q4k-q4k-q6k", "q5k-q6k-q5k", "three-types"])
+@pytest.mark.parametrize("n_in", [2048, 4096, 8192])
+def test_backend_one_token_mixed_types(torch_dev, oracle, types, n_in):
+    """One token through a q/k/v-shaped group of mixed K-quant types (a Q4_K_M layer's q, k in
+    Q4_K and v in Q6_K): two types share one launch, each workgroup taking its tensor's type's
+    path on the same quantized x; a third type falls back to one launch per type. Bit-identical
+    to each tensor alone, and close to the oracle."""
+    be = fh.HipBackend()
+    n_outs = [1024, 256, 256]
+    names = [f"mx{i}_{n_in}" for i in range(3)]
+    packed = []
+    for i, (name, t, n_out) in enumerate(zip(names, types, n_outs)):
+        packed.append(packed_weights(oracle, t, n_out, n_in, 1600 + i + n_in))
+        assert be.upload(name, t, packed[-1], n_in, n_out)
+    x = normal(1700 + n_in, (1, n_in))
+    ys = be.matmul_group(names, x, n_outs)
+    for name, t, p, n_out, y in zip(names, types, packed, n_outs, ys):
+        assert np.array_equal(be.matmul(name, x, n_out), y), f"{name}: group differs from single"
+        check_close(y, oracle.matmul_f32(t, p, x, n_out), f"mixed {fh.TYPE_NAMES[t]} K={n_in}")
+    for name in names:
+        be.release(name)
+
+
 def test_backend_upload_keeps_the_vram_headroom(torch_dev, oracle, monkeypatch):
     """upload() leaves FISH's VRAM headroom free (vram_headroom_bytes, backend.h:171-187): with
     FISH_VRAM_HEADROOM_MB above the free memory the upload is refused (earlier uploads intact),
