@@ -138,11 +138,11 @@ def run_prefill(args, torch, fh, dev):
                         ys=[ys[n] for n in names])
 
     parts = {
-        "quantize_x": lambda c: fh.quantize(x, act=ax),
+        "quantize_x": lambda c: fh.quantize(x, act=ax, for_type=fh.Q4_K),
         "qkv": lambda c: group(c, ["q", "k", "v"], ax),
         "o": lambda c: group(c, ["o"], ax),
         "gate_up": lambda c: group(c, ["gate", "up"], ax),
-        "quantize_h": lambda c: fh.quantize(hx, act=ah),
+        "quantize_h": lambda c: fh.quantize(hx, act=ah, for_type=fh.Q6_K),
         "down": lambda c: group(c, ["down"], ah),
     }
     reps = max(10, args.steps // 4)

@@ -61,6 +61,7 @@ def load() -> ctypes.CDLL:
         "fish_hip_weight_bytes": ([ctypes.c_uint32, ctypes.c_int, ctypes.c_int], ctypes.c_uint64),
         "fish_hip_act_bytes": ([ctypes.c_int, ctypes.c_int], ctypes.c_uint64),
         "fish_hip_quantize": ([_P, ctypes.c_int, ctypes.c_int, _P, _P, _P, _P], ctypes.c_int),
+        "fish_hip_quantize_for": ([ctypes.c_uint32, _P, ctypes.c_int, ctypes.c_int, _P, _P], ctypes.c_int),
         "fish_hip_repack": ([ctypes.c_uint32, _P, ctypes.c_int, ctypes.c_int, _P, _P], ctypes.c_int),
         "fish_hip_matmul": ([ctypes.c_uint32, _P, _P, ctypes.c_int, ctypes.c_int, ctypes.c_int, _P, _P], ctypes.c_int),
         "fish_hip_matmul_group": ([ctypes.c_uint32, ctypes.c_int, _P, _P, ctypes.c_int, ctypes.c_int, _P, _P, _P],
@@ -153,14 +154,21 @@ def act_bytes(n_tok: int, n_in: int) -> int:
     return int(load().fish_hip_act_bytes(n_tok, n_in))
 
 
-def quantize(x, act=None, fish_layouts: bool = False, stream=None):
+def quantize(x, act=None, fish_layouts: bool = False, stream=None, for_type: int | None = None):
     """ActBatch::quantize on the device. x: f32 cuda [n_tok, n_in].
-    Returns act (uint8 cuda) or (act, q32 bytes, q256 bytes) with FISH's layouts."""
+    Returns act (uint8 cuda) or (act, q32 bytes, q256 bytes) with FISH's layouts.
+    for_type: only the planes the matmuls of that weight type read at n_tok tokens."""
     import torch
     assert x.is_cuda and x.dtype == torch.float32 and x.dim() == 2 and x.is_contiguous()
     n_tok, n_in = x.shape
     if act is None:
         act = torch.empty(act_bytes(n_tok, n_in), dtype=torch.uint8, device=x.device)
+    if for_type is not None:
+        if fish_layouts:
+            raise FishHipError("quantize: for_type writes no FISH layouts")
+        _check(load().fish_hip_quantize_for(for_type, x.data_ptr(), n_tok, n_in, act.data_ptr(), _stream(stream)),
+               "quantize_for")
+        return act
     q32 = q256 = None
     if fish_layouts:
         q32 = torch.empty(n_tok * (n_in // 32) * 40, dtype=torch.uint8, device=x.device)

@@ -92,6 +92,14 @@ hipError_t dispatch_matmul(const void* w, const WeightLayout& L, const void* act
     return launch_gemv(w, L, act, n_tok, n_tok, y, ldy, s);
 }
 
+// The activation planes the kernel that dispatch_matmul picks for this tensor
+// reads (kernels.h): a quantization for one consumer writes only those.
+unsigned planes_of(const WeightLayout& L, int n_tok) {
+    if (uses_gemm(L, n_tok)) return kPlanesGemm;
+    if (n_tok > kGemvMaxTok && batch_mfma_supported(L)) return is_kquant(L.type) ? kPlanesBatch256 : kPlanesBatch32;
+    return kPlanesGemv;
+}
+
 // Workspace of one expert-FFN call: routing arrays, the quantized input, the
 // per-slot gate/up/down rows and the quantized hidden rows (slot = one chosen
 // (token, expert) pair, grouped by expert).
@@ -857,8 +865,12 @@ private:
             return e;
         }
         hipError_t e = hipSuccess;
-        if (!fused && any_int8)
-            e = launch_quantize(dx, n_tok, n_in, n_in, act, nullptr, nullptr, stream_, planes_for_tokens(n_tok, n_in));
+        if (!fused && any_int8) {
+            unsigned planes = 0;  // what this group's int8 tensors read, nothing else
+            for (int i = 0; i < n; ++i)
+                if (int8_type(rs[i]->layout.type)) planes |= planes_of(rs[i]->layout, n_tok);
+            e = launch_quantize(dx, n_tok, n_in, n_in, act, nullptr, nullptr, stream_, planes);
+        }
         // tensors of one K-quant type go out as one grouped launch when the batch is GEMM-sized
         bool one_group = n <= kGemmGroupMax;
         for (int i = 0; i < n; ++i)
@@ -1018,6 +1030,15 @@ int fish_hip_abi_version(void) { return FISH_HIP_ABI_VERSION; }
 const char* fish_hip_kernel_name(void) { return "hip-gfx950"; }
 const char* fish_hip_last_error(void) { return g_err.c_str(); }
 
+int fish_hip_quantize_for(uint32_t type, const float* x, int n_tok, int n_in, void* act, void* stream) {
+    if (!x || !act || n_tok <= 0 || n_in <= 0 || n_in % 32) return fail(FISH_HIP_ERR_ARG, "quantize_for: bad arguments");
+    const WeightLayout L = weight_layout(type, n_in, 1);
+    if (!L.total || !int8_type(type)) return fail(FISH_HIP_ERR_ARG, "quantize_for: not an int8-path type");
+    const hipError_t e =
+        launch_quantize(x, n_tok, n_in, n_in, act, nullptr, nullptr, as_stream(stream), planes_of(L, n_tok));
+    return e == hipSuccess ? 0 : hip_fail(e, "quantize_for");
+}
+
 uint64_t fish_hip_weight_bytes(uint32_t type, int n_in, int n_out) {
     return f32path_type(type) ? f32path_bytes(type, n_in, n_out) : weight_layout(type, n_in, n_out).total;
 }
@@ -1102,7 +1123,7 @@ int fish_hip_matmul_tensors(uint32_t type, int n, const void* const* ws, const f
         if (!act_workspace || act_workspace_bytes < act_layout(n_tok, n_in).total)
             return fail(FISH_HIP_ERR_ARG, "matmul_tensors: act_workspace missing or too small");
         e = launch_quantize(x, n_tok, n_in, n_in, act_workspace, nullptr, nullptr, as_stream(stream),
-                            planes_for_tokens(n_tok, n_in));
+                            planes_of(L[0], n_tok));
         if (e == hipSuccess) {
             const int rc = fish_hip_matmul_group(type, n, ws, act_workspace, n_tok, n_in, n_outs, ys, stream);
             if (rc != 0) return rc;

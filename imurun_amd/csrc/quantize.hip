@@ -42,6 +42,9 @@ __device__ __forceinline__ int mfma_offset(int lane) {
 }
 
 // One (token, 256-value chunk) in registers -> every requested layout.
+// GEMM_ONLY: the K-quant GEMM's planes (gA gX gJ) alone, with no run-time checks
+// of the other outputs (n_in a multiple of 256).
+template <bool GEMM_ONLY>
 __device__ __forceinline__ void quantize_chunk(float4 v, int t, int c, int n_tok, int n_in, const QuantOut& o,
                                                int lane) {
     const int k0 = c * 256 + lane * 4;
@@ -49,8 +52,9 @@ __device__ __forceinline__ void quantize_chunk(float4 v, int t, int c, int n_tok
     const bool active = real && k0 < n_in;  // n_in % 32 == 0: whole 8-lane groups switch together
     const float a = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
 
-    // ---- 32-value blocks
-    {
+    // ---- 32-value blocks (skipped when no 32-layout plane is requested: a K-quant
+    // GEMM's input needs only the 256-value planes)
+    if (!GEMM_ONLY && (o.q32 || o.m32 || o.d32 || o.aos32)) {
         const float amax = wave_max8(a);
         const float d = amax / 127.0f;
         const float id = d > 0.0f ? 1.0f / d : 0.0f;
@@ -78,7 +82,7 @@ __device__ __forceinline__ void quantize_chunk(float4 v, int t, int c, int n_tok
     }
 
     // ---- 256-value blocks (only when every row is a whole number of them)
-    if ((o.d256 || o.gA || o.aos256) && (n_in % 256) == 0) {
+    if (GEMM_ONLY || ((o.d256 || o.gA || o.aos256) && (n_in % 256) == 0)) {
         const float amax = wave_max64(a);
         const float d = amax / 127.0f;
         const float id = d > 0.0f ? 1.0f / d : 0.0f;
@@ -88,7 +92,7 @@ __device__ __forceinline__ void quantize_chunk(float4 v, int t, int c, int n_tok
         const int g16 = wave_sum4(s4);
         const int g32 = g16 + dpp_i<kDppHalfMirror>(g16);
         const uint32_t packed = pack4(q0, q1, q2, q3);
-        if (o.gA) {
+        if (GEMM_ONLY || o.gA) {
             // 32x32x32 MFMA planes: token block tb, step k0 / 32, half h, 4-byte slot of the lane
             const int n_sb = n_in / 256, tb = t >> 5, tt = t & 31;
             const size_t step = size_t(k0 >> 5), h = size_t((lane & 7) >> 2);
@@ -103,7 +107,7 @@ __device__ __forceinline__ void quantize_chunk(float4 v, int t, int c, int n_tok
                 o.gJ[(blk * 64 + 32 + tt) * 8 + g] = __builtin_bit_cast(uint16_t, _Float16(float(g32 & 63)));
             }
         }
-        if (!real) return;
+        if (GEMM_ONLY || !real) return;
         if (o.q256) *reinterpret_cast<uint32_t*>(o.q256 + size_t(t) * n_in + k0) = packed;
         if (o.m256)
             *reinterpret_cast<uint32_t*>(o.m256 + size_t(t) * n_in + size_t(c) * 256 + mfma_offset(lane)) = packed;
@@ -127,7 +131,7 @@ __device__ __forceinline__ void quantize_chunk(float4 v, int t, int c, int n_tok
 // One wavefront per (token, run of CPW consecutive chunks): the run's loads are
 // all issued before the first chunk is quantized, so each wavefront keeps
 // CPW KB (2 CPW KB with u) in flight.
-template <int CPW>
+template <int CPW, bool GEMM_ONLY>
 __global__ __launch_bounds__(256) void quantize_kernel(const float* __restrict__ x, int n_tok, int n_in, int ldx,
                                                        QuantOut o, const float* __restrict__ u,
                                                        float* __restrict__ h_out) {
@@ -159,7 +163,7 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float* __restrict__
     }
 #pragma unroll
     for (int j = 0; j < CPW; ++j)
-        if (c0 + j < chunks) quantize_chunk(v[j], t, c0 + j, n_tok, n_in, o, lane);
+        if (c0 + j < chunks) quantize_chunk<GEMM_ONLY>(v[j], t, c0 + j, n_tok, n_in, o, lane);
 }
 
 }  // namespace
@@ -187,14 +191,26 @@ hipError_t launch_quantize(const float* x, int n_tok, int n_in, int ldx, void* a
     o.aos32 = static_cast<uint8_t*>(aos32);
     o.aos256 = L.has256 ? static_cast<uint8_t*>(aos256) : nullptr;
     const long rows = gemm ? L.n_tb * 32 : n_tok, chunks = (n_in + 255) / 256;
+    // the GEMM's planes alone (a K-quant prefill): the kernel without the other layouts' code
+    const bool gemm_only = gemm && !gemv && !b32 && !b256 && !o.aos32 && !o.aos256;
     // four chunks per wavefront only for the largest launches (measured: 6 % faster at 512 x 14336;
     // at 64 x 4096 or 512 x 4096 one chunk per wavefront is faster, the chain per chunk dominating)
     if (rows * chunks >= 16384) {
         const unsigned blocks = unsigned((rows * ((chunks + 3) / 4) + 3) / 4);
-        hipLaunchKernelGGL(quantize_kernel<4>, dim3(blocks), dim3(256), 0, stream, x, n_tok, n_in, ldx, o, u, h_out);
+        if (gemm_only)
+            hipLaunchKernelGGL((quantize_kernel<4, true>), dim3(blocks), dim3(256), 0, stream, x, n_tok, n_in, ldx, o,
+                               u, h_out);
+        else
+            hipLaunchKernelGGL((quantize_kernel<4, false>), dim3(blocks), dim3(256), 0, stream, x, n_tok, n_in, ldx,
+                               o, u, h_out);
     } else {
         const unsigned blocks = unsigned((rows * chunks + 3) / 4);
-        hipLaunchKernelGGL(quantize_kernel<1>, dim3(blocks), dim3(256), 0, stream, x, n_tok, n_in, ldx, o, u, h_out);
+        if (gemm_only)
+            hipLaunchKernelGGL((quantize_kernel<1, true>), dim3(blocks), dim3(256), 0, stream, x, n_tok, n_in, ldx, o,
+                               u, h_out);
+        else
+            hipLaunchKernelGGL((quantize_kernel<1, false>), dim3(blocks), dim3(256), 0, stream, x, n_tok, n_in, ldx,
+                               o, u, h_out);
     }
     return hipGetLastError();
 }

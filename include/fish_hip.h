@@ -83,6 +83,15 @@ FISH_HIP_API int fish_hip_quantize_rows(uint32_t type, const float* x, void* dst
 FISH_HIP_API int fish_hip_quantize(const float* x, int n_tok, int n_in, void* act, void* q32_fish, void* q256_fish,
                                    void* stream);
 
+/* fish_hip_quantize for the matmuls of one int8-path weight type at n_tok
+ * tokens: only the planes that type's kernel reads (the K-quant GEMM, for
+ * instance, reads none of the 32-value planes). The same buffer size
+ * (fish_hip_act_bytes). ActBatch::quantize (ops.cpp:158-175) builds both of
+ * FISH's layouts because its consumer is not known yet; a caller that knows
+ * it (the device backend's matmul_tensors path, ops.cpp:283-299) skips the
+ * work. Returns 0, or FISH_HIP_ERR_ARG for a type outside the int8 path. */
+FISH_HIP_API int fish_hip_quantize_for(uint32_t type, const float* x, int n_tok, int n_in, void* act, void* stream);
+
 /* Upload-time repack of GGUF rows already in device memory (n_out rows of
  * ggml_row_size(type, n_in) bytes) into the device layout at w (the device
  * side of ComputeBackend::upload, backend.h:41-42). */

@@ -62,6 +62,10 @@ def test_bad_arguments_return_errors_without_device_work():
     assert L.fish_hip_supports(fh.Q4_K) == 1 and L.fish_hip_supports(fh.Q5_K) == 1
     assert all(L.fish_hip_supports(t) == 1 for t in fh.F32_PATH_TYPES)
     assert L.fish_hip_supports(9) == 0 and L.fish_hip_supports(23) == 0  # Q8_1, IQ4_XS
+    # quantize_for: only int8-path types, refused before any device work
+    assert L.fish_hip_quantize_for(fh.Q4_1, 1 << 20, 1, 256, 1 << 20, None) == -1
+    assert L.fish_hip_quantize_for(fh.Q4_K, 1 << 20, 1, 4000, 1 << 20, None) == -1  # 32-blocks only
+    assert L.fish_hip_quantize_for(fh.Q4_K, 1 << 20, 1, 4064, 1 << 20, None) == -1  # not whole 256s
     # a type without a block writer is refused
     assert L.fish_hip_quantize_rows(fh.Q4_1, 1 << 20, 1 << 20, 1, 256, 1) == -1
     # f32-path types: only fish_hip_matmul_tensors and the backend take them

@@ -126,6 +126,29 @@ def test_matmul_matches_oracle(torch_dev, oracle, t, n_tok):
 
 
 @pytest.mark.parametrize("t", TYPES)
+@pytest.mark.parametrize("n_in", [1024, 736])
+@pytest.mark.parametrize("n_tok", [1, 4, 5, 64, 65, 130])
+def test_quantize_for_type_feeds_the_same_matmul(torch_dev, oracle, t, n_in, n_tok):
+    """fish_hip_quantize_for writes only the planes that the type's kernel at n_tok reads:
+    the matmul on it equals the matmul on the full quantization bit for bit. Its buffer
+    starts as 0xA5 bytes, so a plane read but not written would show as a difference."""
+    if fh.BLOCK_ELEMS[t] == 256 and n_in % 256:
+        pytest.skip("K-quant rows are whole 256-value blocks")
+    torch, d = torch_dev
+    n_out = 96
+    rows = packed_weights(oracle, t, n_out, n_in, 1300 + n_tok)
+    x = dev_f32(torch_dev, normal(1400 + n_tok, (n_tok, n_in)))
+    w = fh.repack(t, dev_u8(torch_dev, rows), n_in, n_out)
+    full = fh.quantize(x)
+    part = torch.full((fh.act_bytes(n_tok, n_in),), 0xA5, dtype=torch.uint8, device=d)
+    fh.quantize(x, act=part, for_type=t)
+    y_full = fh.matmul(t, w, full, n_tok, n_in, n_out).cpu().numpy()
+    y_part = fh.matmul(t, w, part, n_tok, n_in, n_out).cpu().numpy()
+    assert np.array_equal(y_full.view(np.uint32), y_part.view(np.uint32)), f"{fh.TYPE_NAMES[t]} M={n_tok}"
+    check_close(y_part, oracle.matmul_f32(t, rows, x.cpu().numpy(), n_out), f"{fh.TYPE_NAMES[t]} M={n_tok}")
+
+
+@pytest.mark.parametrize("t", TYPES)
 @pytest.mark.parametrize("n_tok", [5, 16, 17, 33, 64, 100])
 def test_batch_tiles_match_oracle(torch_dev, oracle, t, n_tok):
     """Token counts across the MFMA batch kernel's 16/32/64-token workgroups
