@@ -723,8 +723,11 @@ private:
                 const RowResid ro{B.x, span_vec(l, 7)};
                 const RowNorm fn{span_vec(l, 1), B.xb2, sp_.eps};
                 e = run_group(W + 3, 1, B.att, n_tok, Q, n_e, y_o, act, nullptr, &ro);
-                if (e == hipSuccess) e = run_group(W + 4, 2, B.x, n_tok, E, n_f, y_gu, act, &fn);
-                if (e == hipSuccess) e = launch_silu_mul(B.g, B.u, T * F, stream_, sp_.gelu != 0);
+                // gate and up of one type and shape: the activation is the launch's epilogue
+                const WeightLayout gu[2] = {W[4]->layout, W[5]->layout};
+                const int pair = gemv_x_pair_supported(gu) ? (sp_.gelu ? kActGelu : kActSilu) : kActNone;
+                if (e == hipSuccess) e = run_group(W + 4, 2, B.x, n_tok, E, n_f, y_gu, act, &fn, nullptr, pair);
+                if (e == hipSuccess && pair == kActNone) e = launch_silu_mul(B.g, B.u, T * F, stream_, sp_.gelu != 0);
                 const RowResid rd{B.x, nullptr};
                 if (e == hipSuccess) e = run_group(W + 6, 1, B.g, n_tok, F, n_e, y_d, act, nullptr, &rd);
                 continue;
@@ -819,10 +822,11 @@ private:
         return true;
     }
 
-    // norm (one token, foldable tensors only): the RowNorm prologue of every fused launch
+    // norm (one token, foldable tensors only): the RowNorm prologue of every fused launch;
+    // pair_act (gate and up of one type and shape, with a norm): dys[0] = act(gate) * up
     hipError_t run_group(const Resident* const* rs, int n, const float* dx, int n_tok, int n_in, const int* n_outs,
                          float* const* dys, void* act, const RowNorm* norm = nullptr,
-                         const RowResid* resid = nullptr) {
+                         const RowResid* resid = nullptr, int pair_act = kActNone) {
         if ((norm || resid) && (n_tok != 1 || n > kGemmGroupMax || !foldable(rs, n))) return hipErrorInvalidValue;
         if (resid && n != 1) return hipErrorInvalidValue;
         bool any_int8 = false;
@@ -831,6 +835,7 @@ private:
         bool fused = n_tok == 1 && n <= kGemmGroupMax && int8_type(rs[0]->layout.type) &&
                      gemv_x_supported(rs[0]->layout);
         for (int i = 1; i < n && fused; ++i) fused = rs[i]->layout.type == rs[0]->layout.type;
+        if (pair_act != kActNone && !fused) return hipErrorInvalidValue;
         // one token, int8 types mixed (q/k in Q4_K, v in Q6_K): one fused launch per type
         bool per_type = !fused && n_tok == 1 && n <= kGemmGroupMax;
         for (int i = 0; i < n && per_type; ++i)
@@ -883,7 +888,7 @@ private:
                 ws[i] = rs[size_t(i)]->dev;
                 Ls[i] = rs[size_t(i)]->layout;
             }
-            e = launch_gemv_x(n, ws, Ls, dx, dys, stream_, norm, resid);
+            e = launch_gemv_x(n, ws, Ls, dx, dys, stream_, norm, resid, pair_act);
         } else if (e == hipSuccess && one_group) {
             const void* ws[kGemmGroupMax];
             WeightLayout Ls[kGemmGroupMax];

@@ -229,6 +229,7 @@ struct GemvXGroup {
     int n;
     RowNorm norm;               // norm.w == nullptr: x as given
     RowResid resid;             // resid.x == nullptr: y only
+    int pair_act;               // kActNone, or gate / up pairs: y[0] = act(gate) * up
 };
 
 // The RowNorm prologue on the workgroup's x chunks (thread tid holds values
@@ -264,18 +265,21 @@ __device__ __forceinline__ void row_norm(float4 (&xv)[XV], const RowNorm& nm, in
     }
 }
 
-// The rows of group member gm for workgroup wg of that member, on x held as
-// the float4 chunks xv (loaded by the caller before anything else).
-template <uint32_t T, int LPR, int MAXC, int XV, bool NORM>
-__device__ __forceinline__ void gemv_x_rows(const GemvXGroup& G, int gm, int wg, float4 (&xv)[XV], int n_in,
-                                            uint4* s_codes, float* s_d, int* s_s, double* s_red) {
+// The rows of group member gm for wavefront wave_id of that member, on x held
+// as the float4 chunks xv (loaded by the caller before anything else).
+// PAIR: the workgroup's first half of wavefronts holds gate rows (member 0),
+// the second half the same rows of up (member 1); up's results reach the gate
+// wavefronts through s_pair, which write act(gate) * up, and up is stored.
+template <uint32_t T, int LPR, int MAXC, int XV, bool NORM, bool PAIR = false>
+__device__ __forceinline__ void gemv_x_rows(const GemvXGroup& G, int gm, int wave_id, float4 (&xv)[XV], int n_in,
+                                            uint4* s_codes, float* s_d, int* s_s, double* s_red,
+                                            float* s_pair = nullptr) {
     constexpr bool kq = kquant_type(T);
     constexpr int RPP = 64 / LPR;
     constexpr int RB = gemv_rb<T, MAXC>();
     const int tid = threadIdx.x, lane = tid & 63, sub = lane % LPR;
     const WeightPtrs W = G.w[gm];
     const int n_out = G.n_out[gm];
-    const int wave_id = wg * kGemvXWaves + (tid >> 6);
     const int row_base = wave_id * (RPP * RB) + lane / LPR;
     const int groups = n_in / 32;
 
@@ -306,7 +310,9 @@ __device__ __forceinline__ void gemv_x_rows(const GemvXGroup& G, int gm, int wg,
     const LdsAct L{s_codes, s_d, s_s, kGemvXMaxGroups};
     quantize_to_lds<kq, XV, 64 * kGemvXWaves>(xv, n_in, tid, L);
     __syncthreads();
-    if (wave_id * (RPP * RB) >= n_out) return;  // uniform over the wavefront
+    // (a pair's wavefronts all reach its second barrier; their rows past the end are
+    // clamped loads whose results are not stored)
+    if (!PAIR && wave_id * (RPP * RB) >= n_out) return;  // uniform over the wavefront
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
@@ -325,6 +331,28 @@ __device__ __forceinline__ void gemv_x_rows(const GemvXGroup& G, int gm, int wg,
         }
     }
     float* __restrict__ y = G.y[gm];
+    if constexpr (PAIR) {
+        const int slot = (wave_id % (kGemvXWaves / 2)) * (RPP * RB) + lane / LPR;
+        float v[RB];
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+            v[rb] = acc[rb];
+#pragma unroll
+            for (int off = LPR / 2; off > 0; off >>= 1) v[rb] += __shfl_xor(v[rb], off);
+            if (gm == 1 && sub == 0) {
+                s_pair[slot + rb * RPP] = v[rb];
+                if (row_base + rb * RPP < n_out) y[row_base + rb * RPP] = v[rb];
+            }
+        }
+        __syncthreads();
+        if (gm == 0 && sub == 0) {
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb)
+                if (row_base + rb * RPP < n_out)
+                    y[row_base + rb * RPP] = act_mul(v[rb], s_pair[slot + rb * RPP], G.pair_act == kActGelu);
+        }
+        return;
+    }
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
         float v = acc[rb];
@@ -349,6 +377,10 @@ __device__ __forceinline__ int gemv_x_member(const GemvXGroup& G, int& wg) {
     return gm;
 }
 
+// The wavefront's index in its workgroup, as a scalar (uniform over the
+// wavefront), so row indices derived from it take no vector registers.
+__device__ __forceinline__ int wave_index() { return __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6)); }
+
 // x loads first: unconditional, from a clamped address (chunks past the end lie in
 // whole 32/256-value blocks the quantizer discards, and a load inside a branch would
 // make the compiler wait for every outstanding load at the join)
@@ -372,7 +404,32 @@ __global__ __launch_bounds__(64 * kGemvXWaves) void gemv_x_kernel(GemvXGroup G, 
     const int gm = gemv_x_member(G, wg);
     float4 xv[XV];
     gemv_x_loads<XV>(x, n_in, xv);
-    gemv_x_rows<T, LPR, MAXC, XV, NORM>(G, gm, wg, xv, n_in, s_codes, s_d, s_s, s_red);
+    gemv_x_rows<T, LPR, MAXC, XV, NORM>(G, gm, wg * kGemvXWaves + wave_index(), xv, n_in, s_codes, s_d,
+                                        s_s, s_red);
+}
+
+// A layer's gate and up (one type and shape) with the FFN activation in the
+// epilogue: workgroup wg computes rows wg * 8 RB .. of both, and writes
+// y[0] = act(gate) * up (FISH's silu / gelu, then the product) and y[1] = up,
+// so no separate activation launch runs (model.cpp:1504-1508).
+// (Q4_0 / Q8_0 / Q4_K rows of up to two groups per lane: registers for two
+// workgroups per CU, as the launch without the epilogue has; the others would spill)
+template <uint32_t T, int LPR, int MAXC, int XV>
+__global__ __launch_bounds__(64 * kGemvXWaves) __attribute__((
+    amdgpu_waves_per_eu(MAXC <= 2 && T != kQ5_K && T != kQ6_K ? 8 : 1))) void gemv_xp_kernel(GemvXGroup G,
+                                                                                           const float* __restrict__ x,
+                                                                                           int n_in) {
+    constexpr int HALF = kGemvXWaves / 2;
+    __shared__ uint4 s_codes[2 * kGemvXMaxGroups];
+    __shared__ float s_d[kGemvXMaxGroups];
+    __shared__ int s_s[kGemvXMaxGroups];
+    __shared__ double s_red[kGemvXWaves];
+    __shared__ float s_pair[HALF * (64 / LPR) * gemv_rb<T, MAXC>()];
+    const int wave = wave_index();
+    float4 xv[XV];
+    gemv_x_loads<XV>(x, n_in, xv);
+    gemv_x_rows<T, LPR, MAXC, XV, true, true>(G, wave / HALF, int(blockIdx.x) * HALF + wave % HALF, xv, n_in,
+                                              s_codes, s_d, s_s, s_red, s_pair);
 }
 
 // Two K-quant types in one launch (a layer's q / k in Q4_K and v in Q6_K): both
@@ -390,10 +447,11 @@ __global__ __launch_bounds__(64 * kGemvXWaves) void gemv_x2_kernel(GemvXGroup G,
     const int gm = gemv_x_member(G, wg);
     float4 xv[XV];
     gemv_x_loads<XV>(x, n_in, xv);
+    const int wave_id = wg * kGemvXWaves + wave_index();
     if (G.type[gm] == T1)
-        gemv_x_rows<T1, LPR, MAXC, XV, NORM>(G, gm, wg, xv, n_in, s_codes, s_d, s_s, s_red);
+        gemv_x_rows<T1, LPR, MAXC, XV, NORM>(G, gm, wave_id, xv, n_in, s_codes, s_d, s_s, s_red);
     else
-        gemv_x_rows<T2, LPR, MAXC, XV, NORM>(G, gm, wg, xv, n_in, s_codes, s_d, s_s, s_red);
+        gemv_x_rows<T2, LPR, MAXC, XV, NORM>(G, gm, wave_id, xv, n_in, s_codes, s_d, s_s, s_red);
 }
 
 // rows per wavefront of type t at MAXC groups per lane (gemv_rb)
@@ -427,6 +485,17 @@ hipError_t gemv_x_launch(GemvXGroup G, const float* x, int n_in, hipStream_t s) 
     static_assert(gemv_rb<T, MAXC>() >= 1, "rows per wavefront");
     constexpr int TH = 64 * kGemvXWaves;
     constexpr int XV = gemv_x_xv<LPR, MAXC>();
+    if (G.pair_act) {
+        // gate / up pairs: half the wavefronts of a workgroup per member, the same rows
+        if constexpr (MAXC <= 4) {
+            constexpr int RPW = (64 / LPR) * gemv_rb<T, MAXC>();
+            const int wgs = (G.n_out[0] + (kGemvXWaves / 2) * RPW - 1) / ((kGemvXWaves / 2) * RPW);
+            hipLaunchKernelGGL((gemv_xp_kernel<T, LPR, MAXC, XV>), dim3(unsigned(wgs)), dim3(TH), 0, s, G, x, n_in);
+            return hipGetLastError();
+        } else {
+            return hipErrorInvalidValue;
+        }
+    }
     const int wgs = gemv_x_grid<LPR, MAXC>(G);
     if (G.norm.w) {
         // rows of up to 4 groups per lane (n_in <= 8192): the prologue spills registers beyond
@@ -575,13 +644,23 @@ bool gemv_x_mixed_supported(int n, const WeightLayout* WLs) {
     return a != b && gemv_x2_pair(a, b) && n_in / 32 >= 64 && (n_in / 32 + 63) / 64 <= 4;
 }
 
+bool gemv_x_pair_supported(const WeightLayout* WLs) {
+    const WeightLayout &a = WLs[0], &b = WLs[1];
+    return gemv_x_supported(a) && b.total && a.type == b.type && a.n_in == b.n_in && a.n_out == b.n_out &&
+           (a.n_in / 32 + 63) / 64 <= 4 && a.n_in % 4 == 0;
+}
+
 hipError_t launch_gemv_x(int n, const void* const* ws, const WeightLayout* WLs, const float* x, float* const* ys,
-                         hipStream_t s, const RowNorm* norm, const RowResid* resid) {
+                         hipStream_t s, const RowNorm* norm, const RowResid* resid, int pair_act) {
     if (n <= 0 || n > kGemmGroupMax || !gemv_x_supported(WLs[0])) return hipErrorInvalidValue;
     if ((norm && (!norm->w || WLs[0].n_in % 4)) || (resid && (!resid->x || n != 1 || resid->x == x)))
         return hipErrorInvalidValue;
+    if (pair_act != kActNone &&
+        ((pair_act != kActSilu && pair_act != kActGelu) || n != 2 || !norm || resid || !gemv_x_pair_supported(WLs)))
+        return hipErrorInvalidValue;
     GemvXGroup G{};
     G.n = n;
+    G.pair_act = pair_act;
     if (norm) G.norm = *norm;
     if (resid) G.resid = *resid;
     bool mixed = false;

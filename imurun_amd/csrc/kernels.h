@@ -137,8 +137,14 @@ struct RowResid {
 // one launch when gemv_x_mixed_supported (n_in 2048..8192): both read the same
 // quantization of x.
 bool gemv_x_mixed_supported(int n, const WeightLayout* WLs);
+// Optional epilogue of a two-tensor launch with a RowNorm, the layer's gate and
+// up of one type and shape (gemv_x_pair_supported: n_in up to 8192): ys[0] =
+// act(gate) * up with FISH's float steps (model.cpp:1504-1508), ys[1] = up.
+enum : int { kActNone = 0, kActSilu = 1, kActGelu = 2 };
+bool gemv_x_pair_supported(const WeightLayout* WLs);
 hipError_t launch_gemv_x(int n, const void* const* ws, const WeightLayout* WLs, const float* x, float* const* ys,
-                         hipStream_t stream, const RowNorm* norm = nullptr, const RowResid* resid = nullptr);
+                         hipStream_t stream, const RowNorm* norm = nullptr, const RowResid* resid = nullptr,
+                         int pair_act = kActNone);
 
 // Few-token matmul on int8 MFMA (16x16 tiles), same token mapping as
 // launch_gemv; work-list items of up to kBatchItemTokens tokens. Needs

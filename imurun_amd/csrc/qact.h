@@ -139,4 +139,15 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
     return __fmul_rn(s, u);
 }
 
+// act(g) * u in FISH's float steps, each one rounding whatever the file's
+// contraction setting: SiLU as silu_mul, or the tanh GELU
+// 0.5 g (1 + tanh(sqrt(2/pi) (g + 0.044715 g^3))) (gelu_inplace, ops.cpp:32-38),
+// then times u (model.cpp:1504-1508).
+__device__ __forceinline__ float act_mul(float g, float u, bool gelu) {
+    if (!gelu) return silu_mul(g, u);
+    const float c = __fmul_rn(__fmul_rn(__fmul_rn(0.044715f, g), g), g);
+    const float t = tanhf(__fmul_rn(0.7978845608028654f, __fadd_rn(g, c)));
+    return __fmul_rn(__fmul_rn(__fmul_rn(0.5f, g), __fadd_rn(1.0f, t)), u);
+}
+
 }  // namespace fishhip

@@ -22,6 +22,7 @@
 // expf, within a few ulp of the C library's.
 #include "common.h"
 #include "kernels.h"
+#include "qact.h"
 
 namespace fishhip {
 
@@ -595,15 +596,7 @@ __global__ __launch_bounds__(kTh) void act_mul_kernel(float* __restrict__ g, con
                                                       int gelu) {
     const size_t i = size_t(blockIdx.x) * kTh + threadIdx.x;
     if (i >= n) return;
-    const float v = g[i];
-    float a;
-    if (gelu) {
-        const float k = 0.7978845608028654f;
-        a = 0.5f * v * (1.0f + tanhf(k * (v + 0.044715f * v * v * v)));
-    } else {
-        a = v / (1.0f + expf(-v));
-    }
-    g[i] = a * u[i];
+    g[i] = act_mul(g[i], u[i], gelu != 0);
 }
 
 // Row t of src [n_tok][w0 + w1 + w2] split into d0 [n_tok][w0], d1, d2 (a fused

@@ -159,7 +159,7 @@ class RefLayer:
 
 # per variant: weight types (a fused tensor has one type), span options
 VARIANT_TYPES = {"phi3": dict(TYPES, wv=fh.Q4_K)}
-VARIANT_OPTS = {"gemma2": dict(softcap=5.0, window=24, gelu=True)}
+VARIANT_OPTS = {"gemma2": dict(softcap=5.0, window=24, gelu=True), "gelu": dict(gelu=True)}
 
 
 def layer_extras(variant):
@@ -285,7 +285,7 @@ def check_call(be, ref, x, pos0, what):
 
 
 @pytest.mark.parametrize("rot_dim,variant", [(D, "llama"), (D // 2, "llama"), (D, "qwen3"), (D, "bias"),
-                                             (D, "phi3"), (D, "gemma2")])
+                                             (D, "phi3"), (D, "gemma2"), (D, "gelu")])
 def test_span_layer_matches_fish_forward(oracle, rot_dim, variant):
     be = fh.HipBackend()
     assert be.available()
@@ -312,7 +312,7 @@ def test_span_layer_matches_fish_forward(oracle, rot_dim, variant):
                 att, qr = be.span_inspect("att", Q), be.span_inspect("qr", Q)
                 kc = be.span_inspect("kc", KV, 0, 0, pos0 + n)
                 vc = be.span_inspect("vc", KV, 0, 0, pos0 + n)
-                for drop in ("softcap", "window"):
+                for drop in [k for k in ("softcap", "window") if k in ref.opts]:
                     alt = RefLayer(oracle, packed, an, fn, cos, sin, extras=extras, types=ref.types,
                                    opts={k: v for k, v in ref.opts.items() if k != drop})
                     t, p = n - 1, pos0 + n - 1
@@ -330,6 +330,31 @@ def test_span_layer_matches_fish_forward(oracle, rot_dim, variant):
         x0 = x.copy()
         assert not be.span_forward(x, pos0)
         assert np.array_equal(x, x0)
+    finally:
+        be.span_release()
+        for n in names:
+            be.release(n)
+
+
+@pytest.mark.parametrize("e_dim,variant", [(2048, "gelu"), (4096, "llama")])
+def test_span_decode_at_model_width(oracle, monkeypatch, e_dim, variant):
+    """One-token calls at model widths: the gate/up launch then runs 64 lanes per row (one
+    and two groups per lane) with the activation in its epilogue, SiLU and GELU; every stage
+    is checked as above."""
+    import sys
+    mod = sys.modules[__name__]
+    monkeypatch.setattr(mod, "E", e_dim)
+    monkeypatch.setattr(mod, "SHAPES", dict(wq=(Q, e_dim), wk=(KV, e_dim), wv=(KV, e_dim), wo=(e_dim, Q),
+                                            wg=(F, e_dim), wu=(F, e_dim), wd=(e_dim, F)))
+    be = fh.HipBackend()
+    assert be.available()
+    names, ref, _ = setup_span(oracle, be, D, variant, f"wide{e_dim}")
+    try:
+        pos0 = 0
+        for i, n in enumerate((5, 1, 1, 1)):
+            x = normal(690 + i, (n, e_dim), 1.0)
+            check_call(be, ref, x, pos0, f"{variant} E={e_dim}")
+            pos0 += n
     finally:
         be.span_release()
         for n in names:
