@@ -713,12 +713,18 @@ private:
                     e = run_group(W, 3, B.xb, n_tok, E, n_qkv, y_qkv, act);
                 }
             }
-            if (e == hipSuccess)
+            if (e == hipSuccess && n_tok == 1) {
+                // one token: the attention workgroups prepare q and the new k / v rows themselves
+                e = launch_attention_prep(B.q, B.k, B.v, vecs, B.qr, kc, vc, B.att, B.sc, B.ld, H, HKV, D, sp_.rot_dim,
+                                          sp_.rope_neox != 0, sp_.eps, pos0, d_cos_, d_sin_, scale, stream_, pos_dev,
+                                          sp_.attn_softcap, window);
+            } else if (e == hipSuccess) {
                 e = launch_qkv_prep(B.q, B.k, B.v, vecs, B.qr, kc, vc, n_tok, H, HKV, D, sp_.rot_dim,
                                     sp_.rope_neox != 0, sp_.eps, pos0, d_cos_, d_sin_, stream_, pos_dev);
-            if (e == hipSuccess)
-                e = launch_attention(B.qr, kc, vc, B.att, B.sc, B.ld, n_tok, H, HKV, D, pos0, scale, stream_, pos_dev,
-                                     sp_.attn_softcap, window);
+                if (e == hipSuccess)
+                    e = launch_attention(B.qr, kc, vc, B.att, B.sc, B.ld, n_tok, H, HKV, D, pos0, scale, stream_,
+                                         pos_dev, sp_.attn_softcap, window);
+            }
             if (e == hipSuccess && fold) {
                 const RowResid ro{B.x, span_vec(l, 7)};
                 const RowNorm fn{span_vec(l, 1), B.xb2, sp_.eps};

@@ -205,6 +205,13 @@ size_t attention_scratch_floats(int n_tok, int H, int D, int ld);
 hipError_t launch_attention(const float* q, const _Float16* kc, const _Float16* vc, float* out, float* part, int ld,
                             int n_tok, int H, int HKV, int D, int pos0, float scale, hipStream_t s,
                             const int* pos_dev = nullptr, float softcap = 0.0f, int window = 0);
+// One token: launch_qkv_prep and launch_attention in one step (the attention
+// workgroups prepare q, and the position's k / v rows, themselves).
+hipError_t launch_attention_prep(const float* q, const float* k, const float* v, const SpanVecs& vecs, float* q_out,
+                                 _Float16* kc, _Float16* vc, float* out, float* part, int ld, int H, int HKV, int D,
+                                 int rot_dim, bool neox, float eps, int pos0, const float* cosv, const float* sinv,
+                                 float scale, hipStream_t s, const int* pos_dev = nullptr, float softcap = 0.0f,
+                                 int window = 0);
 hipError_t launch_silu_mul(float* g, const float* u, size_t n, hipStream_t s, bool gelu = false);
 hipError_t launch_split_rows(const float* src, int n_tok, float* d0, int w0, float* d1, int w1, float* d2, int w2,
                              hipStream_t s);

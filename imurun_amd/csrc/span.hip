@@ -88,25 +88,75 @@ __global__ __launch_bounds__(kNormTh) void rmsnorm_kernel(float* __restrict__ x,
     for (int i = threadIdx.x; i < n; i += kNormTh) orow[i] = xr[i] * scale * w[i];
 }
 
-// RoPE of element d of one head of D values held in LDS (ops.cpp:126-152).
-__device__ __forceinline__ float rope_elem(const float* __restrict__ row, int d, int half, int neox,
-                                           const float* __restrict__ c, const float* __restrict__ s) {
-    if (d >= 2 * half) return row[d];  // past rot_dim: unchanged
-    if (neox) {
-        const int i = d < half ? d : d - half;
-        const float x0 = row[i], x1 = row[i + half];
-        return d < half ? x0 * c[i] - x1 * s[i] : x0 * s[i] + x1 * c[i];
+// One head of a token, thread d owning element d (D <= kTh): its inputs, loaded
+// first (head_load), then prepared by the whole workgroup (head_prep): value +
+// bias, the per-head RMS norm when given (the rmsnorm of ops.cpp:18-23 over the
+// head's D values, the squares summed in double over a fixed tree), then RoPE
+// (ops.cpp:126-152: pairs (i, i + half) with NEOX, else (2i, 2i + 1); elements
+// past 2 half unchanged). The loads and the arithmetic are apart so that a
+// caller can issue other loads in between without waiting for them.
+struct HeadIn {
+    float x, b, w, c, s;  // value, bias, norm weight, RoPE cos / sin of the element's pair
+};
+
+__device__ __forceinline__ HeadIn head_load(const float* __restrict__ src_row, const float* __restrict__ bias,
+                                            const float* __restrict__ nw, int head, int D, int half, int neox,
+                                            const float* __restrict__ c, const float* __restrict__ s) {
+    const int d = threadIdx.x;
+    HeadIn r{0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    if (d < D) {
+        r.x = src_row[head * D + d];
+        if (bias) r.b = bias[head * D + d];
+        if (nw) r.w = nw[d];
+        if (d < 2 * half) {
+            const int i = neox ? (d < half ? d : d - half) : d >> 1;
+            r.c = c[i];
+            r.s = s[i];
+        }
     }
-    const int i = d >> 1;
-    const float x0 = row[2 * i], x1 = row[2 * i + 1];
-    return (d & 1) ? x0 * s[i] + x1 * c[i] : x0 * c[i] - x1 * s[i];
+    return r;
+}
+
+// Element d of the prepared head (d < D). row and red are LDS of kTh entries;
+// every thread of the workgroup calls this.
+__device__ __forceinline__ float head_prep(const HeadIn& in, bool has_bias, bool has_norm, int D, int half, int neox,
+                                           float eps, float* row, double* red) {
+    const int d = threadIdx.x;
+    float val = 0.0f;
+    if (d < D) val = has_bias ? in.x + in.b : in.x;
+    if (has_norm) {  // uniform over the workgroup
+        red[d] = d < D ? double(val) * double(val) : 0.0;
+        __syncthreads();
+        for (int st = kTh / 2; st > 0; st >>= 1) {
+            if (d < st) red[d] += red[d + st];
+            __syncthreads();
+        }
+        const float scale = 1.0f / sqrtf(float(red[0] / D) + eps);
+        if (d < D) val = val * scale * in.w;
+    }
+    row[d] = val;
+    __syncthreads();
+    float r = 0.0f;
+    if (d < D) {
+        if (d >= 2 * half) {
+            r = row[d];
+        } else if (neox) {
+            const int i = d < half ? d : d - half;
+            const float x0 = row[i], x1 = row[i + half];
+            r = d < half ? x0 * in.c - x1 * in.s : x0 * in.s + x1 * in.c;
+        } else {
+            const int i = d >> 1;
+            const float x0 = row[2 * i], x1 = row[2 * i + 1];
+            r = (d & 1) ? x0 * in.s + x1 * in.c : x0 * in.c - x1 * in.s;
+        }
+    }
+    __syncthreads();  // row is free again on return
+    return r;
 }
 
 // One workgroup per (token t, head): q heads first, then k heads (whose
-// workgroup also stores the v head of the same index). Thread d owns element d
-// of the head (D <= kTh): value + bias, the per-head RMS norm when given (the
-// rmsnorm of ops.cpp:18-23 over the head's D values), RoPE; q -> q_out, k and
-// v -> f16 cache rows of position pos0 + t.
+// workgroup also stores the v head of the same index); prep_head, then q ->
+// q_out, k and v -> f16 cache rows of position pos0 + t.
 __global__ __launch_bounds__(kTh) void qkv_prep_kernel(const float* __restrict__ q, const float* __restrict__ k,
                                                        const float* __restrict__ v, SpanVecs vecs,
                                                        float* __restrict__ q_out, _Float16* __restrict__ kc,
@@ -123,27 +173,10 @@ __global__ __launch_bounds__(kTh) void qkv_prep_kernel(const float* __restrict__
     const float* src = is_q ? q + size_t(t) * Q : k + size_t(t) * KV;
     const float* bias = is_q ? vecs.bias_q : vecs.bias_k;
     const float* nw = is_q ? vecs.q_norm : vecs.k_norm;
-    float val = 0.0f;
-    if (d < D) {
-        val = src[head * D + d];
-        if (bias) val = val + bias[head * D + d];
-    }
-    if (nw) {  // uniform over the workgroup
-        red[d] = d < D ? double(val) * double(val) : 0.0;
-        __syncthreads();
-        for (int st = kTh / 2; st > 0; st >>= 1) {
-            if (d < st) red[d] += red[d + st];
-            __syncthreads();
-        }
-        const float scale = 1.0f / sqrtf(float(red[0] / D) + eps);
-        if (d < D) val = val * scale * nw[d];
-    }
-    row[d] = val;
-    __syncthreads();
+    const HeadIn in = head_load(src, bias, nw, head, D, half, neox, cosv + size_t(pos) * half,
+                                sinv + size_t(pos) * half);
+    const float r = head_prep(in, bias != nullptr, nw != nullptr, D, half, neox, eps, row, red);
     if (d >= D) return;
-    const float* c = cosv + size_t(pos) * half;
-    const float* s = sinv + size_t(pos) * half;
-    const float r = rope_elem(row, d, half, neox, c, s);
     if (is_q) {
         q_out[size_t(t) * Q + head * D + d] = r;
     } else {
@@ -186,16 +219,37 @@ __device__ __forceinline__ float score(float dot, float scale, float softcap) {
     return softcap > 0.0f ? softcap * tanhf(s / softcap) : s;
 }
 
-template <int NP>
+// PREP (one token): the workgroup prepares its q head from the raw projection
+// itself (prep_head, as qkv_prep_kernel), and the workgroups of the chunk that
+// holds the token's position also prepare that position's k and v rows (the
+// same f16 values the cache gets) and use them in place of the cache rows; of
+// those, the first q head of each KV group stores the rows into the caches and
+// every one stores its q head into q_out. No separate preparation launch.
+struct AttnPrep {
+    const float *q, *k, *v;  // raw projections of the token
+    SpanVecs vecs;
+    float* q_out;
+    _Float16 *kc, *vc;       // the caches, for the position's rows
+    const float *cosv, *sinv;
+    int half, neox;
+    float eps;
+};
+
+template <int NP, bool PREP>
 __global__ __launch_bounds__(kTh) void attn_part_kernel(const float* __restrict__ q, const _Float16* __restrict__ kc,
                                                         const _Float16* __restrict__ vc, float* __restrict__ part,
                                                         int S, int H, int HKV, int D, int pos0,
                                                         const int* __restrict__ pos_dev, float scale, float softcap,
-                                                        int window) {
+                                                        int window, AttnPrep P) {
     constexpr int PB = kCh / 4;
     __shared__ float s_e[kCh];
     __shared__ float s_o[4][128 * NP];
     __shared__ float s_ml[2];
+    // PREP: the prepared q head, the position's k / v rows (f16 pairs), scratch
+    __shared__ float s_q[PREP ? 128 * NP : 1];
+    __shared__ uint32_t s_kn[PREP ? 64 * NP : 1], s_vn[PREP ? 64 * NP : 1];
+    __shared__ float s_row[PREP ? kTh : 1];
+    __shared__ double s_red[PREP ? kTh : 1];
     if (pos_dev) pos0 = *pos_dev;
     const int item = blockIdx.x, chunk = blockIdx.y, t = item / H, h = item % H;
     const int pos = pos0 + t, kvh = h / (H / HKV), KV = HKV * D, Q = H * D;
@@ -213,15 +267,28 @@ __global__ __launch_bounds__(kTh) void attn_part_kernel(const float* __restrict_
         return;
     }
     const int jn = min(pos, j0 + kCh - 1);
-    float2 qv[NP];
-#pragma unroll
-    for (int i = 0; i < NP; ++i) {
-        const int e = 2 * (lane + 64 * i);
-        qv[i] = e < D ? *reinterpret_cast<const float2*>(q + size_t(t) * Q + size_t(h) * D + e) : make_float2(0.f, 0.f);
-    }
     const uint32_t* kb = reinterpret_cast<const uint32_t*>(kc + size_t(kvh) * D);
     const uint32_t* vb = reinterpret_cast<const uint32_t*>(vc + size_t(kvh) * D);
     const int KV2 = KV / 2;
+
+    // PREP: the inputs of the q head (and of the position's k / v rows) are loaded
+    // first, then the cache rows; the preparation waits only for its own loads
+    const bool own = PREP && jn == pos;  // this chunk holds the position (uniform)
+    HeadIn qin{}, kin{};
+    float v_x = 0.0f, v_b = 0.0f;
+    if constexpr (PREP) {
+        const float* c = P.cosv + size_t(pos) * P.half;
+        const float* sn = P.sinv + size_t(pos) * P.half;
+        qin = head_load(P.q + size_t(t) * Q, P.vecs.bias_q, P.vecs.q_norm, h, D, P.half, P.neox, c, sn);
+        if (own) {
+            kin = head_load(P.k + size_t(t) * KV, P.vecs.bias_k, P.vecs.k_norm, kvh, D, P.half, P.neox, c, sn);
+            if (tid < D) {
+                v_x = P.v[size_t(t) * KV + size_t(kvh) * D + tid];
+                if (P.vecs.bias_v) v_b = P.vecs.bias_v[size_t(kvh) * D + tid];
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
 
     // scores of positions j0 + w + 4 b
     uint32_t kv[PB][NP];
@@ -230,6 +297,51 @@ __global__ __launch_bounds__(kTh) void attn_part_kernel(const float* __restrict_
         const uint32_t* kr = kb + size_t(min(j0 + w + 4 * b, jn)) * KV2;
 #pragma unroll
         for (int i = 0; i < NP; ++i) kv[b][i] = 2 * (lane + 64 * i) < D ? kr[lane + 64 * i] : 0u;
+    }
+    float2 qv[NP];
+    if constexpr (PREP) {
+        __builtin_amdgcn_sched_barrier(0);
+        const float r = head_prep(qin, P.vecs.bias_q != nullptr, P.vecs.q_norm != nullptr, D, P.half, P.neox, P.eps,
+                                  s_row, s_red);
+        if (tid < D) {
+            s_q[tid] = r;
+            if (own) P.q_out[size_t(t) * Q + size_t(h) * D + tid] = r;
+        }
+        if (own) {
+            const float rk = head_prep(kin, P.vecs.bias_k != nullptr, P.vecs.k_norm != nullptr, D, P.half, P.neox,
+                                       P.eps, s_row, s_red);
+            if (tid < D) {
+                const _Float16 k16 = _Float16(rk), v16 = _Float16(P.vecs.bias_v ? v_x + v_b : v_x);
+                reinterpret_cast<_Float16*>(s_kn)[tid] = k16;
+                reinterpret_cast<_Float16*>(s_vn)[tid] = v16;
+                if (h % (H / HKV) == 0) {
+                    const size_t at = size_t(pos) * KV + size_t(kvh) * D + tid;
+                    P.kc[at] = k16;
+                    P.vc[at] = v16;
+                }
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < NP; ++i) {
+            const int e = 2 * (lane + 64 * i);
+            qv[i] = e < D ? make_float2(s_q[e], s_q[e + 1]) : make_float2(0.f, 0.f);
+        }
+        if (own) {
+#pragma unroll
+            for (int b = 0; b < PB; ++b)
+                if (min(j0 + w + 4 * b, jn) == pos)
+#pragma unroll
+                    for (int i = 0; i < NP; ++i)
+                        if (2 * (lane + 64 * i) < D) kv[b][i] = s_kn[lane + 64 * i];
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < NP; ++i) {
+            const int e = 2 * (lane + 64 * i);
+            qv[i] = e < D ? *reinterpret_cast<const float2*>(q + size_t(t) * Q + size_t(h) * D + e)
+                          : make_float2(0.f, 0.f);
+        }
     }
 #pragma unroll
     for (int b = 0; b < PB; ++b) {
@@ -269,6 +381,16 @@ __global__ __launch_bounds__(kTh) void attn_part_kernel(const float* __restrict_
         const uint32_t* vr = vb + size_t(min(j0 + w + 4 * b, jn)) * KV2;
 #pragma unroll
         for (int i = 0; i < NP; ++i) vv[b][i] = 2 * (lane + 64 * i) < D ? vr[lane + 64 * i] : 0u;
+    }
+    if constexpr (PREP) {
+        if (own) {
+#pragma unroll
+            for (int b = 0; b < PB; ++b)
+                if (min(j0 + w + 4 * b, jn) == pos)
+#pragma unroll
+                    for (int i = 0; i < NP; ++i)
+                        if (2 * (lane + 64 * i) < D) vv[b][i] = s_vn[lane + 64 * i];
+        }
     }
     float2 acc[NP];
 #pragma unroll
@@ -669,13 +791,34 @@ hipError_t launch_attention(const float* q, const _Float16* kc, const _Float16* 
     }
     const int S = (ld + kCh - 1) / kCh;
     const dim3 grid(unsigned(n_tok * H), unsigned(S));
+    const AttnPrep P{};
     if (D <= 128)
-        hipLaunchKernelGGL(attn_part_kernel<1>, grid, block, 0, s, q, kc, vc, part, S, H, HKV, D, pos0, pos_dev, scale,
-                           softcap, window);
+        hipLaunchKernelGGL((attn_part_kernel<1, false>), grid, block, 0, s, q, kc, vc, part, S, H, HKV, D, pos0,
+                           pos_dev, scale, softcap, window, P);
     else
-        hipLaunchKernelGGL(attn_part_kernel<2>, grid, block, 0, s, q, kc, vc, part, S, H, HKV, D, pos0, pos_dev, scale,
-                           softcap, window);
+        hipLaunchKernelGGL((attn_part_kernel<2, false>), grid, block, 0, s, q, kc, vc, part, S, H, HKV, D, pos0,
+                           pos_dev, scale, softcap, window, P);
     hipLaunchKernelGGL(attn_combine_kernel, dim3(unsigned(n_tok * H)), block, 0, s, part, out, S, H, D);
+    return hipGetLastError();
+}
+
+hipError_t launch_attention_prep(const float* q, const float* k, const float* v, const SpanVecs& vecs, float* q_out,
+                                 _Float16* kc, _Float16* vc, float* out, float* part, int ld, int H, int HKV, int D,
+                                 int rot_dim, bool neox, float eps, int pos0, const float* cosv, const float* sinv,
+                                 float scale, hipStream_t s, const int* pos_dev, float softcap, int window) {
+    if (D <= 0 || D > kTh || D % 2 || HKV <= 0 || H % HKV || ld < pos0 + 1 || rot_dim < 0 || rot_dim > D ||
+        rot_dim % 2)
+        return hipErrorInvalidValue;
+    const AttnPrep P{q, k, v, vecs, q_out, kc, vc, cosv, sinv, rot_dim / 2, neox ? 1 : 0, eps};
+    const int S = (ld + kCh - 1) / kCh;
+    const dim3 grid{unsigned(H), unsigned(S)}, block{unsigned(kTh)};
+    if (D <= 128)
+        hipLaunchKernelGGL((attn_part_kernel<1, true>), grid, block, 0, s, q_out, kc, vc, part, S, H, HKV, D, pos0,
+                           pos_dev, scale, softcap, window, P);
+    else
+        hipLaunchKernelGGL((attn_part_kernel<2, true>), grid, block, 0, s, q_out, kc, vc, part, S, H, HKV, D, pos0,
+                           pos_dev, scale, softcap, window, P);
+    hipLaunchKernelGGL(attn_combine_kernel, dim3(unsigned(H)), block, 0, s, part, out, S, H, D);
     return hipGetLastError();
 }
 
