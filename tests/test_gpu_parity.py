@@ -331,15 +331,16 @@ def test_backend_upload_matmul_group(torch_dev, oracle):
 
 @pytest.mark.parametrize("types", [(fh.Q4_K, fh.Q4_K, fh.Q6_K), (fh.Q5_K, fh.Q6_K, fh.Q5_K), (fh.Q6_K, fh.Q4_K, fh.Q5_K)],
                          ids=["q4k-q4k-q6k", "q5k-q6k-q5k", "three-types"])
-@pytest.mark.parametrize("n_in", [2048, 4096, 8192])
-def test_backend_one_token_mixed_types(torch_dev, oracle, types, n_in):
+@pytest.mark.parametrize("n_in,n_outs", [(2048, [1024, 256, 256]), (4096, [1024, 256, 256]),
+                                         (8192, [1024, 256, 256]), (4096, [4096, 1024, 1024])])
+def test_backend_one_token_mixed_types(torch_dev, oracle, types, n_in, n_outs):
     """One token through a q/k/v-shaped group of mixed K-quant types (a Q4_K_M layer's q, k in
     Q4_K and v in Q6_K): two types share one launch, each workgroup taking its tensor's type's
-    path on the same quantized x; a third type falls back to one launch per type. Bit-identical
-    to each tensor alone, and close to the oracle."""
+    path on the same quantized x; a third type falls back to one launch per type. Small groups
+    run half the rows per wavefront, Llama-3-8B's q/k/v the default. Bit-identical to each
+    tensor alone, and close to the oracle."""
     be = fh.HipBackend()
-    n_outs = [1024, 256, 256]
-    names = [f"mx{i}_{n_in}" for i in range(3)]
+    names = [f"mx{i}_{n_in}_{n_outs[0]}" for i in range(3)]
     packed = []
     for i, (name, t, n_out) in enumerate(zip(names, types, n_outs)):
         packed.append(packed_weights(oracle, t, n_out, n_in, 1600 + i + n_in))
