@@ -666,8 +666,8 @@ def run_kernel_only_gemm(args, torch, fh, dev):
 # the sources it was measured on
 _CSRC = os.path.join("imurun_amd", "csrc")
 TRAFFIC_SOURCES = {
-    "gemv": ["gemv.hip", "dots.h", "qact.h", "common.h", "repack.hip"],
-    "moe": ["moe.hip", "batch.hip", "quantize.hip", "dots.h", "qact.h", "common.h", "repack.hip"],
+    "gemv": ["gemv.hip", "rowdot.h", "dots.h", "qact.h", "common.h", "repack.hip"],
+    "moe": ["moe.hip", "batch.hip", "quantize.hip", "rowdot.h", "dots.h", "qact.h", "common.h", "repack.hip"],
 }
 
 
