@@ -424,8 +424,9 @@ public:
             p.n_head_kv <= 0 || p.n_head % p.n_head_kv || p.head_dim <= 0 || p.head_dim > 256 || p.head_dim % 2 || p.n_ff <= 0 ||
             p.n_ctx <= 0 || p.rot_dim < 0 || p.rot_dim > p.head_dim || p.rot_dim % 2 || !p.rope_cos || !p.rope_sin)
             return false;
-        if (p.kv_q8) return false;  // int8 KV cache: not kept here, FISH keeps per-matmul routing
         const int E = p.n_embd, Q = p.n_head * p.head_dim, KV = p.n_head_kv * p.head_dim, F = p.n_ff;
+        // the int8 cache keeps one scale per 32 values of a head (FISH sets kv_q8 only then)
+        if (p.kv_q8 && (KV % 32 || p.head_dim % 32)) return false;
         if (p.attn_softcap < 0.0f || p.window < 0) return false;
         // every weight resident, unsplit, with the shapes of a dense layer; a fused q|k|v
         // (wq, wk, wv null) or a fused gate|up (wg null) in the first and sixth slot
@@ -476,7 +477,9 @@ public:
         }
         const size_t half = size_t(p.rot_dim / 2), ctx = size_t(p.n_ctx);
         const size_t vec_b = size_t(p.n_layers) * per_layer, rope_b = align256(ctx * half * 4),
-                     kv_b = align256(size_t(p.n_layers) * ctx * KV * 2);
+                     kv_c = size_t(p.n_layers) * ctx * KV * (p.kv_q8 ? 1 : 2),
+                     kv_s = p.kv_q8 ? size_t(p.n_layers) * ctx * (KV / 32) * 4 : 0,
+                     kv_b = align256(kv_c) + align256(kv_s);
         // buffers of later calls, sized once here so that no call grows them: a
         // prefill chunk of up to kSpanChunk tokens, the decode graph's one token
         // (attention partials over the whole context), the activation buffer
@@ -494,8 +497,11 @@ public:
         d_vecs_ = reinterpret_cast<float*>(b);
         d_cos_ = reinterpret_cast<float*>(b + vec_b);
         d_sin_ = reinterpret_cast<float*>(b + vec_b + rope_b);
-        d_kc_ = reinterpret_cast<_Float16*>(b + vec_b + 2 * rope_b);
-        d_vc_ = reinterpret_cast<_Float16*>(b + vec_b + 2 * rope_b + kv_b);
+        // K, then V: values (f16 or int8), then (int8) the scales
+        d_kc_ = b + vec_b + 2 * rope_b;
+        d_vc_ = b + vec_b + 2 * rope_b + kv_b;
+        d_ks_ = p.kv_q8 ? reinterpret_cast<float*>(b + vec_b + 2 * rope_b + align256(kv_c)) : nullptr;
+        d_vs_ = p.kv_q8 ? reinterpret_cast<float*>(b + vec_b + 2 * rope_b + kv_b + align256(kv_c)) : nullptr;
         d_span_ws_ = b + vec_b + 2 * rope_b + 2 * kv_b;
         d_dec_ = b + vec_b + 2 * rope_b + 2 * kv_b + ws_b;
         d_dec_act_ = b + vec_b + 2 * rope_b + 2 * kv_b + ws_b + align256(dec_b);
@@ -583,11 +589,25 @@ public:
             if (layer < 0 || layer >= sp_.n_layers || pos0 < 0 || n <= 0 || pos0 + n > sp_.n_ctx ||
                 n_floats < size_t(n) * KV)
                 return false;
-            const _Float16* src = (part == 100 ? d_kc_ : d_vc_) + (size_t(layer) * sp_.n_ctx + pos0) * KV;
-            std::vector<_Float16> tmp(size_t(n) * KV);
-            e = hipMemcpy(tmp.data(), src, tmp.size() * 2, hipMemcpyDeviceToHost);
-            if (e == hipSuccess)
-                for (size_t i = 0; i < tmp.size(); ++i) out[i] = float(tmp[i]);
+            const size_t first = (size_t(layer) * sp_.n_ctx + pos0) * KV;  // element index
+            const float* scales = part == 100 ? d_ks_ : d_vs_;
+            if (scales) {
+                // int8: value = code * d of its 32-value block, as the attention kernels read it
+                std::vector<int8_t> codes(size_t(n) * KV);
+                std::vector<float> d(size_t(n) * KV / 32);
+                e = hipMemcpy(codes.data(), static_cast<const int8_t*>(part == 100 ? d_kc_ : d_vc_) + first,
+                              codes.size(), hipMemcpyDeviceToHost);
+                if (e == hipSuccess)
+                    e = hipMemcpy(d.data(), scales + first / 32, d.size() * 4, hipMemcpyDeviceToHost);
+                if (e == hipSuccess)
+                    for (size_t i = 0; i < codes.size(); ++i) out[i] = float(codes[i]) * d[i / 32];
+            } else {
+                const _Float16* src = static_cast<const _Float16*>(part == 100 ? d_kc_ : d_vc_) + first;
+                std::vector<_Float16> tmp(size_t(n) * KV);
+                e = hipMemcpy(tmp.data(), src, tmp.size() * 2, hipMemcpyDeviceToHost);
+                if (e == hipSuccess)
+                    for (size_t i = 0; i < tmp.size(); ++i) out[i] = float(tmp[i]);
+            }
         } else {
             if (last_tok_ <= 0 || part < 0 || part >= kSpanParts) return false;
             size_t z[kSpanBufs], cnt[kSpanBufs];
@@ -678,8 +698,10 @@ private:
         const float* pending = nullptr;
         for (int l = 0; l < sp_.n_layers && e == hipSuccess; ++l) {
             const Resident* const* W = rs.data() + size_t(7 * l);
-            _Float16* kc = d_kc_ + size_t(l) * sp_.n_ctx * KV;
-            _Float16* vc = d_vc_ + size_t(l) * sp_.n_ctx * KV;
+            // layer l's caches: f16, or int8 codes with one scale per 32 values
+            const size_t lay = size_t(l) * sp_.n_ctx * KV, esz = d_ks_ ? 1 : 2;
+            const KvCache kc{static_cast<char*>(d_kc_) + lay * esz, d_ks_ ? d_ks_ + lay / 32 : nullptr};
+            const KvCache vc{static_cast<char*>(d_vc_) + lay * esz, d_vs_ ? d_vs_ + lay / 32 : nullptr};
             const SpanVecs vecs{span_vec(l, 2), span_vec(l, 3), span_vec(l, 4), span_vec(l, 5), span_vec(l, 6)};
             const bool fq = span_fused_qkv_[size_t(l)] != 0, fg = span_fused_gu_[size_t(l)] != 0;
             const float* post_a = span_vec(l, 8);
@@ -923,6 +945,7 @@ private:
         d_span_fixed_ = nullptr;
         d_vecs_ = d_cos_ = d_sin_ = nullptr;
         d_kc_ = d_vc_ = nullptr;
+        d_ks_ = d_vs_ = nullptr;
         d_span_ws_ = d_dec_ = d_dec_act_ = nullptr;
         span_keys_.clear();
         span_vec_off_.clear();
@@ -1018,7 +1041,8 @@ private:
     std::vector<size_t> span_vec_off_;  // [layer][kSpanVecs] byte offset in d_vecs_, SIZE_MAX = absent
     void* d_span_fixed_ = nullptr;
     float *d_vecs_ = nullptr, *d_cos_ = nullptr, *d_sin_ = nullptr;
-    _Float16 *d_kc_ = nullptr, *d_vc_ = nullptr;
+    void *d_kc_ = nullptr, *d_vc_ = nullptr;  // K / V caches: f16, or int8 codes
+    float *d_ks_ = nullptr, *d_vs_ = nullptr;  // int8 caches: one scale per 32 values (else null)
     void *d_span_ws_ = nullptr, *d_dec_ = nullptr, *d_dec_act_ = nullptr;
     // buffers of the last span call's last chunk (fish_hip_span_inspect)
     SpanBufs last_bufs_{};

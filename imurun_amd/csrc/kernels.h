@@ -193,22 +193,32 @@ struct SpanVecs {
     const float* bias_v;
 };
 constexpr int kAttnSplitTok = 4;  // tokens per call that split attention over position chunks
+// One layer's K or V cache: f16 rows [n_ctx][kv_dim] (d == nullptr), or int8
+// rows with one f32 scale d per 32 values [n_ctx][kv_dim / 32], value = code * d
+// (d = amax / 127 and the codes by the activation quantizer's arithmetic):
+// FISH's int8 span cache at 2.25 bytes per K + V element instead of 4
+// (SpanParams::kv_q8, backend.h:152-156). int8 needs kv_dim and head_dim
+// multiples of 32; its prefill attention takes the non-MFMA kernel.
+struct KvCache {
+    void* c;
+    float* d;
+};
 hipError_t launch_rmsnorm(float* x, const float* y, const float* b, const float* w, float* out, int n_tok, int n,
                           float eps, hipStream_t s);
 hipError_t launch_qkv_prep(const float* q, const float* k, const float* v, const SpanVecs& vecs, float* q_out,
-                           _Float16* kc, _Float16* vc, int n_tok, int H, int HKV, int D, int rot_dim, bool neox,
+                           const KvCache& kc, const KvCache& vc, int n_tok, int H, int HKV, int D, int rot_dim, bool neox,
                            float eps, int pos0, const float* cosv, const float* sinv, hipStream_t s,
                            const int* pos_dev = nullptr);
 // `part` holds attention_scratch_floats(n_tok, H, D, ld) floats (0 above kAttnSplitTok tokens).
 size_t attention_scratch_floats(int n_tok, int H, int D, int ld);
 // softcap > 0: scores c tanh(s / c); window > 0: positions pos - window + 1 .. pos only.
-hipError_t launch_attention(const float* q, const _Float16* kc, const _Float16* vc, float* out, float* part, int ld,
+hipError_t launch_attention(const float* q, const KvCache& kc, const KvCache& vc, float* out, float* part, int ld,
                             int n_tok, int H, int HKV, int D, int pos0, float scale, hipStream_t s,
                             const int* pos_dev = nullptr, float softcap = 0.0f, int window = 0);
 // One token: launch_qkv_prep and launch_attention in one step (the attention
 // workgroups prepare q, and the position's k / v rows, themselves).
 hipError_t launch_attention_prep(const float* q, const float* k, const float* v, const SpanVecs& vecs, float* q_out,
-                                 _Float16* kc, _Float16* vc, float* out, float* part, int ld, int H, int HKV, int D,
+                                 const KvCache& kc, const KvCache& vc, float* out, float* part, int ld, int H, int HKV, int D,
                                  int rot_dim, bool neox, float eps, int pos0, const float* cosv, const float* sinv,
                                  float scale, hipStream_t s, const int* pos_dev = nullptr, float softcap = 0.0f,
                                  int window = 0);

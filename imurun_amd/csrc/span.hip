@@ -154,13 +154,41 @@ __device__ __forceinline__ float head_prep(const HeadIn& in, bool has_bias, bool
     return r;
 }
 
+// The int8 code of element x of a 32-value block held by the 32 lanes of one
+// half wavefront (all of them active), and the block's d = amax / 127: the
+// activation quantizer's arithmetic (qact.h).
+__device__ __forceinline__ int kv_code(float x, float& d) {
+    float a = fabsf(x);
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1) a = fmaxf(a, __shfl_xor(a, off));
+    d = block_d(a);
+    return code(x, block_id(d));
+}
+
+// Element x of a K or V row into the cache at element index `at`, by the thread
+// that owns element at % D of the head (thread index == element index within
+// the head): f16, or (Q8) the int8 code plus the block's d from the block's
+// first thread. Every thread of the 32-value block calls this.
+template <bool Q8>
+__device__ __forceinline__ void kv_store(const KvCache& c, size_t at, float x) {
+    if constexpr (Q8) {
+        float d;
+        const int q = kv_code(x, d);
+        static_cast<int8_t*>(c.c)[at] = int8_t(q);
+        if ((threadIdx.x & 31) == 0) c.d[at >> 5] = d;
+    } else {
+        static_cast<_Float16*>(c.c)[at] = _Float16(x);
+    }
+}
+
 // One workgroup per (token t, head): q heads first, then k heads (whose
 // workgroup also stores the v head of the same index); prep_head, then q ->
-// q_out, k and v -> f16 cache rows of position pos0 + t.
+// q_out, k and v -> cache rows of position pos0 + t.
+template <bool Q8>
 __global__ __launch_bounds__(kTh) void qkv_prep_kernel(const float* __restrict__ q, const float* __restrict__ k,
                                                        const float* __restrict__ v, SpanVecs vecs,
-                                                       float* __restrict__ q_out, _Float16* __restrict__ kc,
-                                                       _Float16* __restrict__ vc, int Q, int KV, int D, int half,
+                                                       float* __restrict__ q_out, KvCache kc, KvCache vc, int Q,
+                                                       int KV, int D, int half,
                                                        int neox, float eps, int pos0, const int* __restrict__ pos_dev,
                                                        const float* __restrict__ cosv,
                                                        const float* __restrict__ sinv) {
@@ -181,10 +209,10 @@ __global__ __launch_bounds__(kTh) void qkv_prep_kernel(const float* __restrict__
         q_out[size_t(t) * Q + head * D + d] = r;
     } else {
         const size_t at = size_t(pos) * KV + head * D + d;
-        kc[at] = _Float16(r);
+        kv_store<Q8>(kc, at, r);
         float vv = v[size_t(t) * KV + head * D + d];
         if (vecs.bias_v) vv = vv + vecs.bias_v[head * D + d];
-        vc[at] = _Float16(vv);
+        kv_store<Q8>(vc, at, vv);
     }
 }
 
@@ -212,6 +240,42 @@ __device__ __forceinline__ float2 f16x2(uint32_t u) {
     return make_float2(float(h.x), float(h.y));
 }
 
+// A lane's pair of elements (e, e + 1) of one cache row as loaded: the f16 pair,
+// or (Q8) the two int8 codes in the low 16 bits and their block's d.
+struct KvRaw {
+    uint32_t w;
+    float d;
+};
+template <bool Q8>
+__device__ __forceinline__ KvRaw kv_raw(const KvCache& c, size_t elem) {
+    KvRaw r;
+    if constexpr (Q8) {
+        r.w = *reinterpret_cast<const uint16_t*>(static_cast<const int8_t*>(c.c) + elem);
+        r.d = c.d[elem >> 5];
+    } else {
+        r.w = *reinterpret_cast<const uint32_t*>(static_cast<const _Float16*>(c.c) + elem);
+        r.d = 0.0f;
+    }
+    return r;
+}
+template <bool Q8>
+__device__ __forceinline__ float2 kv_val(const KvRaw& r) {
+    if constexpr (Q8)
+        return make_float2(float(int8_t(r.w & 0xFFu)) * r.d, float(int8_t((r.w >> 8) & 0xFFu)) * r.d);
+    else
+        return f16x2(r.w);
+}
+
+// The raw pair (e, e + 1) of a row held in LDS: f16 pairs as dwords, or int8
+// codes with one d per 32 values.
+template <bool Q8>
+__device__ __forceinline__ KvRaw lds_raw(const uint32_t* w, const float* d, int e) {
+    if constexpr (Q8)
+        return KvRaw{uint32_t(reinterpret_cast<const uint16_t*>(w)[e >> 1]), d[e >> 5]};
+    else
+        return KvRaw{w[e >> 1], 0.0f};
+}
+
 // A position's score: dot * scale, then Gemma-2's soft cap c tanh(s / c) when c > 0
 // (ops.cpp:334-335)
 __device__ __forceinline__ float score(float dot, float scale, float softcap) {
@@ -222,22 +286,22 @@ __device__ __forceinline__ float score(float dot, float scale, float softcap) {
 // PREP (one token): the workgroup prepares its q head from the raw projection
 // itself (prep_head, as qkv_prep_kernel), and the workgroups of the chunk that
 // holds the token's position also prepare that position's k and v rows (the
-// same f16 values the cache gets) and use them in place of the cache rows; of
+// same values the cache gets) and use them in place of the cache rows; of
 // those, the first q head of each KV group stores the rows into the caches and
 // every one stores its q head into q_out. No separate preparation launch.
 struct AttnPrep {
     const float *q, *k, *v;  // raw projections of the token
     SpanVecs vecs;
     float* q_out;
-    _Float16 *kc, *vc;       // the caches, for the position's rows
+    KvCache kc, vc;          // the caches, for the position's rows
     const float *cosv, *sinv;
     int half, neox;
     float eps;
 };
 
-template <int NP, bool PREP>
-__global__ __launch_bounds__(kTh) void attn_part_kernel(const float* __restrict__ q, const _Float16* __restrict__ kc,
-                                                        const _Float16* __restrict__ vc, float* __restrict__ part,
+template <int NP, bool PREP, bool Q8>
+__global__ __launch_bounds__(kTh) void attn_part_kernel(const float* __restrict__ q, KvCache kc, KvCache vc,
+                                                        float* __restrict__ part,
                                                         int S, int H, int HKV, int D, int pos0,
                                                         const int* __restrict__ pos_dev, float scale, float softcap,
                                                         int window, AttnPrep P) {
@@ -245,9 +309,11 @@ __global__ __launch_bounds__(kTh) void attn_part_kernel(const float* __restrict_
     __shared__ float s_e[kCh];
     __shared__ float s_o[4][128 * NP];
     __shared__ float s_ml[2];
-    // PREP: the prepared q head, the position's k / v rows (f16 pairs), scratch
+    // PREP: the prepared q head, the position's k / v rows (f16 pairs, or int8 codes
+    // and their d per 32), scratch
     __shared__ float s_q[PREP ? 128 * NP : 1];
     __shared__ uint32_t s_kn[PREP ? 64 * NP : 1], s_vn[PREP ? 64 * NP : 1];
+    __shared__ float s_knd[PREP && Q8 ? 4 * NP : 1], s_vnd[PREP && Q8 ? 4 * NP : 1];
     __shared__ float s_row[PREP ? kTh : 1];
     __shared__ double s_red[PREP ? kTh : 1];
     if (pos_dev) pos0 = *pos_dev;
@@ -267,9 +333,7 @@ __global__ __launch_bounds__(kTh) void attn_part_kernel(const float* __restrict_
         return;
     }
     const int jn = min(pos, j0 + kCh - 1);
-    const uint32_t* kb = reinterpret_cast<const uint32_t*>(kc + size_t(kvh) * D);
-    const uint32_t* vb = reinterpret_cast<const uint32_t*>(vc + size_t(kvh) * D);
-    const int KV2 = KV / 2;
+    const size_t hoff = size_t(kvh) * D;  // the KV head's first element in a cache row
 
     // PREP: the inputs of the q head (and of the position's k / v rows) are loaded
     // first, then the cache rows; the preparation waits only for its own loads
@@ -291,12 +355,15 @@ __global__ __launch_bounds__(kTh) void attn_part_kernel(const float* __restrict_
     }
 
     // scores of positions j0 + w + 4 b
-    uint32_t kv[PB][NP];
+    KvRaw kv[PB][NP];
 #pragma unroll
     for (int b = 0; b < PB; ++b) {
-        const uint32_t* kr = kb + size_t(min(j0 + w + 4 * b, jn)) * KV2;
+        const size_t rb = size_t(min(j0 + w + 4 * b, jn)) * KV + hoff;
 #pragma unroll
-        for (int i = 0; i < NP; ++i) kv[b][i] = 2 * (lane + 64 * i) < D ? kr[lane + 64 * i] : 0u;
+        for (int i = 0; i < NP; ++i) {
+            const int e = 2 * (lane + 64 * i);
+            kv[b][i] = e < D ? kv_raw<Q8>(kc, rb + e) : KvRaw{0u, 0.0f};
+        }
     }
     float2 qv[NP];
     if constexpr (PREP) {
@@ -310,14 +377,34 @@ __global__ __launch_bounds__(kTh) void attn_part_kernel(const float* __restrict_
         if (own) {
             const float rk = head_prep(kin, P.vecs.bias_k != nullptr, P.vecs.k_norm != nullptr, D, P.half, P.neox,
                                        P.eps, s_row, s_red);
-            if (tid < D) {
-                const _Float16 k16 = _Float16(rk), v16 = _Float16(P.vecs.bias_v ? v_x + v_b : v_x);
-                reinterpret_cast<_Float16*>(s_kn)[tid] = k16;
-                reinterpret_cast<_Float16*>(s_vn)[tid] = v16;
-                if (h % (H / HKV) == 0) {
-                    const size_t at = size_t(pos) * KV + size_t(kvh) * D + tid;
-                    P.kc[at] = k16;
-                    P.vc[at] = v16;
+            if (tid < D) {  // whole 32-value blocks (D % 32 == 0 for Q8)
+                const float vx = P.vecs.bias_v ? v_x + v_b : v_x;
+                const size_t at = size_t(pos) * KV + size_t(kvh) * D + tid;
+                if constexpr (Q8) {
+                    float dk, dv;
+                    const int qk = kv_code(rk, dk), qv8 = kv_code(vx, dv);
+                    reinterpret_cast<int8_t*>(s_kn)[tid] = int8_t(qk);
+                    reinterpret_cast<int8_t*>(s_vn)[tid] = int8_t(qv8);
+                    if ((tid & 31) == 0) {
+                        s_knd[tid >> 5] = dk;
+                        s_vnd[tid >> 5] = dv;
+                    }
+                    if (h % (H / HKV) == 0) {
+                        static_cast<int8_t*>(P.kc.c)[at] = int8_t(qk);
+                        static_cast<int8_t*>(P.vc.c)[at] = int8_t(qv8);
+                        if ((tid & 31) == 0) {
+                            P.kc.d[at >> 5] = dk;
+                            P.vc.d[at >> 5] = dv;
+                        }
+                    }
+                } else {
+                    const _Float16 k16 = _Float16(rk), v16 = _Float16(vx);
+                    reinterpret_cast<_Float16*>(s_kn)[tid] = k16;
+                    reinterpret_cast<_Float16*>(s_vn)[tid] = v16;
+                    if (h % (H / HKV) == 0) {
+                        static_cast<_Float16*>(P.kc.c)[at] = k16;
+                        static_cast<_Float16*>(P.vc.c)[at] = v16;
+                    }
                 }
             }
         }
@@ -333,7 +420,7 @@ __global__ __launch_bounds__(kTh) void attn_part_kernel(const float* __restrict_
                 if (min(j0 + w + 4 * b, jn) == pos)
 #pragma unroll
                     for (int i = 0; i < NP; ++i)
-                        if (2 * (lane + 64 * i) < D) kv[b][i] = s_kn[lane + 64 * i];
+                        if (2 * (lane + 64 * i) < D) kv[b][i] = lds_raw<Q8>(s_kn, s_knd, 2 * (lane + 64 * i));
         }
     } else {
 #pragma unroll
@@ -348,7 +435,7 @@ __global__ __launch_bounds__(kTh) void attn_part_kernel(const float* __restrict_
         float sum = 0.0f;
 #pragma unroll
         for (int i = 0; i < NP; ++i) {
-            const float2 k2 = f16x2(kv[b][i]);
+            const float2 k2 = kv_val<Q8>(kv[b][i]);
             sum += qv[i].x * k2.x;
             sum += qv[i].y * k2.y;
         }
@@ -375,12 +462,15 @@ __global__ __launch_bounds__(kTh) void attn_part_kernel(const float* __restrict_
         }
     }
     __syncthreads();
-    uint32_t vv[PB][NP];
+    KvRaw vv[PB][NP];
 #pragma unroll
     for (int b = 0; b < PB; ++b) {
-        const uint32_t* vr = vb + size_t(min(j0 + w + 4 * b, jn)) * KV2;
+        const size_t rb = size_t(min(j0 + w + 4 * b, jn)) * KV + hoff;
 #pragma unroll
-        for (int i = 0; i < NP; ++i) vv[b][i] = 2 * (lane + 64 * i) < D ? vr[lane + 64 * i] : 0u;
+        for (int i = 0; i < NP; ++i) {
+            const int e = 2 * (lane + 64 * i);
+            vv[b][i] = e < D ? kv_raw<Q8>(vc, rb + e) : KvRaw{0u, 0.0f};
+        }
     }
     if constexpr (PREP) {
         if (own) {
@@ -389,7 +479,7 @@ __global__ __launch_bounds__(kTh) void attn_part_kernel(const float* __restrict_
                 if (min(j0 + w + 4 * b, jn) == pos)
 #pragma unroll
                     for (int i = 0; i < NP; ++i)
-                        if (2 * (lane + 64 * i) < D) vv[b][i] = s_vn[lane + 64 * i];
+                        if (2 * (lane + 64 * i) < D) vv[b][i] = lds_raw<Q8>(s_vn, s_vnd, 2 * (lane + 64 * i));
         }
     }
     float2 acc[NP];
@@ -400,7 +490,7 @@ __global__ __launch_bounds__(kTh) void attn_part_kernel(const float* __restrict_
         const float e = s_e[w + 4 * b];  // 0 past jn
 #pragma unroll
         for (int i = 0; i < NP; ++i) {
-            const float2 v2 = f16x2(vv[b][i]);
+            const float2 v2 = kv_val<Q8>(vv[b][i]);
             acc[i].x += e * v2.x;
             acc[i].y += e * v2.y;
         }
@@ -453,9 +543,9 @@ __global__ __launch_bounds__(kTh) void attn_combine_kernel(const float* __restri
 // the chunks of kCh positions up to the token's own, each chunk as in
 // attn_part_kernel, and merges them into a running (max, sum, output) --
 // no partials in memory, so the scratch does not grow with tokens x context.
-template <int NP>
-__global__ __launch_bounds__(kTh) void attn_full_kernel(const float* __restrict__ q, const _Float16* __restrict__ kc,
-                                                        const _Float16* __restrict__ vc, float* __restrict__ out,
+template <int NP, bool Q8>
+__global__ __launch_bounds__(kTh) void attn_full_kernel(const float* __restrict__ q, KvCache kc, KvCache vc,
+                                                        float* __restrict__ out,
                                                         int H, int HKV, int D, int pos0,
                                                         const int* __restrict__ pos_dev, float scale, float softcap,
                                                         int window) {
@@ -474,33 +564,37 @@ __global__ __launch_bounds__(kTh) void attn_full_kernel(const float* __restrict_
         const int e = 2 * (lane + 64 * i);
         qv[i] = e < D ? *reinterpret_cast<const float2*>(q + size_t(t) * Q + size_t(h) * D + e) : make_float2(0.f, 0.f);
     }
-    const uint32_t* kb = reinterpret_cast<const uint32_t*>(kc + size_t(kvh) * D);
-    const uint32_t* vb = reinterpret_cast<const uint32_t*>(vc + size_t(kvh) * D);
-    const int KV2 = KV / 2;
+    const size_t hoff = size_t(kvh) * D;
     float o_run = 0.0f, m_run = -INFINITY, l_run = 0.0f;
     for (int j0 = jlo / kCh * kCh; j0 <= pos; j0 += kCh) {
         const int jn = min(pos, j0 + kCh - 1);
-        uint32_t kv[PB][NP];
+        KvRaw kv[PB][NP];
 #pragma unroll
         for (int b = 0; b < PB; ++b) {
-            const uint32_t* kr = kb + size_t(min(j0 + w + 4 * b, jn)) * KV2;
+            const size_t rb = size_t(min(j0 + w + 4 * b, jn)) * KV + hoff;
 #pragma unroll
-            for (int i = 0; i < NP; ++i) kv[b][i] = 2 * (lane + 64 * i) < D ? kr[lane + 64 * i] : 0u;
+            for (int i = 0; i < NP; ++i) {
+                const int e = 2 * (lane + 64 * i);
+                kv[b][i] = e < D ? kv_raw<Q8>(kc, rb + e) : KvRaw{0u, 0.0f};
+            }
         }
         // V rows of the chunk in flight while the scores are formed
-        uint32_t vv[PB][NP];
+        KvRaw vv[PB][NP];
 #pragma unroll
         for (int b = 0; b < PB; ++b) {
-            const uint32_t* vr = vb + size_t(min(j0 + w + 4 * b, jn)) * KV2;
+            const size_t rb = size_t(min(j0 + w + 4 * b, jn)) * KV + hoff;
 #pragma unroll
-            for (int i = 0; i < NP; ++i) vv[b][i] = 2 * (lane + 64 * i) < D ? vr[lane + 64 * i] : 0u;
+            for (int i = 0; i < NP; ++i) {
+                const int e = 2 * (lane + 64 * i);
+                vv[b][i] = e < D ? kv_raw<Q8>(vc, rb + e) : KvRaw{0u, 0.0f};
+            }
         }
 #pragma unroll
         for (int b = 0; b < PB; ++b) {
             float sum = 0.0f;
 #pragma unroll
             for (int i = 0; i < NP; ++i) {
-                const float2 k2 = f16x2(kv[b][i]);
+                const float2 k2 = kv_val<Q8>(kv[b][i]);
                 sum += qv[i].x * k2.x;
                 sum += qv[i].y * k2.y;
             }
@@ -535,7 +629,7 @@ __global__ __launch_bounds__(kTh) void attn_full_kernel(const float* __restrict_
             const float e = s_e[w + 4 * b];  // 0 past jn
 #pragma unroll
             for (int i = 0; i < NP; ++i) {
-                const float2 v2 = f16x2(vv[b][i]);
+                const float2 v2 = kv_val<Q8>(vv[b][i]);
                 acc[i].x += e * v2.x;
                 acc[i].y += e * v2.y;
             }
@@ -753,72 +847,110 @@ hipError_t launch_rmsnorm(float* x, const float* y, const float* b, const float*
     return hipGetLastError();
 }
 
-hipError_t launch_qkv_prep(const float* q, const float* k, const float* v, const SpanVecs& vecs, float* q_out,
-                           _Float16* kc, _Float16* vc, int n_tok, int H, int HKV, int D, int rot_dim, bool neox,
-                           float eps, int pos0, const float* cosv, const float* sinv, hipStream_t s,
-                           const int* pos_dev) {
-    if (n_tok <= 0 || H <= 0 || HKV <= 0 || D <= 0 || D > kTh || rot_dim < 0 || rot_dim > D || rot_dim % 2)
-        return hipErrorInvalidValue;
-    hipLaunchKernelGGL(qkv_prep_kernel, dim3(unsigned(n_tok), unsigned(H + HKV)), dim3(kTh), 0, s, q, k, v, vecs,
-                       q_out, kc, vc, H * D, HKV * D, D, rot_dim / 2, neox ? 1 : 0, eps, pos0, pos_dev, cosv, sinv);
-    return hipGetLastError();
-}
+namespace {
 
-hipError_t launch_attention(const float* q, const _Float16* kc, const _Float16* vc, float* out, float* part, int ld,
-                            int n_tok, int H, int HKV, int D, int pos0, float scale, hipStream_t s,
-                            const int* pos_dev, float softcap, int window) {
-    if (n_tok <= 0 || D <= 0 || D > kTh || D % 2 || HKV <= 0 || H % HKV || ld < pos0 + n_tok) return hipErrorInvalidValue;
+// int8 caches: kv_dim and head_dim multiples of 32 (whole 32-value blocks per head)
+bool kv_ok(const KvCache& c, int D) { return c.c && (!c.d || D % 32 == 0); }
+
+template <bool Q8>
+void attention_split(const float* q, const KvCache& kc, const KvCache& vc, float* out, float* part, int ld, int n_tok,
+                     int H, int HKV, int D, int pos0, float scale, hipStream_t s, const int* pos_dev, float softcap,
+                     int window) {
     const dim3 block(kTh);
-    if (n_tok > kAttnSplitTok && !pos_dev && (D == 64 || D == 128)) {
-        const dim3 grid(unsigned((n_tok + kAttnMfmaTok - 1) / kAttnMfmaTok * H));
-        if (D == 64)
-            hipLaunchKernelGGL(attn_mfma_kernel<64>, grid, block, 0, s, q, kc, vc, out, n_tok, ld, H, HKV, pos0, scale,
-                               softcap, window);
-        else
-            hipLaunchKernelGGL(attn_mfma_kernel<128>, grid, block, 0, s, q, kc, vc, out, n_tok, ld, H, HKV, pos0, scale,
-                               softcap, window);
-        return hipGetLastError();
-    }
     if (n_tok > kAttnSplitTok) {
         const dim3 grid(unsigned(n_tok * H));
         if (D <= 128)
-            hipLaunchKernelGGL(attn_full_kernel<1>, grid, block, 0, s, q, kc, vc, out, H, HKV, D, pos0, pos_dev, scale,
-                               softcap, window);
+            hipLaunchKernelGGL((attn_full_kernel<1, Q8>), grid, block, 0, s, q, kc, vc, out, H, HKV, D, pos0, pos_dev,
+                               scale, softcap, window);
         else
-            hipLaunchKernelGGL(attn_full_kernel<2>, grid, block, 0, s, q, kc, vc, out, H, HKV, D, pos0, pos_dev, scale,
-                               softcap, window);
-        return hipGetLastError();
+            hipLaunchKernelGGL((attn_full_kernel<2, Q8>), grid, block, 0, s, q, kc, vc, out, H, HKV, D, pos0, pos_dev,
+                               scale, softcap, window);
+        return;
     }
     const int S = (ld + kCh - 1) / kCh;
     const dim3 grid(unsigned(n_tok * H), unsigned(S));
     const AttnPrep P{};
     if (D <= 128)
-        hipLaunchKernelGGL((attn_part_kernel<1, false>), grid, block, 0, s, q, kc, vc, part, S, H, HKV, D, pos0,
+        hipLaunchKernelGGL((attn_part_kernel<1, false, Q8>), grid, block, 0, s, q, kc, vc, part, S, H, HKV, D, pos0,
                            pos_dev, scale, softcap, window, P);
     else
-        hipLaunchKernelGGL((attn_part_kernel<2, false>), grid, block, 0, s, q, kc, vc, part, S, H, HKV, D, pos0,
+        hipLaunchKernelGGL((attn_part_kernel<2, false, Q8>), grid, block, 0, s, q, kc, vc, part, S, H, HKV, D, pos0,
                            pos_dev, scale, softcap, window, P);
     hipLaunchKernelGGL(attn_combine_kernel, dim3(unsigned(n_tok * H)), block, 0, s, part, out, S, H, D);
+}
+
+template <bool Q8>
+void attention_prep(const AttnPrep& P, const KvCache& kc, const KvCache& vc, float* out, float* part, int ld, int H,
+                    int HKV, int D, int pos0, float scale, hipStream_t s, const int* pos_dev, float softcap,
+                    int window) {
+    const int S = (ld + kCh - 1) / kCh;
+    const dim3 grid{unsigned(H), unsigned(S)}, block{unsigned(kTh)};
+    if (D <= 128)
+        hipLaunchKernelGGL((attn_part_kernel<1, true, Q8>), grid, block, 0, s, P.q_out, kc, vc, part, S, H, HKV, D,
+                           pos0, pos_dev, scale, softcap, window, P);
+    else
+        hipLaunchKernelGGL((attn_part_kernel<2, true, Q8>), grid, block, 0, s, P.q_out, kc, vc, part, S, H, HKV, D,
+                           pos0, pos_dev, scale, softcap, window, P);
+    hipLaunchKernelGGL(attn_combine_kernel, dim3(unsigned(H)), block, 0, s, part, out, S, H, D);
+}
+
+}  // namespace
+
+hipError_t launch_qkv_prep(const float* q, const float* k, const float* v, const SpanVecs& vecs, float* q_out,
+                           const KvCache& kc, const KvCache& vc, int n_tok, int H, int HKV, int D, int rot_dim,
+                           bool neox, float eps, int pos0, const float* cosv, const float* sinv, hipStream_t s,
+                           const int* pos_dev) {
+    if (n_tok <= 0 || H <= 0 || HKV <= 0 || D <= 0 || D > kTh || rot_dim < 0 || rot_dim > D || rot_dim % 2 ||
+        !kv_ok(kc, D) || !kv_ok(vc, D) || !kc.d != !vc.d)
+        return hipErrorInvalidValue;
+    const dim3 grid(unsigned(n_tok), unsigned(H + HKV));
+    if (kc.d)
+        hipLaunchKernelGGL(qkv_prep_kernel<true>, grid, dim3(kTh), 0, s, q, k, v, vecs, q_out, kc, vc, H * D, HKV * D,
+                           D, rot_dim / 2, neox ? 1 : 0, eps, pos0, pos_dev, cosv, sinv);
+    else
+        hipLaunchKernelGGL(qkv_prep_kernel<false>, grid, dim3(kTh), 0, s, q, k, v, vecs, q_out, kc, vc, H * D, HKV * D,
+                           D, rot_dim / 2, neox ? 1 : 0, eps, pos0, pos_dev, cosv, sinv);
+    return hipGetLastError();
+}
+
+hipError_t launch_attention(const float* q, const KvCache& kc, const KvCache& vc, float* out, float* part, int ld,
+                            int n_tok, int H, int HKV, int D, int pos0, float scale, hipStream_t s,
+                            const int* pos_dev, float softcap, int window) {
+    if (n_tok <= 0 || D <= 0 || D > kTh || D % 2 || HKV <= 0 || H % HKV || ld < pos0 + n_tok || !kv_ok(kc, D) ||
+        !kv_ok(vc, D) || !kc.d != !vc.d)
+        return hipErrorInvalidValue;
+    if (n_tok > kAttnSplitTok && !pos_dev && (D == 64 || D == 128) && !kc.d) {
+        const dim3 grid(unsigned((n_tok + kAttnMfmaTok - 1) / kAttnMfmaTok * H)), block(kTh);
+        const _Float16* k16 = static_cast<const _Float16*>(kc.c);
+        const _Float16* v16 = static_cast<const _Float16*>(vc.c);
+        if (D == 64)
+            hipLaunchKernelGGL(attn_mfma_kernel<64>, grid, block, 0, s, q, k16, v16, out, n_tok, ld, H, HKV, pos0,
+                               scale, softcap, window);
+        else
+            hipLaunchKernelGGL(attn_mfma_kernel<128>, grid, block, 0, s, q, k16, v16, out, n_tok, ld, H, HKV, pos0,
+                               scale, softcap, window);
+        return hipGetLastError();
+    }
+    if (kc.d)
+        attention_split<true>(q, kc, vc, out, part, ld, n_tok, H, HKV, D, pos0, scale, s, pos_dev, softcap, window);
+    else
+        attention_split<false>(q, kc, vc, out, part, ld, n_tok, H, HKV, D, pos0, scale, s, pos_dev, softcap, window);
     return hipGetLastError();
 }
 
 hipError_t launch_attention_prep(const float* q, const float* k, const float* v, const SpanVecs& vecs, float* q_out,
-                                 _Float16* kc, _Float16* vc, float* out, float* part, int ld, int H, int HKV, int D,
-                                 int rot_dim, bool neox, float eps, int pos0, const float* cosv, const float* sinv,
-                                 float scale, hipStream_t s, const int* pos_dev, float softcap, int window) {
+                                 const KvCache& kc, const KvCache& vc, float* out, float* part, int ld, int H, int HKV,
+                                 int D, int rot_dim, bool neox, float eps, int pos0, const float* cosv,
+                                 const float* sinv, float scale, hipStream_t s, const int* pos_dev, float softcap,
+                                 int window) {
     if (D <= 0 || D > kTh || D % 2 || HKV <= 0 || H % HKV || ld < pos0 + 1 || rot_dim < 0 || rot_dim > D ||
-        rot_dim % 2)
+        rot_dim % 2 || !kv_ok(kc, D) || !kv_ok(vc, D) || !kc.d != !vc.d)
         return hipErrorInvalidValue;
     const AttnPrep P{q, k, v, vecs, q_out, kc, vc, cosv, sinv, rot_dim / 2, neox ? 1 : 0, eps};
-    const int S = (ld + kCh - 1) / kCh;
-    const dim3 grid{unsigned(H), unsigned(S)}, block{unsigned(kTh)};
-    if (D <= 128)
-        hipLaunchKernelGGL((attn_part_kernel<1, true>), grid, block, 0, s, q_out, kc, vc, part, S, H, HKV, D, pos0,
-                           pos_dev, scale, softcap, window, P);
+    if (kc.d)
+        attention_prep<true>(P, kc, vc, out, part, ld, H, HKV, D, pos0, scale, s, pos_dev, softcap, window);
     else
-        hipLaunchKernelGGL((attn_part_kernel<2, true>), grid, block, 0, s, q_out, kc, vc, part, S, H, HKV, D, pos0,
-                           pos_dev, scale, softcap, window, P);
-    hipLaunchKernelGGL(attn_combine_kernel, dim3(unsigned(H)), block, 0, s, part, out, S, H, D);
+        attention_prep<false>(P, kc, vc, out, part, ld, H, HKV, D, pos0, scale, s, pos_dev, softcap, window);
     return hipGetLastError();
 }
 

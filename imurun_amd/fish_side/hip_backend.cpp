@@ -49,15 +49,13 @@ public:
                                              ys) != 0;
     }
 
-    // Layer spans (backend.h:89-162) for dense layers with separate q/k/v and
-    // gate/up projections, RMS norms, RoPE, an f16 KV cache and SiLU: llama, and
-    // the Qwen-2 projection biases and Qwen-3 per-head q/k norms. Everything
-    // else a span can carry (fused qkv or gate|up, post norms, soft-caps,
-    // sliding windows, GELU, the int8 KV cache) is refused, and FISH then keeps
-    // routing per matmul.
+    // Layer spans (backend.h:89-162): every field of SpanParams and SpanLayer is
+    // passed on (fused q|k|v and gate|up, biases, q/k norms, post norms,
+    // soft-caps, sliding windows, GELU, the int8 KV cache); a span the device
+    // cannot run is refused there, and FISH then keeps routing per matmul.
     bool span_prepare(const SpanParams& p) override {
         const int n = p.layer_end - p.layer_begin;
-        if (n <= 0 || !p.layers || p.kv_q8) return false;
+        if (n <= 0 || !p.layers) return false;
         std::vector<fish_hip_span_layer> ls(static_cast<size_t>(n));
         for (int i = 0; i < n; ++i) {
             const SpanLayer& L = p.layers[i];

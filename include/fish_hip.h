@@ -304,8 +304,9 @@ typedef struct fish_hip_span_params {
     int rot_dim;
     int rope_neox;
     const fish_hip_span_layer* layers;
-    /* SpanParams::kv_q8 (backend.h:150-153): an int8 KV cache requested by
-     * FISH's planner; this backend keeps f16 K and V only, so nonzero is refused */
+    /* SpanParams::kv_q8 (backend.h:152-156): an int8 KV cache (one f32 scale
+     * per 32 values, 2.25 bytes per K + V element) requested by FISH's planner;
+     * needs kv_dim and head_dim multiples of 32, else the span is refused */
     int kv_q8;
     /* SpanParams attn_softcap (Gemma-2: scores become c tanh(s / c), 0 = none),
      * window (positions a sliding-window layer attends over) and gelu (the FFN

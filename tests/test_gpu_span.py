@@ -132,9 +132,12 @@ class RefLayer:
         if "q_norm" in self.x:
             q, k = self.head_rms(q, self.x["q_norm"], H), self.head_rms(k, self.x["k_norm"], HKV)
         q, k = self.rope(q, pos, H), self.rope(k, pos, HKV)
-        # the cache holds f16 K and V (round to nearest even)
-        self.kc[pos] = k.astype(np.float16).astype(np.float32)
-        self.vc[pos] = v.astype(np.float16).astype(np.float32)
+        # the cache holds f16 K and V (round to nearest even), or their int8 form
+        if self.opts.get("kv_q8"):
+            self.kc[pos], self.vc[pos] = q8_rows(k)[0], q8_rows(v)[0]
+        else:
+            self.kc[pos] = k.astype(np.float16).astype(np.float32)
+            self.vc[pos] = v.astype(np.float16).astype(np.float32)
         att = np.zeros((n, Q), np.float64)
         for t in range(n):
             p = pos0 + t
@@ -159,7 +162,20 @@ class RefLayer:
 
 # per variant: weight types (a fused tensor has one type), span options
 VARIANT_TYPES = {"phi3": dict(TYPES, wv=fh.Q4_K)}
-VARIANT_OPTS = {"gemma2": dict(softcap=5.0, window=24, gelu=True), "gelu": dict(gelu=True)}
+VARIANT_OPTS = {"gemma2": dict(softcap=5.0, window=24, gelu=True), "gelu": dict(gelu=True), "q8kv": dict(kv_q8=True)}
+
+
+def q8_rows(x):
+    """The int8 KV cache's value of each element (SpanParams::kv_q8, backend.h:152-156): per
+    32 values d = amax / 127 (f32 division), codes clamp(rint(x * (1 / d)), -127, 127) with
+    one f32 rounding of the product, value = code * d; and the d of each element's block."""
+    x = np.ascontiguousarray(x, np.float32)
+    b = x.reshape(x.shape[0], -1, 32)
+    amax = np.abs(b).max(axis=2, keepdims=True)
+    d = (amax / np.float32(127)).astype(np.float32)
+    inv = np.where(d > 0, np.float32(1) / np.where(d > 0, d, np.float32(1)), np.float32(0)).astype(np.float32)
+    q = np.clip(np.rint((b * inv).astype(np.float32)), -127, 127).astype(np.float32)
+    return (q * d).reshape(x.shape).astype(np.float32), np.broadcast_to(d, b.shape).reshape(x.shape)
 
 
 def layer_extras(variant):
@@ -208,7 +224,7 @@ def setup_span(oracle, be, rot_dim, variant, tag, ctx=CTX):
         span_extras["sliding_window"] = True
     assert be.span_prepare([(names_span, an, fn, span_extras)], E, H, HKV, D, F, ctx, cos, sin, rope_neox=True,
                            attn_softcap=opts.get("softcap", 0.0), window=opts.get("window", 0),
-                           gelu=opts.get("gelu", False))
+                           gelu=opts.get("gelu", False), kv_q8=opts.get("kv_q8", False))
     ref = RefLayer(oracle, packed, an, fn, cos, sin, extras=extras, types=types, opts=opts)
     return uploaded, ref, (packed, an, fn, cos, sin, extras)
 
@@ -239,6 +255,14 @@ def check_stages(be, ref, x_in, x_out, pos0, what):
     kc = be.span_inspect("kc", KV, 0, 0, pos0 + n)
     vc = be.span_inspect("vc", KV, 0, 0, pos0 + n)
     for got, want, nm in ((kc[pos0:], k_want, "k"), (vc[pos0:], v_want, "v")):
+        if ref.opts.get("kv_q8"):
+            # int8 rows: within one code step of the form of the reference's values (the
+            # device's own k and v differ from them in the last bits)
+            val, dstep = q8_rows(want)
+            assert np.all(np.abs(got - val) <= 1.01 * dstep + 1e-30), f"{what}: {nm} int8 cache rows"
+            assert np.all(np.abs(got / np.where(dstep > 0, dstep, 1) - np.rint(got / np.where(dstep > 0, dstep, 1)))
+                          < 1e-3), f"{what}: {nm} cache rows are codes x d"
+            continue
         ulp = np.spacing(np.abs(want).astype(np.float16)).astype(np.float64)
         assert np.all(np.abs(got - want.astype(np.float16).astype(np.float64)) <= ulp), f"{what}: {nm} cache rows"
     # attention over the device's q and cache rows, in float64
@@ -285,14 +309,14 @@ def check_call(be, ref, x, pos0, what):
 
 
 @pytest.mark.parametrize("rot_dim,variant", [(D, "llama"), (D // 2, "llama"), (D, "qwen3"), (D, "bias"),
-                                             (D, "phi3"), (D, "gemma2"), (D, "gelu")])
+                                             (D, "phi3"), (D, "gemma2"), (D, "gelu"), (D, "q8kv")])
 def test_span_layer_matches_fish_forward(oracle, rot_dim, variant):
     be = fh.HipBackend()
     assert be.available()
     names, ref, (packed, an, fn, cos, sin, extras) = setup_span(oracle, be, rot_dim, variant, "span")
     try:
         pos0 = 0
-        for i, n in enumerate((37, 1, 1, 1, 100, 1)):
+        for i, n in enumerate((37, 1, 1, 3, 100, 1)):
             x = normal(650 + i, (n, E), 1.0)
             d_dev, d_ref = check_call(be, ref, x, pos0, variant)
             if i == 0:
@@ -319,11 +343,12 @@ def test_span_layer_matches_fish_forward(oracle, rot_dim, variant):
                     a_alt = alt.attend(qr[t, :D].astype(np.float64), kc[:, :D].astype(np.float64),
                                        vc[:, :D].astype(np.float64), p)
                     assert np.abs(att[t, :D] - a_alt).max() > 1e-3 * np.abs(a_alt).max(), drop
-                g, u = be.span_inspect("h", F), be.span_inspect("u", F)
-                silu = RefLayer(oracle, packed, an, fn, cos, sin, extras=extras, types=ref.types, opts={})
-                xb2 = be.span_inspect("xb2", E)
-                gg = ref.mm("wg", xb2)
-                assert np.abs(silu.act(gg, u) - ref.act(gg, u)).max() > 1e-2 * np.abs(ref.act(gg, u)).max()
+                if ref.opts.get("gelu"):
+                    g, u = be.span_inspect("h", F), be.span_inspect("u", F)
+                    silu = RefLayer(oracle, packed, an, fn, cos, sin, extras=extras, types=ref.types, opts={})
+                    xb2 = be.span_inspect("xb2", E)
+                    gg = ref.mm("wg", xb2)
+                    assert np.abs(silu.act(gg, u) - ref.act(gg, u)).max() > 1e-2 * np.abs(ref.act(gg, u)).max()
             pos0 += n
         # past the context: refused, x untouched
         x = normal(660, (CTX - pos0 + 1, E), 1.0)
@@ -399,8 +424,9 @@ def test_span_prefill_longer_than_one_chunk(oracle):
             be.release(n)
 
 
-def test_span_refuses_int8_kv_cache(oracle):
-    """kv_q8 (backend.h:150-153) is refused: this backend keeps f16 K and V only."""
+def test_span_int8_kv_cache_needs_whole_blocks(oracle):
+    """kv_q8 (backend.h:152-156) gives an int8 cache when kv_dim and head_dim are multiples of
+    32 (FISH's planner sets it only then, model.cpp:1023); otherwise span_prepare refuses."""
     be = fh.HipBackend()
     packed = {n: fh.quantize_rows(TYPES[n], normal(600 + i, SHAPES[n], 0.03)) for i, n in enumerate(TYPES)}
     names = [f"kvq8.{n}" for n in TYPES]
@@ -409,8 +435,20 @@ def test_span_refuses_int8_kv_cache(oracle):
     an = np.ones(E, np.float32)
     cos, sin = rope_tables(D)
     try:
-        assert not be.span_prepare([(names, an, an)], E, H, HKV, D, F, CTX, cos, sin, kv_q8=True)
-        assert be.span_prepare([(names, an, an)], E, H, HKV, D, F, CTX, cos, sin)
+        assert be.span_prepare([(names, an, an)], E, H, HKV, D, F, CTX, cos, sin, kv_q8=True)
+        be.span_release()
+        # head_dim 136 (not whole 32-value blocks) with q / o shaped to match: refused with kv_q8 only
+        d2 = 136
+        shp = dict(SHAPES, wq=(H * d2, E), wk=(HKV * d2, E), wv=(HKV * d2, E), wo=(E, H * d2))
+        t2 = dict(TYPES, wo=fh.Q8_0)  # o's rows of 4 x 136 values: 32-value blocks
+        p2 = {n: fh.quantize_rows(t2[n], normal(610 + i, shp[n], 0.03)) for i, n in enumerate(t2)}
+        n2 = [f"kvq8b.{n}" for n in t2]
+        for n, name in zip(t2, n2):
+            assert be.upload(name, t2[n], p2[n], shp[n][1], shp[n][0])
+        names += n2
+        c2, s2 = rope_tables(d2)
+        assert not be.span_prepare([(n2, an, an)], E, H, HKV, d2, F, CTX, c2, s2, kv_q8=True)
+        assert be.span_prepare([(n2, an, an)], E, H, HKV, d2, F, CTX, c2, s2)
     finally:
         be.span_release()
         for n in names:
