@@ -188,6 +188,31 @@ def test_model_generates_through_a_layer_span(fish, tmp_path, name):
     assert dev == cpu
 
 
+@pytest.mark.gpu
+def test_model_generates_through_a_span_with_int8_kv(fish, tmp_path):
+    # FISH_GPU_KV=q8 makes FISH's planner ask for the int8 KV cache (model.cpp:1019-1036); the
+    # span keeps it (one f32 scale per 32 values) and runs both layers through it, one call per
+    # forward. The int8 K and V move the logits by a fraction of a percent; on this model greedy
+    # decoding still picks the CPU's tokens.
+    path = str(tmp_path / "kvq8.gguf")
+    tiny_llama(path, MODELS["q4_k_m"], seed=14)
+    cpu, _, _ = run(fish, path, gpu=False)
+    os.environ["FISH_GPU_SPAN"] = "1"
+    os.environ["FISH_GPU_NO_IMPORTANCE"] = "1"
+    os.environ["FISH_GPU_KV"] = "q8"
+    try:
+        served0 = fh.load().fish_hip_backend_served()
+        dev, st, _ = run(fish, path, gpu=True)
+        served = fh.load().fish_hip_backend_served() - served0
+    finally:
+        os.environ["FISH_GPU_SPAN"] = "0"
+        os.environ.pop("FISH_GPU_NO_IMPORTANCE", None)
+        os.environ.pop("FISH_GPU_KV", None)
+    assert st.gpu_layers == 2 and b"KV int8" in st.placement, st.placement
+    assert st.generated_tokens <= served <= 3 * st.generated_tokens, (served, st.placement)
+    assert dev == cpu
+
+
 # Qwen-family layers: Qwen-3 (per-head q / k RMSNorm, n_head * head_dim != n_embd) and
 # Qwen-2 (q / k / v biases), both with FISH's NeoX RoPE; Phi-3 (fused q|k|v and fused
 # gate|up); Gemma-2 (post norms, GELU, attention soft cap 5 and a 32-position sliding
