@@ -304,12 +304,33 @@ __device__ __forceinline__ void gemv_x_rows(const GemvXGroup& G, int gm, int wav
     // the Q4_0 2 x 14336x4096 gate+up, 3 % on the Q8_0 4096x4096; slower on
     // longer rows and on the K-quants)
     constexpr bool NT = (T == kQ4_0 || T == kQ8_0) && MAXC <= 2;
+    // K-quants: the scale data of every group first, then every group's codes, so
+    // that decoding the scales (the meta shuffles and 6-bit unpacking) waits only
+    // for them and runs before the barrier, under the other wavefronts'
+    // quantization (Q4_K down 4096x14336: 10.5 -> 10.1 us). Q8_0 / Q4_0 (one f16 scale
+    // a group) keep each group's loads together and decode after the barrier (the split
+    // made the Q8_0 4096^2 GEMV 3 % slower).
     Frag f[RB][MAXC];
+    if constexpr (kq) {
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb) {
-        const int row = min(row_base + rb * RPP, n_out - 1);
+        for (int rb = 0; rb < RB; ++rb) {
+            const int row = min(row_base + rb * RPP, n_out - 1);
 #pragma unroll
-        for (int k = 0; k < MAXC; ++k) f[rb][k] = load_group_raw<T, true, NT>(W, row, cg[k], n_in, lane);
+            for (int k = 0; k < MAXC; ++k) load_group_scales<T, true>(f[rb][k], W, row, cg[k], n_in, lane);
+        }
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+            const int row = min(row_base + rb * RPP, n_out - 1);
+#pragma unroll
+            for (int k = 0; k < MAXC; ++k) load_group_codes<T, NT>(f[rb][k], W, row, cg[k], n_in);
+        }
+    } else {
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+            const int row = min(row_base + rb * RPP, n_out - 1);
+#pragma unroll
+            for (int k = 0; k < MAXC; ++k) f[rb][k] = load_group_raw<T, true, NT>(W, row, cg[k], n_in, lane);
+        }
     }
 
     // every load is issued before the quantization's first use of x
@@ -317,14 +338,23 @@ __device__ __forceinline__ void gemv_x_rows(const GemvXGroup& G, int gm, int wav
     if constexpr (NORM) row_norm<XV, 64 * kGemvXWaves>(xv, G.norm, n_in, tid, s_red);
     const LdsAct L{s_codes, s_d, s_s, kGemvXMaxGroups};
     quantize_to_lds<kq, XV, 64 * kGemvXWaves>(xv, n_in, tid, L);
+    if constexpr (kq) {
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+            for (int k = 0; k < MAXC; ++k) finish_group<T, true>(f[rb][k], cg[k], lane);
+    }
     __syncthreads();
     // (a pair's wavefronts all reach its second barrier; their rows past the end are
     // clamped loads whose results are not stored)
     if (!PAIR && wave_id * (RPP * RB) >= n_out) return;  // uniform over the wavefront
+    if constexpr (!kq) {
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb)
+        for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-        for (int k = 0; k < MAXC; ++k) finish_group<T, true>(f[rb][k], cg[k], lane);
+            for (int k = 0; k < MAXC; ++k) finish_group<T, true>(f[rb][k], cg[k], lane);
+    }
 
     float acc[RB];
 #pragma unroll
@@ -385,9 +415,15 @@ __device__ __forceinline__ int gemv_x_member(const GemvXGroup& G, int& wg) {
     return gm;
 }
 
-// The wavefront's index in its workgroup, as a scalar (uniform over the
-// wavefront), so row indices derived from it take no vector registers.
-__device__ __forceinline__ int wave_index() { return __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6)); }
+// The wavefront's index in its workgroup. SCALAR: read as a scalar (uniform over
+// the wavefront), so that row indices derived from it take no vector registers:
+// the gate / up pair kernel needs that to fit two workgroups per CU; the others
+// measured 2 % slower with it (Q8_0 4096^2: 5.76 against 5.85 us).
+template <bool SCALAR = false>
+__device__ __forceinline__ int wave_index() {
+    if constexpr (SCALAR) return __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
+    return int(threadIdx.x >> 6);
+}
 
 // x loads first: unconditional, from a clamped address (chunks past the end lie in
 // whole 32/256-value blocks the quantizer discards, and a load inside a branch would
@@ -433,7 +469,7 @@ __global__ __launch_bounds__(64 * kGemvXWaves) __attribute__((
     __shared__ int s_s[kGemvXMaxGroups];
     __shared__ double s_red[kGemvXWaves];
     __shared__ float s_pair[HALF * (64 / LPR) * gemv_rb<T, MAXC>()];
-    const int wave = wave_index();
+    const int wave = wave_index<true>();
     float4 xv[XV];
     gemv_x_loads<XV>(x, n_in, xv);
     gemv_x_rows<T, LPR, MAXC, XV, true, true>(G, wave / HALF, int(blockIdx.x) * HALF + wave % HALF, xv, n_in,

@@ -72,8 +72,45 @@ __device__ __forceinline__ Frag load_group_raw(const WeightPtrs& W, int row, int
     return f;
 }
 
-// Decodes the scales of a group loaded by load_group_raw<T, WAVE> (group
-// index c; every lane of the wavefront calls it in the WAVE form).
+// The same loads in two parts, for callers that decode the scales while other
+// work waits on the codes: every group's scale data first (load_group_scales),
+// then every group's codes (load_group_codes); a wait for the scales then does
+// not wait for the codes issued after them.
+template <uint32_t T, bool WAVE>
+__device__ __forceinline__ void load_group_scales(Frag& f, const WeightPtrs& W, int row, int c, int n_in, int lane) {
+    const size_t gi = size_t(row) * (n_in / 32) + c;
+    if constexpr (T == kQ8_0 || T == kQ4_0) {
+        f.raw = W.d[gi];
+    } else if constexpr (has_mins(T)) {
+        const uint8_t* m = W.aux + (size_t(row) * (n_in / 256) + (c >> 3)) * 16;
+        if constexpr (WAVE) f.raw = reinterpret_cast<const uint32_t*>(m)[lane & 3];
+        else f.meta = *reinterpret_cast<const uint4*>(m);
+    } else {
+        f.raw2 = *reinterpret_cast<const uint16_t*>(W.sc + size_t(row) * (n_in / 16) + 2 * c);
+        f.raw = W.d[size_t(row) * (n_in / 256) + (c >> 3)];
+    }
+}
+template <uint32_t T, bool NT = false>
+__device__ __forceinline__ void load_group_codes(Frag& f, const WeightPtrs& W, int row, int c, int n_in) {
+    const size_t gi = size_t(row) * (n_in / 32) + c;
+    if constexpr (T == kQ8_0) {
+        const uint8_t* p = W.codes + size_t(row) * n_in + size_t(c) * 32;
+        f.w0 = load16<NT>(p);
+        f.w1 = load16<NT>(p + 16);
+    } else if constexpr (T == kQ4_0) {
+        f.w0 = load16<NT>(W.codes + gi * 16);
+    } else if constexpr (has_mins(T)) {
+        f.w0 = *reinterpret_cast<const uint4*>(W.codes + gi * 16);
+        if constexpr (T == kQ5_K) f.hb = W.hb[gi];
+    } else {
+        f.w0 = *reinterpret_cast<const uint4*>(W.codes + gi * 16);
+        f.qh = *reinterpret_cast<const uint2*>(W.aux + gi * 8);
+    }
+}
+
+// Decodes the scales of a group loaded by load_group_raw<T, WAVE> or
+// load_group_scales<T, WAVE> (group index c; every lane of the wavefront calls
+// it in the WAVE form).
 template <uint32_t T, bool WAVE>
 __device__ __forceinline__ void finish_group(Frag& f, int c, int lane) {
     if constexpr (T == kQ8_0 || T == kQ4_0) {
