@@ -489,7 +489,8 @@ public:
         size_t dec_act = 0;
         for (int n_in : {E, Q, F}) dec_act = std::max(dec_act, act_layout(1, n_in).total);
         const size_t total = vec_b + 2 * rope_b + 2 * kv_b + ws_b + align256(dec_b) + dec_act + 256;
-        if (!act || !reserve(0, act, 0) || dev_alloc(&d_span_fixed_, total) != hipSuccess) {
+        if (!act || !reserve(0, act, 0) || dev_alloc(&d_span_fixed_, total) != hipSuccess ||
+            hipHostMalloc(&h_dec_, size_t(E) * 4 + 256, hipHostMallocDefault) != hipSuccess) {
             span_free();
             return false;
         }
@@ -803,10 +804,19 @@ private:
         }
         if (!dec_exec_) {
             dec_ = span_bufs(d_dec_, 1, sp_.n_ctx);
+            // the token's x and position go in and x comes out through one pinned staging
+            // buffer (h_dec_, allocated by span_prepare), as copy nodes of the graph itself:
+            // one launch and one wait per token
+            char* hx = static_cast<char*>(h_dec_);
             hipGraph_t g = nullptr;
             e = hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal);
             if (e == hipSuccess) {
-                const hipError_t le = span_layers(rs, dec_, 1, 0, dec_.pos, d_dec_act_);
+                hipError_t le = hipMemcpyAsync(dec_.x, hx, size_t(E) * 4, hipMemcpyHostToDevice, stream_);
+                if (le == hipSuccess)
+                    le = hipMemcpyAsync(dec_.pos, hx + size_t(E) * 4, sizeof(int), hipMemcpyHostToDevice, stream_);
+                if (le == hipSuccess) le = span_layers(rs, dec_, 1, 0, dec_.pos, d_dec_act_);
+                if (le == hipSuccess)
+                    le = hipMemcpyAsync(hx, dec_.x, size_t(E) * 4, hipMemcpyDeviceToHost, stream_);
                 e = hipStreamEndCapture(stream_, &g);
                 if (e == hipSuccess) e = le;
             }
@@ -822,19 +832,16 @@ private:
         last_bufs_ = dec_;
         last_tok_ = 1;
         last_pos0_ = pos0;
-        if (!grow_host(size_t(E) * 4 + 256)) return false;
-        int* pos_host = reinterpret_cast<int*>(static_cast<char*>(h_y_) + size_t(E) * 4);
-        *pos_host = pos0;
-        e = hipMemcpyAsync(dec_.x, x, size_t(E) * 4, hipMemcpyHostToDevice, stream_);
-        if (e == hipSuccess) e = hipMemcpyAsync(dec_.pos, pos_host, sizeof(int), hipMemcpyHostToDevice, stream_);
-        if (e == hipSuccess) e = hipGraphLaunch(dec_exec_, stream_);
-        if (e == hipSuccess) e = hipMemcpyAsync(h_y_, dec_.x, size_t(E) * 4, hipMemcpyDeviceToHost, stream_);
+        char* hx = static_cast<char*>(h_dec_);
+        std::memcpy(hx, x, size_t(E) * 4);
+        std::memcpy(hx + size_t(E) * 4, &pos0, sizeof(int));
+        e = hipGraphLaunch(dec_exec_, stream_);
         if (e == hipSuccess) e = hipStreamSynchronize(stream_);
         if (e != hipSuccess) {
             mark_broken(e, "span_forward");
             return false;
         }
-        std::memcpy(x, h_y_, size_t(E) * 4);
+        std::memcpy(x, hx, size_t(E) * 4);
         ++served_;
         return true;
     }
@@ -941,6 +948,8 @@ private:
     void span_free() {
         if (dec_exec_) (void)hipGraphExecDestroy(dec_exec_);
         dec_exec_ = nullptr;
+        if (h_dec_) (void)hipHostFree(h_dec_);  // after the graph whose copy nodes use it
+        h_dec_ = nullptr;
         if (d_span_fixed_) (void)hipFree(d_span_fixed_);
         d_span_fixed_ = nullptr;
         d_vecs_ = d_cos_ = d_sin_ = nullptr;
@@ -1031,6 +1040,7 @@ private:
     size_t cap_moe_ = 0;
     void* h_y_ = nullptr;
     size_t cap_h_y_ = 0;
+    void* h_dec_ = nullptr;  // pinned x / position staging of the decode graph's copy nodes
     // layer span: parameters, weight keys (7 per layer); one allocation holds the
     // per-layer vectors, RoPE tables, f16 KV cache and every per-call buffer
     bool span_on_ = false;
