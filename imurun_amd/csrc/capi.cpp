@@ -935,8 +935,30 @@ private:
             }
             e = launch_gemm_group(n, ws, Ls, act, n_tok, dys, ldy, stream_);
         } else {
+            // mixed types (a Q4_K_M layer's q, k in Q4_K and v in Q6_K): the GEMM-sized tensors
+            // of each type still share one grouped launch (q with k), the rest go one by one
+            bool done[kGemmGroupMax] = {};
             for (int i = 0; i < n && e == hipSuccess; ++i) {
                 const Resident& r = *rs[i];
+                if (i < kGemmGroupMax && done[i]) continue;
+                if (n <= kGemmGroupMax && int8_type(r.layout.type) && uses_gemm(r.layout, n_tok)) {
+                    const void* ws[kGemmGroupMax];
+                    WeightLayout Ls[kGemmGroupMax];
+                    float* ys[kGemmGroupMax];
+                    int ldy[kGemmGroupMax];
+                    int m = 0;
+                    for (int j = i; j < n; ++j) {
+                        if (done[j] || rs[j]->layout.type != r.layout.type) continue;
+                        done[j] = true;
+                        ws[m] = rs[j]->dev;
+                        Ls[m] = rs[j]->layout;
+                        ys[m] = dys[j];
+                        ldy[m] = n_outs[j];
+                        ++m;
+                    }
+                    e = launch_gemm_group(m, ws, Ls, act, n_tok, ys, ldy, stream_);
+                    continue;
+                }
                 e = f32path_type(r.layout.type)
                         ? launch_dq_matmul(r.layout.type, r.dev, dx, n_tok, n_in, n_outs[i], dys[i], stream_)
                         : dispatch_matmul(r.dev, r.layout, act, n_tok, dys[i], n_outs[i], stream_);

@@ -354,6 +354,27 @@ def test_backend_one_token_mixed_types(torch_dev, oracle, types, n_in, n_outs):
         be.release(name)
 
 
+@pytest.mark.parametrize("n_tok", [5, 130, 256])
+def test_backend_batch_mixed_types(torch_dev, oracle, n_tok):
+    """A q/k/v-shaped group of a Q4_K_M layer (q, k Q4_K; v Q6_K) on a batch: at GEMM sizes the
+    tensors of each type share one grouped launch (q with k), v runs alone; every output is
+    bit-identical to the tensor's own matmul and close to the oracle."""
+    be = fh.HipBackend()
+    n_in, n_outs, types = 2048, [1024, 256, 256], [fh.Q4_K, fh.Q4_K, fh.Q6_K]
+    names = [f"bm{i}_{n_tok}" for i in range(3)]
+    packed = []
+    for i, (name, t, n_out) in enumerate(zip(names, types, n_outs)):
+        packed.append(packed_weights(oracle, t, n_out, n_in, 1800 + i))
+        assert be.upload(name, t, packed[-1], n_in, n_out)
+    x = normal(1810 + n_tok, (n_tok, n_in))
+    ys = be.matmul_group(names, x, n_outs)
+    for name, t, p, n_out, y in zip(names, types, packed, n_outs, ys):
+        assert np.array_equal(be.matmul(name, x, n_out), y), f"{name}: group differs from single"
+        check_close(y, oracle.matmul_f32(t, p, x, n_out), f"mixed batch {fh.TYPE_NAMES[t]} M={n_tok}")
+    for name in names:
+        be.release(name)
+
+
 def test_backend_upload_keeps_the_vram_headroom(torch_dev, oracle, monkeypatch):
     """upload() leaves FISH's VRAM headroom free (vram_headroom_bytes, backend.h:171-187): with
     FISH_VRAM_HEADROOM_MB above the free memory the upload is refused (earlier uploads intact),
