@@ -544,16 +544,22 @@ hipError_t launch_gemm_group(int n, const void* const* ws, const WeightLayout* W
     }
     const bool small = type == kQ6_K ? rows32 * ((n_tok + 255) / 256) <= kGemmCUs / 2
                                      : rows64 * ((n_tok + 127) / 128) <= kGemmCUs / 2;
+    // still a quarter of the CUs or fewer with those tiles (a lone 1024-row projection of a
+    // 256-token chunk: 64 workgroups): two token wavefronts per workgroup, twice the workgroups
+    const bool tiny = small && rows32 * ((n_tok + 127) / 128) <= kGemmCUs / 4;
     switch (type) {
         case kQ4_K:
+            if (tiny) return gemm_launch<kQ4_K, 2, 1, 1, 1>(G, n_outs, A, n_in, n_tok, s);
             return small ? gemm_launch<kQ4_K, 4, 1, 1, 1>(G, n_outs, A, n_in, n_tok, s)
                          : gemm_launch<kQ4_K, 4, 1, 1, 2>(G, n_outs, A, n_in, n_tok, s);
         case kQ5_K:
+            if (tiny) return gemm_launch<kQ5_K, 2, 1, 1, 1>(G, n_outs, A, n_in, n_tok, s);
             return small ? gemm_launch<kQ5_K, 4, 1, 1, 1>(G, n_outs, A, n_in, n_tok, s)
                          : gemm_launch<kQ5_K, 4, 1, 1, 2>(G, n_outs, A, n_in, n_tok, s);
         // Q6_K (no mins MFMA, heavier dequantization): four token wavefronts share each
         // dequantized stage (measured 8-11 % faster on the 4096 x 14336 down projection)
         case kQ6_K:
+            if (tiny) return gemm_launch<kQ6_K, 2, 1, 1, 1>(G, n_outs, A, n_in, n_tok, s);
             return small ? gemm_launch<kQ6_K, 4, 1, 1, 1>(G, n_outs, A, n_in, n_tok, s)
                          : gemm_launch<kQ6_K, 4, 1, 2, 1>(G, n_outs, A, n_in, n_tok, s);
         default: return hipErrorInvalidValue;
