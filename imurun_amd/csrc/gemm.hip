@@ -199,9 +199,13 @@ __device__ __forceinline__ void dequant_part(const Raw& r, const DqPrep& p, int 
 }
 
 // A wavefront owns TPW 32-token blocks x RPW 32-row blocks; a workgroup WT x WR
-// wavefronts (32 TPW WT tokens x 32 RPW WR rows).
-template <uint32_t T, int WT, int WR, int TPW, int RPW>
-__global__ __launch_bounds__(64 * WT * WR) __attribute__((amdgpu_waves_per_eu(2))) void gemm_kq_kernel(
+// wavefronts (32 TPW WT tokens x 32 RPW WR rows) per K part. With KS = 2 the
+// workgroup holds two such sets of wavefronts, each over half of the
+// super-blocks with its own LDS ring, and the second set's sums are added to
+// the first's at the end (through LDS, in that order): twice the wavefronts on
+// the same tiles, for grids of one tile per CU or fewer.
+template <uint32_t T, int WT, int WR, int TPW, int RPW, int KS>
+__global__ __launch_bounds__(64 * WT * WR * KS) __attribute__((amdgpu_waves_per_eu(2))) void gemm_kq_kernel(
     GemmGroup G, ActPtrs A, int n_in, int n_tok, int tok_tiles) {
     constexpr int NW = WT * WR;
     constexpr int RWG = 32 * RPW * WR;                // rows per workgroup
@@ -209,18 +213,26 @@ __global__ __launch_bounds__(64 * WT * WR) __attribute__((amdgpu_waves_per_eu(2)
     constexpr int ITEMS = RWG * SSTEPS;               // (row, step) items per stage
     constexpr int IPT = (ITEMS + 64 * NW - 1) / (64 * NW);
     constexpr int SHIFT = (T == kQ4_K) ? 3 : 6;  // I = 8 H + L (Q4_K) or 64 H + L
-    // [stage][plane][step][half][row] of 16-byte pieces
-    __shared__ uint4 s_b[RING * 2 * SSTEPS * 2 * RWG];
-    // per super-block epilogue data, loaded during its first stage:
+    // per K part: [stage][plane][step][half][row] of 16-byte pieces
+    constexpr int SB = RING * 2 * SSTEPS * 2 * RWG;
+    __shared__ uint4 s_b_all[KS * SB];
+    // per K part, per super-block epilogue data, loaded during its first stage:
     // row meta (Q4_K / Q5_K d, dmin, scales; Q6_K d in .x), token scales, mins operands
-    __shared__ uint4 s_meta[RWG];
-    __shared__ float4 s_xd[TBW * 2 * 4];
+    __shared__ uint4 s_meta_all[KS * RWG];
+    __shared__ float4 s_xd_all[KS * TBW * 2 * 4];
     // mins operands: straight from the thread's own load when the thread's wavefront
     // owns one token block (thread tid loads block tid / 64, the wavefront's own)
     constexpr bool J_REG = TPW == 1 && WR == 1;
-    __shared__ uint4 s_j[has_mins(T) && !J_REG ? TBW * 64 : 1];
+    constexpr int SJ = has_mins(T) && !J_REG ? TBW * 64 : 0;
+    __shared__ uint4 s_j_all[SJ ? KS * SJ : 1];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // K part of this thread, and its index within the part
+    const int ks = int(threadIdx.x) / (64 * NW);
+    uint4* s_b = s_b_all + ks * SB;
+    uint4* s_meta = s_meta_all + ks * RWG;
+    float4* s_xd = s_xd_all + ks * (TBW * 2 * 4);
+    uint4* s_j = s_j_all + ks * SJ;
+    const int tid = int(threadIdx.x) % (64 * NW), lane = tid & 63, wave = tid >> 6;
     const int l32 = lane & 31, half = lane >> 5;
     const int wt = wave % WT, wr = wave / WT;
 
@@ -242,7 +254,9 @@ __global__ __launch_bounds__(64 * WT * WR) __attribute__((amdgpu_waves_per_eu(2)
     float* __restrict__ y = G.y[gm];
     const int row0 = row_tile * RWG;
 
-    const int steps = n_in / 32, stages = steps / SSTEPS, n_sb = n_in / 256;
+    // the part's stages and super-blocks: s0 .. s0 + stages - 1, sb0 .. sb0 + nsb - 1
+    const int steps = n_in / 32, n_sb = n_in / 256, stages = steps / SSTEPS / KS, nsb = n_sb / KS;
+    const int s0 = ks * stages, sb0 = ks * nsb;
     const int tb0 = tok_tile * TBW + wt * TPW;       // first 32-token block of the wavefront
     int tb[TPW];
 #pragma unroll
@@ -266,7 +280,7 @@ __global__ __launch_bounds__(64 * WT * WR) __attribute__((amdgpu_waves_per_eu(2)
     auto load_stage = [&](Raw (&raw)[IPT], int stage) {
 #pragma unroll
         for (int j = 0; j < IPT; ++j)
-            load_raw<T>(raw[j], W, min(row0 + it_row[j], n_out - 1), stage * SSTEPS + it_step[j], n_in);
+            load_raw<T>(raw[j], W, min(row0 + it_row[j], n_out - 1), (s0 + stage) * SSTEPS + it_step[j], n_in);
     };
     auto store_stage = [&](const Raw (&raw)[IPT], int stage, int slot) {
 #pragma unroll
@@ -275,7 +289,7 @@ __global__ __launch_bounds__(64 * WT * WR) __attribute__((amdgpu_waves_per_eu(2)
                 if (!it_on[j]) continue;
             }
             uint4 o[2][2];
-            dequant<T>(raw[j], stage * SSTEPS + it_step[j], o);
+            dequant<T>(raw[j], (s0 + stage) * SSTEPS + it_step[j], o);
 #pragma unroll
             for (int p = 0; p < 2; ++p)
 #pragma unroll
@@ -289,7 +303,7 @@ __global__ __launch_bounds__(64 * WT * WR) __attribute__((amdgpu_waves_per_eu(2)
 #pragma unroll
     for (int b = 0; b < TPW; ++b) a_off[b] = tb[b] * steps * 64 + lane;
     auto load_a = [&](v4i (&a)[TPW][SSTEPS], int stage) {
-        const uint4* base = gA + size_t(stage) * (SSTEPS * 64);
+        const uint4* base = gA + size_t(s0 + stage) * (SSTEPS * 64);
 #pragma unroll
         for (int b = 0; b < TPW; ++b)
 #pragma unroll
@@ -315,10 +329,10 @@ __global__ __launch_bounds__(64 * WT * WR) __attribute__((amdgpu_waves_per_eu(2)
     // VALU work between its MFMAs.
     auto compute_stage = [&](v4i (&a)[TPW][SSTEPS], int slot, int next, const Raw (&raw)[IPT], int dq_stage,
                              int dq_slot) {
-        const uint4* base = gA + size_t(next) * (SSTEPS * 64);
+        const uint4* base = gA + size_t(s0 + next) * (SSTEPS * 64);
         DqPrep prep[IPT];
 #pragma unroll
-        for (int j = 0; j < IPT; ++j) prep[j] = dequant_prep<T>(raw[j], dq_stage * SSTEPS + it_step[j]);
+        for (int j = 0; j < IPT; ++j) prep[j] = dequant_prep<T>(raw[j], (s0 + dq_stage) * SSTEPS + it_step[j]);
         v4i bh[RPW], bl[RPW];
 #pragma unroll
         for (int r = 0; r < RPW; ++r) {
@@ -373,6 +387,7 @@ __global__ __launch_bounds__(64 * WT * WR) __attribute__((amdgpu_waves_per_eu(2)
     // every thread loads and stores (duplicate copies of the same values):
     // no divergent branch, so no wait for all outstanding loads
     auto load_epi = [&](int sb) {
+        sb += sb0;  // the part's super-block
         const size_t r = size_t(min(row0 + tid % RWG, n_out - 1));
         if constexpr (has_mins(T)) e_meta = *reinterpret_cast<const uint4*>(W.aux + (r * n_sb + sb) * 16);
         else e_meta.x = W.d[r * n_sb + sb];
@@ -475,13 +490,38 @@ __global__ __launch_bounds__(64 * WT * WR) __attribute__((amdgpu_waves_per_eu(2)
         slot = slot + 1 == RING ? 0 : slot + 1;
         // odd stage i + 1: raw1 holds stage i + 3
         __syncthreads();
-        load_epi(min((i >> 1) + 1, n_sb - 1));
+        load_epi(min((i >> 1) + 1, nsb - 1));
         __builtin_amdgcn_sched_barrier(0);
         load_stage(raw0, min(i + 4, stages - 1));
         __builtin_amdgcn_sched_barrier(0);
         compute_stage(a0, slot, min(i + 2, stages - 1), raw1, i + 3, slot + 2 >= RING ? slot + 2 - RING : slot + 2);
         slot = slot + 1 == RING ? 0 : slot + 1;
         epilogue();
+    }
+
+    if constexpr (KS == 2) {
+        // the second part's sums go through LDS to the same lane of the first part's
+        // same wavefront, which adds them to its own (first part + second part)
+        constexpr int NV = TPW * RPW * 16;
+        static_assert(size_t(NV) * 64 * NW * 4 <= sizeof(s_b_all), "exchange fits the LDS rings");
+        float* xch = reinterpret_cast<float*>(s_b_all) + size_t(tid) * NV;
+        __syncthreads();  // every wavefront is done with the rings
+        if (ks == 1) {
+#pragma unroll
+            for (int b = 0; b < TPW; ++b)
+#pragma unroll
+                for (int r = 0; r < RPW; ++r)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) xch[(b * RPW + r) * 16 + i] = accY[b][r][i];
+        }
+        __syncthreads();
+        if (ks == 1) return;
+#pragma unroll
+        for (int b = 0; b < TPW; ++b)
+#pragma unroll
+            for (int r = 0; r < RPW; ++r)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) accY[b][r][i] = accY[b][r][i] + xch[(b * RPW + r) * 16 + i];
     }
 
     // ---- store: lane owns row block r's row, register i of token block b is token 8 (i / 4) + 4 half + i % 4
@@ -499,6 +539,12 @@ __global__ __launch_bounds__(64 * WT * WR) __attribute__((amdgpu_waves_per_eu(2)
     }
 }
 
+// KS = 2 (two K parts per workgroup) for grids of at most one workgroup per CU whose
+// super-blocks split evenly: measured at M = 512, down (Q6_K 4096x14336, 256 workgroups)
+// 106 -> 94 us and o (4096x4096, 256) 32.6 -> 29.1 us, while the larger grids lost (gate+up,
+// 1792 workgroups: 171 -> 187 us). The split changes the order of the f32 additions, so a
+// tensor's outputs can differ in the last bits between a launch that splits and one that
+// does not (a large group and the same tensor alone).
 template <uint32_t T, int WT, int WR, int TPW, int RPW>
 hipError_t gemm_launch(GemmGroup G, const int* n_outs, const ActPtrs& A, int n_in, int n_tok, hipStream_t s) {
     int tiles = 0;
@@ -507,8 +553,13 @@ hipError_t gemm_launch(GemmGroup G, const int* n_outs, const ActPtrs& A, int n_i
         G.tiles_end[j] = tiles;
     }
     const int tok_tiles = (n_tok + 32 * TPW * WT - 1) / (32 * TPW * WT);
-    hipLaunchKernelGGL((gemm_kq_kernel<T, WT, WR, TPW, RPW>), dim3(unsigned(tiles * tok_tiles)), dim3(64 * WT * WR),
-                       0, s, G, A, n_in, n_tok, tok_tiles);
+    const dim3 grid(unsigned(tiles * tok_tiles));
+    if ((n_in / 256) % 2 == 0 && tiles * tok_tiles <= kGemmCUs)
+        hipLaunchKernelGGL((gemm_kq_kernel<T, WT, WR, TPW, RPW, 2>), grid, dim3(2 * 64 * WT * WR), 0, s, G, A, n_in,
+                           n_tok, tok_tiles);
+    else
+        hipLaunchKernelGGL((gemm_kq_kernel<T, WT, WR, TPW, RPW, 1>), grid, dim3(64 * WT * WR), 0, s, G, A, n_in,
+                           n_tok, tok_tiles);
     return hipGetLastError();
 }
 

@@ -195,7 +195,10 @@ def test_matmul_matches_reference_golden(torch_dev, golden, t, k):
 ])
 def test_full_size_shapes(torch_dev, oracle, t, n_out, n_in, n_tok):
     """Full-size shapes: all rows on the GPU; a row/token sample checked against
-    the oracle, and row slicing must reproduce the full result bit for bit."""
+    the oracle, and row slicing must reproduce the full result: bit for bit, except
+    where the slice's small grid takes the GEMM's two-part K split and the full one
+    does not (the two halves' sums are then added once more at the end: f32
+    rounding of the same sum, bounded here at 1e-6 of the largest output)."""
     torch, d = torch_dev
     rows_np = packed_weights(oracle, t, n_out, n_in, 7, 0.02)
     x = normal(8, (n_tok, n_in))
@@ -207,10 +210,15 @@ def test_full_size_shapes(torch_dev, oracle, t, n_out, n_in, n_tok):
     sub = np.concatenate([rows_np[i * rb:(i + 1) * rb] for i in sel_rows])
     want = oracle.matmul_f32(t, sub, x[sel_tok], sel_rows.size)
     check_close(y[np.ix_(sel_tok, sel_rows)], want, f"{fh.TYPE_NAMES[t]} {n_out}x{n_in} M={n_tok}")
-    # row slicing: the first 1024 rows on their own give identical bits
+    # row slicing: the first 1024 rows on their own give the same outputs
     w_part = fh.repack(t, dev_u8(torch_dev, rows_np[:1024 * rb]), n_in, 1024)
     y_part = fh.matmul_batch(t, w_part, dev_f32(torch_dev, x), 1024).cpu().numpy()
-    assert np.array_equal(y_part, y[:, :1024])
+    split_differs = fh.BLOCK_ELEMS[t] == 256 and n_tok > 64 and (n_in // 256) % 2 == 0
+    if split_differs:
+        err = float(np.abs(y_part - y[:, :1024]).max())
+        assert err <= 1e-6 * float(np.abs(y).max()), err
+    else:
+        assert np.array_equal(y_part, y[:, :1024])
 
 
 @pytest.mark.parametrize("t,n_tok", [(fh.Q4_K, 130), (fh.Q6_K, 200), (fh.Q4_K, 512), (fh.Q4_K, 3), (fh.Q4_0, 70),
