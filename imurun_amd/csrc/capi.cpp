@@ -777,8 +777,13 @@ private:
             } else if (e == hipSuccess) {
                 e = run_group(W + 4, 2, B.xb2, n_tok, E, n_f, y_gu, act);
             }
-            if (e == hipSuccess) e = launch_silu_mul(B.g, B.u, T * F, stream_, sp_.gelu != 0);
-            if (e == hipSuccess) e = run_group(W + 6, 1, B.g, n_tok, F, n_e, y_d, act);
+            // act(g) * u: formed by the down projection's quantization when that reads only
+            // the quantized h (one launch fewer, g read once), else a launch of its own
+            const GateUp gu{B.u, B.g, sp_.gelu != 0};
+            const bool gu_q = quantizes_input(W + 6, 1, n_tok);
+            if (e == hipSuccess && !gu_q) e = launch_silu_mul(B.g, B.u, T * F, stream_, sp_.gelu != 0);
+            if (e == hipSuccess)
+                e = run_group(W + 6, 1, B.g, n_tok, F, n_e, y_d, act, nullptr, nullptr, kActNone, gu_q ? &gu : nullptr);
             // Gemma-2: the FFN output normed before the residual add (model.cpp:1791-1793)
             if (e == hipSuccess && post_f)
                 e = launch_rmsnorm(B.dn, nullptr, nullptr, post_f, B.dn, n_tok, E, sp_.eps, stream_);
@@ -857,12 +862,25 @@ private:
         return true;
     }
 
+    // A group of more than one token whose every tensor is int8 reads only the
+    // quantized activations, so an activation applied by the quantization reaches
+    // all of them.
+    static bool quantizes_input(const Resident* const* rs, int n, int n_tok) {
+        if (n_tok < 2) return false;
+        for (int i = 0; i < n; ++i)
+            if (!int8_type(rs[i]->layout.type)) return false;
+        return true;
+    }
+
     // norm (one token, foldable tensors only): the RowNorm prologue of every fused launch;
-    // pair_act (gate and up of one type and shape, with a norm): dys[0] = act(gate) * up
+    // pair_act (gate and up of one type and shape, with a norm): dys[0] = act(gate) * up;
+    // gu (int8 tensors of more than one token): the input is act(dx) * gu->u, formed by the
+    // quantization and written to gu->h
     hipError_t run_group(const Resident* const* rs, int n, const float* dx, int n_tok, int n_in, const int* n_outs,
                          float* const* dys, void* act, const RowNorm* norm = nullptr,
-                         const RowResid* resid = nullptr, int pair_act = kActNone) {
+                         const RowResid* resid = nullptr, int pair_act = kActNone, const GateUp* gu = nullptr) {
         if ((norm || resid) && (n_tok != 1 || n > kGemmGroupMax || !foldable(rs, n))) return hipErrorInvalidValue;
+        if (gu && !quantizes_input(rs, n, n_tok)) return hipErrorInvalidValue;
         if (resid && n != 1) return hipErrorInvalidValue;
         bool any_int8 = false;
         for (int i = 0; i < n; ++i) any_int8 = any_int8 || int8_type(rs[i]->layout.type);
@@ -909,7 +927,8 @@ private:
             unsigned planes = 0;  // what this group's int8 tensors read, nothing else
             for (int i = 0; i < n; ++i)
                 if (int8_type(rs[i]->layout.type)) planes |= planes_of(rs[i]->layout, n_tok);
-            e = launch_quantize(dx, n_tok, n_in, n_in, act, nullptr, nullptr, stream_, planes);
+            if (gu) e = launch_quantize(dx, n_tok, n_in, n_in, act, nullptr, nullptr, stream_, planes, gu->u, gu->h, gu->gelu);
+            else e = launch_quantize(dx, n_tok, n_in, n_in, act, nullptr, nullptr, stream_, planes);
         }
         // tensors of one K-quant type go out as one grouped launch when the batch is GEMM-sized
         bool one_group = n <= kGemmGroupMax;

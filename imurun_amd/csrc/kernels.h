@@ -34,10 +34,12 @@ inline unsigned planes_for_tokens(int n_tok, int n_in) {
 // f32 x[n_tok][ldx] -> device activation buffer `act` (act_layout(n_tok, n_in)),
 // the planes in `planes` only. aos32 / aos256 (nullable) receive FISH's
 // Q8Act / Q8ActK bytes as well. With u != nullptr the quantized values are
-// silu(x) * u (FFN gate and up, ops.cpp:25-30 and model.cpp:1504-1508),
-// optionally also written to h_out.
+// silu(x) * u, or gelu(x) * u with gelu set (FFN gate and up, ops.cpp:25-38
+// and model.cpp:1504-1508), optionally also written to h_out (row stride
+// n_in; h_out == x rewrites x in place when ldx == n_in).
 hipError_t launch_quantize(const float* x, int n_tok, int n_in, int ldx, void* act, void* aos32, void* aos256,
-                           hipStream_t stream, unsigned planes, const float* u = nullptr, float* h_out = nullptr);
+                           hipStream_t stream, unsigned planes, const float* u = nullptr, float* h_out = nullptr,
+                           bool gelu = false);
 
 // Expert routing from router logits (model.cpp:1528-1547) and grouping of
 // the chosen (token, expert) pairs by expert, tokens ascending
@@ -132,6 +134,14 @@ struct RowNorm {
 struct RowResid {
     float* x;
     const float* bias;
+};
+// An FFN's hidden activation formed by the quantization of the down
+// projection's input (more than one token): h = act(g) * u, written to h
+// (which may be g itself).
+struct GateUp {
+    const float* u;
+    float* h;
+    bool gelu;
 };
 // Tensors of two K-quant types (Q4_K with Q5_K or Q6_K, Q5_K with Q6_K) may share
 // one launch when gemv_x_mixed_supported (n_in 2048..8192): both read the same

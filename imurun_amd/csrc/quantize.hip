@@ -130,11 +130,12 @@ __device__ __forceinline__ void quantize_chunk(float4 v, int t, int c, int n_tok
 
 // One wavefront per (token, run of CPW consecutive chunks): the run's loads are
 // all issued before the first chunk is quantized, so each wavefront keeps
-// CPW KB (2 CPW KB with u) in flight.
+// CPW KB (2 CPW KB with u) in flight. With u the values quantized are
+// act(x) * u (SiLU, or the tanh GELU when gelu is set), written to h_out when
+// given; h_out may be x itself (each value is read and rewritten by one lane).
 template <int CPW, bool GEMM_ONLY>
-__global__ __launch_bounds__(256) void quantize_kernel(const float* __restrict__ x, int n_tok, int n_in, int ldx,
-                                                       QuantOut o, const float* __restrict__ u,
-                                                       float* __restrict__ h_out) {
+__global__ __launch_bounds__(256) void quantize_kernel(const float* x, int n_tok, int n_in, int ldx, QuantOut o,
+                                                       const float* __restrict__ u, float* h_out, int gelu) {
     const int lane = threadIdx.x & 63;
     const int chunks = (n_in + 255) / 256, runs = (chunks + CPW - 1) / CPW;
     const long wave = long(blockIdx.x) * 4 + (threadIdx.x >> 6);
@@ -150,13 +151,21 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float* __restrict__
         if (t < n_tok && c0 + j < chunks && k0 < n_in) v[j] = *reinterpret_cast<const float4*>(x + size_t(t) * ldx + k0);
     }
     if (u) {
+        // every load of the run before the first store (h_out may be x)
+        float4 w[CPW];
+#pragma unroll
+        for (int j = 0; j < CPW; ++j) {
+            const int k0 = (c0 + j) * 256 + lane * 4;
+            w[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (t < n_tok && c0 + j < chunks && k0 < n_in) w[j] = *reinterpret_cast<const float4*>(u + size_t(t) * ldx + k0);
+        }
+        const bool ge = gelu != 0;
 #pragma unroll
         for (int j = 0; j < CPW; ++j) {
             const int k0 = (c0 + j) * 256 + lane * 4;
             if (t < n_tok && c0 + j < chunks && k0 < n_in) {
-                const float4 w = *reinterpret_cast<const float4*>(u + size_t(t) * ldx + k0);
-                v[j] = make_float4(silu_mul(v[j].x, w.x), silu_mul(v[j].y, w.y), silu_mul(v[j].z, w.z),
-                                   silu_mul(v[j].w, w.w));
+                v[j] = make_float4(act_mul(v[j].x, w[j].x, ge), act_mul(v[j].y, w[j].y, ge),
+                                   act_mul(v[j].z, w[j].z, ge), act_mul(v[j].w, w[j].w, ge));
                 if (h_out) *reinterpret_cast<float4*>(h_out + size_t(t) * n_in + k0) = v[j];
             }
         }
@@ -169,7 +178,7 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float* __restrict__
 }  // namespace
 
 hipError_t launch_quantize(const float* x, int n_tok, int n_in, int ldx, void* act, void* aos32, void* aos256,
-                           hipStream_t stream, unsigned planes, const float* u, float* h_out) {
+                           hipStream_t stream, unsigned planes, const float* u, float* h_out, bool gelu) {
     const ActLayout L = act_layout(n_tok, n_in);
     if (!L.total) return hipErrorInvalidValue;
     uint8_t* b = static_cast<uint8_t*>(act);
@@ -199,18 +208,18 @@ hipError_t launch_quantize(const float* x, int n_tok, int n_in, int ldx, void* a
         const unsigned blocks = unsigned((rows * ((chunks + 3) / 4) + 3) / 4);
         if (gemm_only)
             hipLaunchKernelGGL((quantize_kernel<4, true>), dim3(blocks), dim3(256), 0, stream, x, n_tok, n_in, ldx, o,
-                               u, h_out);
+                               u, h_out, gelu ? 1 : 0);
         else
             hipLaunchKernelGGL((quantize_kernel<4, false>), dim3(blocks), dim3(256), 0, stream, x, n_tok, n_in, ldx,
-                               o, u, h_out);
+                               o, u, h_out, gelu ? 1 : 0);
     } else {
         const unsigned blocks = unsigned((rows * chunks + 3) / 4);
         if (gemm_only)
             hipLaunchKernelGGL((quantize_kernel<1, true>), dim3(blocks), dim3(256), 0, stream, x, n_tok, n_in, ldx, o,
-                               u, h_out);
+                               u, h_out, gelu ? 1 : 0);
         else
             hipLaunchKernelGGL((quantize_kernel<1, false>), dim3(blocks), dim3(256), 0, stream, x, n_tok, n_in, ldx,
-                               o, u, h_out);
+                               o, u, h_out, gelu ? 1 : 0);
     }
     return hipGetLastError();
 }
