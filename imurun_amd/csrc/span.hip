@@ -354,8 +354,9 @@ __global__ __launch_bounds__(kTh) void attn_part_kernel(const float* __restrict_
         __builtin_amdgcn_sched_barrier(0);
     }
 
-    // scores of positions j0 + w + 4 b
-    KvRaw kv[PB][NP];
+    // scores of positions j0 + w + 4 b; their V rows are loaded with the K rows, so the
+    // chunk waits for the cache once
+    KvRaw kv[PB][NP], vv[PB][NP];
 #pragma unroll
     for (int b = 0; b < PB; ++b) {
         const size_t rb = size_t(min(j0 + w + 4 * b, jn)) * KV + hoff;
@@ -363,6 +364,15 @@ __global__ __launch_bounds__(kTh) void attn_part_kernel(const float* __restrict_
         for (int i = 0; i < NP; ++i) {
             const int e = 2 * (lane + 64 * i);
             kv[b][i] = e < D ? kv_raw<Q8>(kc, rb + e) : KvRaw{0u, 0.0f};
+        }
+    }
+#pragma unroll
+    for (int b = 0; b < PB; ++b) {
+        const size_t rb = size_t(min(j0 + w + 4 * b, jn)) * KV + hoff;
+#pragma unroll
+        for (int i = 0; i < NP; ++i) {
+            const int e = 2 * (lane + 64 * i);
+            vv[b][i] = e < D ? kv_raw<Q8>(vc, rb + e) : KvRaw{0u, 0.0f};
         }
     }
     float2 qv[NP];
@@ -462,16 +472,6 @@ __global__ __launch_bounds__(kTh) void attn_part_kernel(const float* __restrict_
         }
     }
     __syncthreads();
-    KvRaw vv[PB][NP];
-#pragma unroll
-    for (int b = 0; b < PB; ++b) {
-        const size_t rb = size_t(min(j0 + w + 4 * b, jn)) * KV + hoff;
-#pragma unroll
-        for (int i = 0; i < NP; ++i) {
-            const int e = 2 * (lane + 64 * i);
-            vv[b][i] = e < D ? kv_raw<Q8>(vc, rb + e) : KvRaw{0u, 0.0f};
-        }
-    }
     if constexpr (PREP) {
         if (own) {
 #pragma unroll
@@ -505,38 +505,60 @@ __global__ __launch_bounds__(kTh) void attn_part_kernel(const float* __restrict_
     }
 }
 
+// Chunks past the token's position hold nothing and are not read. Every load of
+// the first kTh chunks' (m, l) and of the first kCombineRegs chunks' o is issued
+// before the first wait, so a decode token's combine waits on memory once.
+constexpr int kCombineRegs = 16;
 __global__ __launch_bounds__(kTh) void attn_combine_kernel(const float* __restrict__ part, float* __restrict__ out,
-                                                           int S, int H, int D) {
-    __shared__ float red[kTh];
+                                                           int S, int H, int D, int pos0,
+                                                           const int* __restrict__ pos_dev) {
+    __shared__ float s_red[2][kTh / 64];
     __shared__ float s_w[kTh];
-    const int item = blockIdx.x, t = item / H, h = item % H, tid = threadIdx.x;
+    if (pos_dev) pos0 = *pos_dev;
+    const int item = blockIdx.x, t = item / H, h = item % H, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int sv = min(S, (pos0 + t) / kCh + 1);  // chunks holding positions up to the token's
     const size_t st = size_t(D + 2);
     const float* pp = part + size_t(item) * S * st;
-    float m = -INFINITY;
-    for (int c = tid; c < S; c += kTh) m = fmaxf(m, pp[size_t(c) * st + D]);
-    const float M = block_reduce_f(m, red, true);
-    float l = 0.0f, o = 0.0f;
-    for (int c0 = 0; c0 < S; c0 += kTh) {
-        const int c = c0 + tid;
-        float wc = 0.0f;
-        if (c < S) {
-            const float mc = pp[size_t(c) * st + D];
-            wc = mc == -INFINITY ? 0.0f : expf(mc - M);
-            l += pp[size_t(c) * st + D + 1] * wc;
-        }
-        s_w[tid] = wc;
-        __syncthreads();
-        const int nc = min(kTh, S - c0);
-        if (tid < D) {
-            const float* pc = pp + size_t(c0) * st + tid;
-#pragma unroll 8
-            for (int cc = 0; cc < nc; ++cc) o += pc[size_t(cc) * st] * s_w[cc];
-        }
-        __syncthreads();
+    float o_r[kCombineRegs];
+#pragma unroll
+    for (int c = 0; c < kCombineRegs; ++c) o_r[c] = (tid < D && c < sv) ? pp[size_t(c) * st + tid] : 0.0f;
+    const float mc = tid < sv ? pp[size_t(tid) * st + D] : -INFINITY;
+    const float lc = tid < sv ? pp[size_t(tid) * st + D + 1] : 0.0f;
+    float m = mc;
+    for (int c = tid + kTh; c < sv; c += kTh) m = fmaxf(m, pp[size_t(c) * st + D]);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    if (lane == 0) s_red[0][wv] = m;
+    __syncthreads();
+    float M = s_red[0][0];
+#pragma unroll
+    for (int i = 1; i < kTh / 64; ++i) M = fmaxf(M, s_red[0][i]);
+    // chunk weights exp(m - M); an empty chunk (m = -inf) weighs 0
+    const float wc = mc == -INFINITY ? 0.0f : expf(mc - M);
+    s_w[tid] = wc;
+    float l = lc * wc;
+    for (int c = tid + kTh; c < sv; c += kTh) {
+        const float mx = pp[size_t(c) * st + D];
+        l += pp[size_t(c) * st + D + 1] * (mx == -INFINITY ? 0.0f : expf(mx - M));
     }
-    const float L = block_reduce_f(l, red, false);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) l += __shfl_xor(l, off);
+    if (lane == 0) s_red[1][wv] = l;
+    __syncthreads();
+    float L = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kTh / 64; ++i) L += s_red[1][i];
+    if (tid >= D) return;
+    float o = 0.0f;
+#pragma unroll
+    for (int c = 0; c < kCombineRegs; ++c) o += o_r[c] * s_w[c];
+    for (int c = kCombineRegs; c < min(sv, kTh); ++c) o += pp[size_t(c) * st + tid] * s_w[c];
+    for (int c = kTh; c < sv; ++c) {
+        const float mx = pp[size_t(c) * st + D];
+        o += pp[size_t(c) * st + tid] * (mx == -INFINITY ? 0.0f : expf(mx - M));
+    }
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-    if (tid < D) out[size_t(t) * H * D + size_t(h) * D + tid] = o * inv;
+    out[size_t(t) * H * D + size_t(h) * D + tid] = o * inv;
 }
 
 // Attention of more tokens (prefill): one workgroup per (token, head) walks
@@ -876,7 +898,8 @@ void attention_split(const float* q, const KvCache& kc, const KvCache& vc, float
     else
         hipLaunchKernelGGL((attn_part_kernel<2, false, Q8>), grid, block, 0, s, q, kc, vc, part, S, H, HKV, D, pos0,
                            pos_dev, scale, softcap, window, P);
-    hipLaunchKernelGGL(attn_combine_kernel, dim3(unsigned(n_tok * H)), block, 0, s, part, out, S, H, D);
+    hipLaunchKernelGGL(attn_combine_kernel, dim3(unsigned(n_tok * H)), block, 0, s, part, out, S, H, D, pos0,
+                       pos_dev);
 }
 
 template <bool Q8>
@@ -891,7 +914,7 @@ void attention_prep(const AttnPrep& P, const KvCache& kc, const KvCache& vc, flo
     else
         hipLaunchKernelGGL((attn_part_kernel<2, true, Q8>), grid, block, 0, s, P.q_out, kc, vc, part, S, H, HKV, D,
                            pos0, pos_dev, scale, softcap, window, P);
-    hipLaunchKernelGGL(attn_combine_kernel, dim3(unsigned(H)), block, 0, s, part, out, S, H, D);
+    hipLaunchKernelGGL(attn_combine_kernel, dim3(unsigned(H)), block, 0, s, part, out, S, H, D, pos0, pos_dev);
 }
 
 }  // namespace
