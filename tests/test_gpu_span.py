@@ -409,6 +409,27 @@ def test_span_kv_rewind_then_new_tokens(oracle):
             be.release(n)
 
 
+@pytest.mark.parametrize("variant", ["llama", "gemma2"])
+def test_span_decode_at_long_positions(oracle, variant):
+    """One-token calls with 6 and then 16-17 chunks of 64 positions behind the token, after
+    prefills of more than one 256-token chunk: the combine then also reads chunks past the
+    16 whose outputs it loads up front. Gemma-2's soft cap and 24-position window ride along;
+    every stage is checked as above."""
+    be = fh.HipBackend()
+    names, ref, _ = setup_span(oracle, be, D, variant, f"long{variant}", ctx=1100)
+    try:
+        check_call(be, ref, normal(701, (383, E), 1.0), 0, "prefill to 383")
+        for p in (383, 384, 385):
+            check_call(be, ref, normal(702 + p, (1, E), 1.0), p, f"decode at {p}")
+        check_call(be, ref, normal(703, (637, E), 1.0), 386, "prefill to 1023")
+        for p in (1023, 1024, 1025):
+            check_call(be, ref, normal(704 + p, (1, E), 1.0), p, f"decode at {p}")
+    finally:
+        be.span_release()
+        for n in names:
+            be.release(n)
+
+
 def test_span_prefill_longer_than_one_chunk(oracle):
     """A batch of 300 tokens (more than FISH's 256-token forward batch) runs as two chunks, the
     second attending over the cache rows the first wrote."""
