@@ -673,33 +673,46 @@ __global__ __launch_bounds__(kTh) void attn_full_kernel(const float* __restrict_
     if (tid < D) out[size_t(t) * Q + size_t(h) * D + tid] = o_run * (1.0f / l_run);
 }
 
-// Attention of more tokens on f32 MFMA (v_mfma_f32_32x32x2_f32), for head
-// dims D of 64 or 128. One workgroup (four wavefronts) per (block of 32
+// Attention of more tokens on MFMA, for head dims D of 64 or 128. One
+// workgroup (four wavefronts) per (block of 32
 // tokens, head); wavefront w takes the key blocks of 32 positions
 // b = b_lo + w, b_lo + w + 4, ... that the block's tokens can see, keeps a
 // running max, sum and output per token, and the four are merged at the end
 // (exact max, then the four sums and outputs rescaled and added in wavefront
 // order). The tiles are transposed so that tokens run along lanes:
-//   S^T = K Q^T   (32 keys x 32 tokens; k = the D head values, two per step),
+//   S^T = K Q^T   (32 keys x 32 tokens; k = the D head values),
 //   O^T += V^T P^T (D values x 32 tokens in D / 32 tiles; k = the 32 keys).
 // In the 32x32 MFMA output a lane holds one column (its token) and 16 rows:
 // register r of lane half h is row 8 (r / 4) + 4 h + r % 4. So a token's
 // softmax statistics stay in its own two lanes (l, l + 32), and the
 // probabilities of S^T are already the B operand of the second product when
-// its k order is taken to be that row order (step r pairs the keys of
-// register r in the two halves). K and V rows are staged through LDS per
+// its k order is taken to be that row order. K and V rows are staged through LDS per
 // wavefront, rows past the block's last position as zeros (so a masked
 // probability of 0 never meets a never-written cache row). Mathematically
 // FISH's softmax (ops.cpp:331-350); the rounding order differs.
 constexpr int kAttnMfmaTok = 32;
-
+// The tiles run on f16 MFMA (v_mfma_f32_32x32x16_f16, 8x the rate of the f32
+// form v_mfma_f32_32x32x2_f32) at f32 accuracy: K and V are f16 in the cache
+// already, so only q and p are split, x = hi + lo with hi = f16(x),
+// lo = f16(x - hi), and each product takes two MFMAs (K q hi + K q lo,
+// V p hi + V p lo). f16 x f16 products are exact in the f32 accumulator, and
+// what the split drops is below 2^-22 of |x| (2^-25 absolute where the lo part
+// is subnormal). A token's q is first scaled by a power of two (its scores by
+// the inverse) when its largest value exceeds 2^14, so hi never overflows.
+// Operand lanes of the 32x32x16 form: A row = lane % 32, k = 8 (lane / 32) + e;
+// B k likewise, column = lane % 32; the output as in the f32 form (register r
+// of lane half h is row 8 (r / 4) + 4 h + r % 4). For O^T += V^T P^T the 8 k
+// slots of a lane are the keys its S^T registers r = 8 u .. 8 u + 7 hold
+// (16 u + 8 (e / 4) + 4 hf + e % 4), so p is the B operand straight from
+// registers and V^T is gathered from the staged rows in that key order.
 template <int D>
-__global__ __launch_bounds__(256) void attn_mfma_kernel(const float* __restrict__ q, const _Float16* __restrict__ kc,
-                                                        const _Float16* __restrict__ vc, float* __restrict__ out,
-                                                        int n_tok, int ld, int H, int HKV, int pos0, float scale,
-                                                        float softcap, int window) {
+__global__ __launch_bounds__(256) void attn_mfma16_kernel(const float* __restrict__ q, const _Float16* __restrict__ kc,
+                                                          const _Float16* __restrict__ vc, float* __restrict__ out,
+                                                          int n_tok, int ld, int H, int HKV, int pos0, float scale,
+                                                          float softcap, int window) {
     typedef float v16f __attribute__((ext_vector_type(16)));
-    constexpr int NS = D / 2;      // k-steps of S^T
+    typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+    constexpr int NK = D / 16;     // k-steps of S^T
     constexpr int DT = D / 32;     // 32-row tiles of O^T
     constexpr int KROW = D + 8;    // LDS row stride in halves (16 bytes of padding)
     constexpr int STAGE = 2 * 4 * 32 * KROW * 2;                // K and V rows of the four wavefronts
@@ -716,11 +729,38 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(const float* __restrict_
     const int first_lo = window > 0 ? max(0, pos0 + t0 - window + 1) : 0;
     const int kb_lo = first_lo / 32, kb_hi = pos_last / 32;
 
-    // Q^T operand: step s uses q[t][2 s + hf]
-    float qv[NS];
+    // Q^T operand: step kk uses q[t][16 kk + 8 hf + e], split into hi + lo
     const float* qr = q + size_t(tc) * Q + size_t(head) * D;
+    float qf[NK][8];
+    float qmax = 0.0f;
 #pragma unroll
-    for (int s = 0; s < NS; ++s) qv[s] = qr[2 * s + hf];
+    for (int kk = 0; kk < NK; ++kk) {
+        const float4 a = *reinterpret_cast<const float4*>(qr + 16 * kk + 8 * hf);
+        const float4 b = *reinterpret_cast<const float4*>(qr + 16 * kk + 8 * hf + 4);
+        qf[kk][0] = a.x; qf[kk][1] = a.y; qf[kk][2] = a.z; qf[kk][3] = a.w;
+        qf[kk][4] = b.x; qf[kk][5] = b.y; qf[kk][6] = b.z; qf[kk][7] = b.w;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qmax = fmaxf(qmax, fabsf(qf[kk][e]));
+    }
+    qmax = fmaxf(qmax, __shfl_xor(qmax, 32));
+    // the token's power-of-two scale: 2^-sh brings its largest value to at most 2^14
+    int sh = 0;
+    if (qmax > 16384.0f) {
+        int ex;
+        (void)frexpf(qmax, &ex);  // qmax = f 2^ex, 0.5 <= f < 1
+        sh = ex - 14;
+    }
+    const float sc_out = sh ? ldexpf(scale, sh) : scale;
+    v8h qh[NK], ql[NK];
+#pragma unroll
+    for (int kk = 0; kk < NK; ++kk)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float x = sh ? ldexpf(qf[kk][e], -sh) : qf[kk][e];
+            const _Float16 h = _Float16(x);
+            qh[kk][e] = h;
+            ql[kk][e] = _Float16(x - float(h));
+        }
 
     _Float16* sk = reinterpret_cast<_Float16*>(s_mem) + size_t(w) * 32 * KROW;
     _Float16* sv = reinterpret_cast<_Float16*>(s_mem) + size_t(4 + w) * 32 * KROW;
@@ -748,14 +788,13 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(const float* __restrict_
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        // S^T = K Q^T, two accumulators
+        // S^T = K Q^T: rows = the block's keys (A from LDS), columns = tokens
         v16f s0 = v16f{}, s1 = v16f{};
 #pragma unroll
-        for (int s = 0; s < NS; s += 2) {
-            const float k0 = float(sk[col * KROW + 2 * s + hf]);
-            const float k1 = float(sk[col * KROW + 2 * s + 2 + hf]);
-            s0 = __builtin_amdgcn_mfma_f32_32x32x2f32(k0, qv[s], s0, 0, 0, 0);
-            s1 = __builtin_amdgcn_mfma_f32_32x32x2f32(k1, qv[s + 1], s1, 0, 0, 0);
+        for (int kk = 0; kk < NK; ++kk) {
+            const v8h ka = *reinterpret_cast<const v8h*>(sk + col * KROW + 16 * kk + 8 * hf);
+            s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qh[kk], s0, 0, 0, 0);
+            s1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, ql[kk], s1, 0, 0, 0);
         }
         // scores of this lane's token over its 16 keys (the other 16 are in lane l ^ 32)
         float p[16];
@@ -763,7 +802,7 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(const float* __restrict_
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int j = j0 + 8 * (r >> 2) + 4 * hf + (r & 3);
-            const float sc = score(s0[r] + s1[r], scale, softcap);
+            const float sc = score(s0[r] + s1[r], sc_out, softcap);
             p[r] = (j <= pos && j >= jlo) ? sc : -INFINITY;
             mx = fmaxf(mx, p[r]);
         }
@@ -781,14 +820,26 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(const float* __restrict_
         m_run = mn;
 #pragma unroll
         for (int c = 0; c < DT; ++c) o[c] *= a;
-        // O^T += V^T P^T; step r pairs the keys of register r in the two halves
+        // O^T += V^T P^T over the keys of registers 8 u .. 8 u + 7
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int kr = 8 * (r >> 2) + 4 * hf + (r & 3);
+        for (int u = 0; u < 2; ++u) {
+            v8h ph, pl;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const _Float16 h = _Float16(p[8 * u + e]);
+                ph[e] = h;
+                pl[e] = _Float16(p[8 * u + e] - float(h));
+            }
 #pragma unroll
             for (int c = 0; c < DT; ++c) {
-                const float vv = float(sv[kr * KROW + 32 * c + col]);
-                o[c] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv, p[r], o[c], 0, 0, 0);
+                v8h va;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int kr = 16 * u + 8 * (e >> 2) + 4 * hf + (e & 3);
+                    va[e] = sv[kr * KROW + 32 * c + col];
+                }
+                o[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, ph, o[c], 0, 0, 0);
+                o[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pl, o[c], 0, 0, 0);
             }
         }
         __builtin_amdgcn_wave_barrier();  // the next block overwrites this wavefront's rows
@@ -947,10 +998,10 @@ hipError_t launch_attention(const float* q, const KvCache& kc, const KvCache& vc
         const _Float16* k16 = static_cast<const _Float16*>(kc.c);
         const _Float16* v16 = static_cast<const _Float16*>(vc.c);
         if (D == 64)
-            hipLaunchKernelGGL(attn_mfma_kernel<64>, grid, block, 0, s, q, k16, v16, out, n_tok, ld, H, HKV, pos0,
+            hipLaunchKernelGGL(attn_mfma16_kernel<64>, grid, block, 0, s, q, k16, v16, out, n_tok, ld, H, HKV, pos0,
                                scale, softcap, window);
         else
-            hipLaunchKernelGGL(attn_mfma_kernel<128>, grid, block, 0, s, q, k16, v16, out, n_tok, ld, H, HKV, pos0,
+            hipLaunchKernelGGL(attn_mfma16_kernel<128>, grid, block, 0, s, q, k16, v16, out, n_tok, ld, H, HKV, pos0,
                                scale, softcap, window);
         return hipGetLastError();
     }
