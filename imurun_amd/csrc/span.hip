@@ -768,23 +768,31 @@ __global__ __launch_bounds__(256) void attn_mfma16_kernel(const float* __restric
 #pragma unroll
     for (int c = 0; c < DT; ++c) o[c] = v16f{};
     float m_run = -INFINITY, l_run = 0.0f;
+    // rows j0 .. j0 + 31 of K and V, 16 bytes per lane per piece; the next block's
+    // pieces are loaded while the current block computes
+    constexpr int PCS = 32 * (D / 8) / 64;  // pieces per lane
+    uint4 nk[PCS], nv[PCS];
+    auto load_block = [&](int kb) {
+#pragma unroll
+        for (int pc = 0; pc < PCS; ++pc) {
+            const int i = lane + 64 * pc, r = i / (D / 8), c8 = i % (D / 8);
+            const size_t at = size_t(min(kb * 32 + r, ld - 1)) * KV + size_t(kvh) * D + size_t(c8) * 8;
+            nk[pc] = *reinterpret_cast<const uint4*>(kc + at);
+            nv[pc] = *reinterpret_cast<const uint4*>(vc + at);
+        }
+    };
+    if (kb_lo + w <= kb_hi) load_block(kb_lo + w);
     for (int kb = kb_lo + w; kb <= kb_hi; kb += 4) {  // uniform over the wavefront
         const int j0 = kb * 32;
-        // stage rows j0 .. j0 + 31 of K and V, 16 bytes per lane per step
+        // stage the block (rows past the block's last position as zeros)
 #pragma unroll
-        for (int i = lane; i < 32 * (D / 8); i += 64) {
-            const int r = i / (D / 8), c8 = i % (D / 8), j = j0 + r;
-            uint4 kv4 = make_uint4(0, 0, 0, 0), vv4 = make_uint4(0, 0, 0, 0);
-            const size_t at = size_t(min(j, ld - 1)) * KV + size_t(kvh) * D + size_t(c8) * 8;
-            const uint4 kl = *reinterpret_cast<const uint4*>(kc + at);
-            const uint4 vl = *reinterpret_cast<const uint4*>(vc + at);
-            if (j <= pos_last) {
-                kv4 = kl;
-                vv4 = vl;
-            }
-            *reinterpret_cast<uint4*>(sk + r * KROW + c8 * 8) = kv4;
-            *reinterpret_cast<uint4*>(sv + r * KROW + c8 * 8) = vv4;
+        for (int pc = 0; pc < PCS; ++pc) {
+            const int i = lane + 64 * pc, r = i / (D / 8), c8 = i % (D / 8);
+            const bool live = j0 + r <= pos_last;
+            *reinterpret_cast<uint4*>(sk + r * KROW + c8 * 8) = live ? nk[pc] : make_uint4(0, 0, 0, 0);
+            *reinterpret_cast<uint4*>(sv + r * KROW + c8 * 8) = live ? nv[pc] : make_uint4(0, 0, 0, 0);
         }
+        if (kb + 4 <= kb_hi) load_block(kb + 4);
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
