@@ -726,6 +726,16 @@ private:
             if (e == hipSuccess && fold) {
                 const RowNorm an{span_vec(l, 0), B.xb, sp_.eps};
                 e = run_group(W, 3, B.x, n_tok, E, n_qkv, y_qkv, act, &an);
+            } else if (e == hipSuccess && n_tok > 1) {
+                // the attention norm formed by the projections' quantization (one launch)
+                const PreNorm an{B.x, pending, nullptr, span_vec(l, 0), sp_.eps};
+                if (fq) {
+                    // fused q|k|v (model.cpp:1665-1674): one matmul, then its columns split
+                    e = run_group(W, 1, B.xb, n_tok, E, n_fq, y_fz, act, nullptr, nullptr, kActNone, nullptr, &an);
+                    if (e == hipSuccess) e = launch_split_rows(B.fz, n_tok, B.q, Q, B.k, KV, B.v, KV, stream_);
+                } else {
+                    e = run_group(W, 3, B.xb, n_tok, E, n_qkv, y_qkv, act, nullptr, nullptr, kActNone, nullptr, &an);
+                }
             } else if (e == hipSuccess) {
                 e = launch_rmsnorm(B.x, pending, nullptr, span_vec(l, 0), B.xb, n_tok, E, sp_.eps, stream_);
                 if (e == hipSuccess && fq) {
@@ -762,20 +772,20 @@ private:
                 continue;
             }
             if (e == hipSuccess) e = run_group(W + 3, 1, B.att, n_tok, Q, n_e, y_o, act);
-            if (e == hipSuccess && post_a) {
-                // Gemma-2: proj = rmsnorm(proj + bias_o) before the residual add (model.cpp:1756-1760)
+            // the FFN norm (x += proj (+ bias_o) first), formed by the gate / up quantization;
+            // Gemma-2 norms proj + bias_o itself before the residual add (model.cpp:1756-1760)
+            if (e == hipSuccess && post_a)
                 e = launch_rmsnorm(B.proj, nullptr, span_vec(l, 7), post_a, B.proj, n_tok, E, sp_.eps, stream_);
-                if (e == hipSuccess)
-                    e = launch_rmsnorm(B.x, B.proj, nullptr, span_vec(l, 1), B.xb2, n_tok, E, sp_.eps, stream_);
-            } else if (e == hipSuccess) {
-                e = launch_rmsnorm(B.x, B.proj, span_vec(l, 7), span_vec(l, 1), B.xb2, n_tok, E, sp_.eps, stream_);
-            }
+            const PreNorm fnorm{B.x, B.proj, post_a ? nullptr : span_vec(l, 7), span_vec(l, 1), sp_.eps};
+            const PreNorm* fpre = n_tok > 1 ? &fnorm : nullptr;  // one token: a launch of its own
+            if (e == hipSuccess && !fpre)
+                e = launch_rmsnorm(fnorm.x, fnorm.y, fnorm.b, fnorm.w, B.xb2, n_tok, E, sp_.eps, stream_);
             if (e == hipSuccess && fg) {
                 // fused gate|up, gate rows first (model.cpp:1481-1490)
-                e = run_group(W + 5, 1, B.xb2, n_tok, E, n_fg, y_fz, act);
+                e = run_group(W + 5, 1, B.xb2, n_tok, E, n_fg, y_fz, act, nullptr, nullptr, kActNone, nullptr, fpre);
                 if (e == hipSuccess) e = launch_split_rows(B.fz, n_tok, B.g, F, B.u, F, nullptr, 0, stream_);
             } else if (e == hipSuccess) {
-                e = run_group(W + 4, 2, B.xb2, n_tok, E, n_f, y_gu, act);
+                e = run_group(W + 4, 2, B.xb2, n_tok, E, n_f, y_gu, act, nullptr, nullptr, kActNone, nullptr, fpre);
             }
             // act(g) * u: formed by the down projection's quantization when that reads only
             // the quantized h (one launch fewer, g read once), else a launch of its own
@@ -875,12 +885,15 @@ private:
     // norm (one token, foldable tensors only): the RowNorm prologue of every fused launch;
     // pair_act (gate and up of one type and shape, with a norm): dys[0] = act(gate) * up;
     // gu (int8 tensors of more than one token): the input is act(dx) * gu->u, formed by the
-    // quantization and written to gu->h
+    // quantization and written to gu->h; pre (more than one token): the input dx is
+    // rmsnorm(pre->x) * pre->w, formed first, by the group's quantization when it has one
     hipError_t run_group(const Resident* const* rs, int n, const float* dx, int n_tok, int n_in, const int* n_outs,
                          float* const* dys, void* act, const RowNorm* norm = nullptr,
-                         const RowResid* resid = nullptr, int pair_act = kActNone, const GateUp* gu = nullptr) {
+                         const RowResid* resid = nullptr, int pair_act = kActNone, const GateUp* gu = nullptr,
+                         const PreNorm* pre = nullptr) {
         if ((norm || resid) && (n_tok != 1 || n > kGemmGroupMax || !foldable(rs, n))) return hipErrorInvalidValue;
         if (gu && !quantizes_input(rs, n, n_tok)) return hipErrorInvalidValue;
+        if (pre && (gu || n_tok < 2)) return hipErrorInvalidValue;
         if (resid && n != 1) return hipErrorInvalidValue;
         bool any_int8 = false;
         for (int i = 0; i < n; ++i) any_int8 = any_int8 || int8_type(rs[i]->layout.type);
@@ -923,12 +936,20 @@ private:
             return e;
         }
         hipError_t e = hipSuccess;
+        float* const xn = const_cast<float*>(dx);  // the norm's output (pre): the group's input
         if (!fused && any_int8) {
             unsigned planes = 0;  // what this group's int8 tensors read, nothing else
             for (int i = 0; i < n; ++i)
                 if (int8_type(rs[i]->layout.type)) planes |= planes_of(rs[i]->layout, n_tok);
-            if (gu) e = launch_quantize(dx, n_tok, n_in, n_in, act, nullptr, nullptr, stream_, planes, gu->u, gu->h, gu->gelu);
-            else e = launch_quantize(dx, n_tok, n_in, n_in, act, nullptr, nullptr, stream_, planes);
+            if (pre)
+                e = launch_rmsnorm_quantize(pre->x, pre->y, pre->b, pre->w, xn, n_tok, n_in, pre->eps, act, planes,
+                                            stream_);
+            else if (gu)
+                e = launch_quantize(dx, n_tok, n_in, n_in, act, nullptr, nullptr, stream_, planes, gu->u, gu->h, gu->gelu);
+            else
+                e = launch_quantize(dx, n_tok, n_in, n_in, act, nullptr, nullptr, stream_, planes);
+        } else if (pre) {
+            e = launch_rmsnorm(pre->x, pre->y, pre->b, pre->w, xn, n_tok, n_in, pre->eps, stream_);
         }
         // tensors of one K-quant type go out as one grouped launch when the batch is GEMM-sized
         bool one_group = n <= kGemmGroupMax;

@@ -40,6 +40,12 @@ inline unsigned planes_for_tokens(int n_tok, int n_in) {
 hipError_t launch_quantize(const float* x, int n_tok, int n_in, int ldx, void* act, void* aos32, void* aos256,
                            hipStream_t stream, unsigned planes, const float* u = nullptr, float* h_out = nullptr,
                            bool gelu = false);
+// A layer's RMS norm and the quantization of its output in one launch (more
+// than one token): x += y (+ b) when y is given, xn = rmsnorm(x) * w (written
+// to xn, rows of n), then xn quantized into `act` (the planes in `planes`).
+// Bit for bit the span's launch_rmsnorm followed by launch_quantize of xn.
+hipError_t launch_rmsnorm_quantize(float* x, const float* y, const float* b, const float* w, float* xn, int n_tok,
+                                   int n, float eps, void* act, unsigned planes, hipStream_t stream);
 
 // Expert routing from router logits (model.cpp:1528-1547) and grouping of
 // the chosen (token, expert) pairs by expert, tokens ascending
@@ -142,6 +148,16 @@ struct GateUp {
     const float* u;
     float* h;
     bool gelu;
+};
+// A layer's RMS norm in front of a group of more than one token (the span's
+// prefill): x += y (+ b) when y is given, then the group's input xn =
+// rmsnorm(x) * w; formed by the group's quantization when it has one.
+struct PreNorm {
+    float* x;
+    const float* y;
+    const float* b;
+    const float* w;
+    float eps;
 };
 // Tensors of two K-quant types (Q4_K with Q5_K or Q6_K, Q5_K with Q6_K) may share
 // one launch when gemv_x_mixed_supported (n_in 2048..8192): both read the same

@@ -177,10 +177,10 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float* x, int n_tok
 
 }  // namespace
 
-hipError_t launch_quantize(const float* x, int n_tok, int n_in, int ldx, void* act, void* aos32, void* aos256,
-                           hipStream_t stream, unsigned planes, const float* u, float* h_out, bool gelu) {
-    const ActLayout L = act_layout(n_tok, n_in);
-    if (!L.total) return hipErrorInvalidValue;
+namespace {
+
+// The outputs of act_layout L in `act` that `planes` asks for.
+QuantOut quant_out(const ActLayout& L, void* act, void* aos32, void* aos256, unsigned planes) {
     uint8_t* b = static_cast<uint8_t*>(act);
     const bool gemv = planes & kPlanesGemv, b32 = planes & kPlanesBatch32;
     const bool b256 = L.has256 && (planes & kPlanesBatch256), gemm = L.has256 && (planes & kPlanesGemm);
@@ -199,9 +199,77 @@ hipError_t launch_quantize(const float* x, int n_tok, int n_in, int ldx, void* a
     o.gJ = gemm ? reinterpret_cast<uint16_t*>(b + L.gJ) : nullptr;
     o.aos32 = static_cast<uint8_t*>(aos32);
     o.aos256 = L.has256 ? static_cast<uint8_t*>(aos256) : nullptr;
+    return o;
+}
+
+bool gemm_planes_only(const QuantOut& o) {
+    return o.gA && !o.q32 && !o.d32 && !o.d256 && !o.bsm && !o.m32 && !o.m256 && !o.aos32 && !o.aos256;
+}
+
+// RMS norm of one token row, then its quantization, in one workgroup of
+// kNormQTh threads: x += y (+ b) when y is given (written back), xn = x * scale
+// * w with scale = 1 / sqrt(sum x^2 / n + eps), the sum in double over a
+// tree of kNormQTh partial sums -- the steps and order of the layer span's
+// rmsnorm kernel, each operation rounded on its own (no contraction) -- and
+// xn, written out, is read back in 256-value chunks (wavefront w takes chunks
+// w, w + 16, ...) and quantized as quantize_kernel does. Rows from n_tok up to
+// the next 32-token block (GEMM planes) only zero-fill.
+constexpr int kNormQTh = 1024;
+template <bool GEMM_ONLY>
+__global__ __launch_bounds__(kNormQTh) void rmsnorm_quantize_kernel(float* __restrict__ x, const float* __restrict__ y,
+                                                                    const float* __restrict__ b,
+                                                                    const float* __restrict__ w, float* xn, int n_tok,
+                                                                    int n, float eps, QuantOut o) {
+    __shared__ double red[kNormQTh];
+    const int t = int(blockIdx.x), tid = int(threadIdx.x), lane = tid & 63, wv = tid >> 6;
+    if (t < n_tok) {
+        float* xr = x + size_t(t) * n;
+        const float* yr = y ? y + size_t(t) * n : nullptr;
+        float* orow = xn + size_t(t) * n;
+        double sq = 0.0;
+#pragma unroll 4
+        for (int i = tid; i < n; i += kNormQTh) {
+            float v = xr[i];
+            if (yr) {
+                v = __fadd_rn(v, b ? __fadd_rn(yr[i], b[i]) : yr[i]);
+                xr[i] = v;
+            } else if (b) {
+                v = __fadd_rn(v, b[i]);
+                xr[i] = v;
+            }
+            sq = __dadd_rn(sq, __dmul_rn(double(v), double(v)));
+        }
+        red[tid] = sq;
+        __syncthreads();
+        for (int st = kNormQTh / 2; st > 0; st >>= 1) {
+            if (tid < st) red[tid] = __dadd_rn(red[tid], red[tid + st]);
+            __syncthreads();
+        }
+        const float scale = 1.0f / sqrtf(__fadd_rn(float(red[0] / n), eps));
+        for (int i = tid; i < n; i += kNormQTh) orow[i] = __fmul_rn(__fmul_rn(xr[i], scale), w[i]);
+        __syncthreads();  // the row is written before its chunks are read back
+    }
+    const int chunks = (n + 255) / 256;
+    const float* orow = xn + size_t(min(t, n_tok - 1)) * n;
+    for (int c = wv; c < chunks; c += kNormQTh / 64) {
+        const int k0 = c * 256 + lane * 4;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (t < n_tok && k0 < n) v = *reinterpret_cast<const float4*>(orow + k0);
+        quantize_chunk<GEMM_ONLY>(v, t, c, n_tok, n, o, lane);
+    }
+}
+
+}  // namespace
+
+hipError_t launch_quantize(const float* x, int n_tok, int n_in, int ldx, void* act, void* aos32, void* aos256,
+                           hipStream_t stream, unsigned planes, const float* u, float* h_out, bool gelu) {
+    const ActLayout L = act_layout(n_tok, n_in);
+    if (!L.total) return hipErrorInvalidValue;
+    const QuantOut o = quant_out(L, act, aos32, aos256, planes);
+    const bool gemm = o.gA != nullptr;
     const long rows = gemm ? L.n_tb * 32 : n_tok, chunks = (n_in + 255) / 256;
     // the GEMM's planes alone (a K-quant prefill): the kernel without the other layouts' code
-    const bool gemm_only = gemm && !gemv && !b32 && !b256 && !o.aos32 && !o.aos256;
+    const bool gemm_only = gemm_planes_only(o);
     // four chunks per wavefront only for the largest launches (measured: 6 % faster at 512 x 14336;
     // at 64 x 4096 or 512 x 4096 one chunk per wavefront is faster, the chain per chunk dominating)
     if (rows * chunks >= 16384) {
@@ -221,6 +289,21 @@ hipError_t launch_quantize(const float* x, int n_tok, int n_in, int ldx, void* a
             hipLaunchKernelGGL((quantize_kernel<1, false>), dim3(blocks), dim3(256), 0, stream, x, n_tok, n_in, ldx,
                                o, u, h_out, gelu ? 1 : 0);
     }
+    return hipGetLastError();
+}
+
+hipError_t launch_rmsnorm_quantize(float* x, const float* y, const float* b, const float* w, float* xn, int n_tok,
+                                   int n, float eps, void* act, unsigned planes, hipStream_t stream) {
+    const ActLayout L = act_layout(n_tok, n);
+    if (!L.total || n % 4) return hipErrorInvalidValue;
+    const QuantOut o = quant_out(L, act, nullptr, nullptr, planes);
+    const unsigned rows = unsigned(o.gA ? L.n_tb * 32 : n_tok);
+    if (gemm_planes_only(o))
+        hipLaunchKernelGGL(rmsnorm_quantize_kernel<true>, dim3(rows), dim3(kNormQTh), 0, stream, x, y, b, w, xn, n_tok,
+                           n, eps, o);
+    else
+        hipLaunchKernelGGL(rmsnorm_quantize_kernel<false>, dim3(rows), dim3(kNormQTh), 0, stream, x, y, b, w, xn, n_tok,
+                           n, eps, o);
     return hipGetLastError();
 }
 
