@@ -209,7 +209,7 @@ hipError_t launch_gemm_group(int n, const void* const* ws, const WeightLayout* W
 // instead of pos0 (a graph replayed for every decode position; the caller
 // keeps pos_dev[0] + n_tok <= the cache and ld). rmsnorm with y != nullptr
 // first adds y (+ b when given) into x (written back). Attention of more than
-// kAttnSplitTok tokens with head dims 64 or 128 (and no pos_dev, f16 cache)
+// kAttnSplitTok tokens with head dims 64, 128 or 256 (and no pos_dev, f16 cache)
 // runs on MFMA tiles of 32 tokens x 32 positions, f16 products at f32 accuracy
 // (q and p split into two f16 parts).
 struct SpanVecs {

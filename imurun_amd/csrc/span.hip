@@ -673,7 +673,7 @@ __global__ __launch_bounds__(kTh) void attn_full_kernel(const float* __restrict_
     if (tid < D) out[size_t(t) * Q + size_t(h) * D + tid] = o_run * (1.0f / l_run);
 }
 
-// Attention of more tokens on MFMA, for head dims D of 64 or 128. One
+// Attention of more tokens on MFMA, for head dims D of 64, 128 or 256. One
 // workgroup (four wavefronts) per (block of 32
 // tokens, head); wavefront w takes the key blocks of 32 positions
 // b = b_lo + w, b_lo + w + 4, ... that the block's tokens can see, keeps a
@@ -781,9 +781,12 @@ __global__ __launch_bounds__(256) void attn_mfma16_kernel(const float* __restric
             nv[pc] = *reinterpret_cast<const uint4*>(vc + at);
         }
     };
-    if (kb_lo + w <= kb_hi) load_block(kb_lo + w);
+    // (head dim 256: no registers to spare, each block loaded when it is staged)
+    constexpr bool PF = D <= 128;
+    if (PF && kb_lo + w <= kb_hi) load_block(kb_lo + w);
     for (int kb = kb_lo + w; kb <= kb_hi; kb += 4) {  // uniform over the wavefront
         const int j0 = kb * 32;
+        if (!PF) load_block(kb);
         // stage the block (rows past the block's last position as zeros)
 #pragma unroll
         for (int pc = 0; pc < PCS; ++pc) {
@@ -792,7 +795,7 @@ __global__ __launch_bounds__(256) void attn_mfma16_kernel(const float* __restric
             *reinterpret_cast<uint4*>(sk + r * KROW + c8 * 8) = live ? nk[pc] : make_uint4(0, 0, 0, 0);
             *reinterpret_cast<uint4*>(sv + r * KROW + c8 * 8) = live ? nv[pc] : make_uint4(0, 0, 0, 0);
         }
-        if (kb + 4 <= kb_hi) load_block(kb + 4);
+        if (PF && kb + 4 <= kb_hi) load_block(kb + 4);
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -1001,11 +1004,14 @@ hipError_t launch_attention(const float* q, const KvCache& kc, const KvCache& vc
     if (n_tok <= 0 || D <= 0 || D > kTh || D % 2 || HKV <= 0 || H % HKV || ld < pos0 + n_tok || !kv_ok(kc, D) ||
         !kv_ok(vc, D) || !kc.d != !vc.d)
         return hipErrorInvalidValue;
-    if (n_tok > kAttnSplitTok && !pos_dev && (D == 64 || D == 128) && !kc.d) {
+    if (n_tok > kAttnSplitTok && !pos_dev && (D == 64 || D == 128 || D == 256) && !kc.d) {
         const dim3 grid(unsigned((n_tok + kAttnMfmaTok - 1) / kAttnMfmaTok * H)), block(kTh);
         const _Float16* k16 = static_cast<const _Float16*>(kc.c);
         const _Float16* v16 = static_cast<const _Float16*>(vc.c);
-        if (D == 64)
+        if (D == 256)
+            hipLaunchKernelGGL(attn_mfma16_kernel<256>, grid, block, 0, s, q, k16, v16, out, n_tok, ld, H, HKV, pos0,
+                               scale, softcap, window);
+        else if (D == 64)
             hipLaunchKernelGGL(attn_mfma16_kernel<64>, grid, block, 0, s, q, k16, v16, out, n_tok, ld, H, HKV, pos0,
                                scale, softcap, window);
         else

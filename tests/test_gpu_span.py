@@ -386,6 +386,33 @@ def test_span_decode_at_model_width(oracle, monkeypatch, e_dim, variant):
             be.release(n)
 
 
+@pytest.mark.parametrize("variant", ["llama", "gemma2"])
+def test_span_head_dim_256(oracle, monkeypatch, variant):
+    """Head dim 256 (Gemma-2's): the prefill attention on f16 MFMA tiles of 256 values (no
+    row prefetch), then one-token calls through the position chunks; every stage is checked
+    as above, Gemma-2's soft cap and window included."""
+    import sys
+    mod = sys.modules[__name__]
+    h, hkv, d = 2, 1, 256
+    for name, val in (("H", h), ("HKV", hkv), ("D", d), ("Q", h * d), ("KV", hkv * d)):
+        monkeypatch.setattr(mod, name, val)
+    monkeypatch.setattr(mod, "SHAPES", dict(wq=(h * d, E), wk=(hkv * d, E), wv=(hkv * d, E), wo=(E, h * d),
+                                            wg=(F, E), wu=(F, E), wd=(E, F)))
+    be = fh.HipBackend()
+    assert be.available()
+    names, ref, _ = setup_span(oracle, be, d, variant, f"d256{variant}")
+    try:
+        pos0 = 0
+        for i, n in enumerate((37, 100, 1, 1)):
+            x = normal(720 + i, (n, E), 1.0)
+            check_call(be, ref, x, pos0, f"{variant} D=256")
+            pos0 += n
+    finally:
+        be.span_release()
+        for n in names:
+            be.release(n)
+
+
 def test_span_kv_rewind_then_new_tokens(oracle):
     """span_kv_truncate(n) then new tokens from position n (prefix reuse, backend.h:158): the
     rewritten positions replace the old ones for every later call; rows past n are never
